@@ -1,0 +1,73 @@
+/* Thin C-ABI shim between the C host code (kernels_hip.c) and HIP.
+ *
+ * Everything here takes plain pointers and sizes.  Device pointers are
+ * marked _d.  Launchers are asynchronous on the shim's single stream and
+ * return 0 or a QH_E* error code; nothing here aborts.
+ */
+#ifndef QWEN3_HIP_SHIM_H
+#define QWEN3_HIP_SHIM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    QH_OK = 0,
+    QH_EINVAL = 1,      /* bad argument (sizes, pointers, alignment) */
+    QH_ENODEV = 2,      /* no HIP device / init failed */
+    QH_ENOMEM = 3,      /* device or pinned allocation failed */
+    QH_ELAUNCH = 4,     /* kernel launch failed */
+    QH_ERUNTIME = 5,    /* any other HIP runtime error (copy, sync, event) */
+    QH_ELAYOUT = 6,     /* weight layout not usable for this shape */
+    QH_ESTATE = 7,      /* call order (e.g. use before init) */
+    QH_ETOOBIG = 8      /* size beyond a documented maximum */
+};
+
+int         qh_init(int device);        /* idempotent; creates the stream */
+void        qh_shutdown(void);
+int         qh_device(void);
+const char *qh_device_name(void);
+int         qh_device_count(void);      /* initialises HIP */
+int         qh_last_hip_error(void);    /* raw hipError_t of the last failure */
+const char *qh_last_hip_error_string(void);
+
+int qh_malloc(void **p_d, size_t bytes);
+int qh_free(void *p_d);
+int qh_host_alloc(void **p, size_t bytes);     /* pinned host memory */
+int qh_host_free(void *p);
+int qh_h2d(void *dst_d, const void *src, size_t bytes);   /* async on the stream */
+int qh_d2h(void *dst, const void *src_d, size_t bytes);   /* async on the stream */
+int qh_d2d(void *dst_d, const void *src_d, size_t bytes); /* async on the stream */
+int qh_sync(void);
+void *qh_stream(void);                                    /* hipStream_t */
+
+/* C[M,N] = A[M,K] . B[N,K]^T;  A fp32, B bf16 bits, C fp32; row-major,
+ * lda = ldb = K, ldc = N.  A is rounded to bf16 (RNE) on the load path. */
+int qh_gemm(float *c_d, const float *a_d, const uint16_t *b_d,
+            int M, int K, int N);
+/* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */
+int qh_gemm_gate_up_silu(float *h_d, const float *x_d, const uint16_t *wg_d,
+                         const uint16_t *wu_d, int M, int K, int N);
+/* tile-major [N/tn][K/tk][tn][tk] -> row-major [N][K] */
+int qh_tile_to_row(uint16_t *dst_d, const uint16_t *src_d, int N, int K,
+                   int tile_n, int tile_k);
+/* first index of the maximum of v[0..n) (ties -> lowest index) */
+int qh_argmax(int *out_d, const float *v_d, int n);
+
+/* kernel choice for a GEMM shape (for logs/tests): returns a static name */
+const char *qh_gemm_plan(int M, int K, int N, int gated);
+/* override the automatic choice: 0 = auto, otherwise a plan id (see
+ * qh_gemm_plan names); for tests and sweeps */
+int qh_force_plan(int plan_id);
+
+/* HIP events on the shim stream, for timing what this stream runs */
+int   qh_timer_record(int slot);            /* slot in [0, 64) */
+int   qh_timer_elapsed_ms(int a, int b, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN3_HIP_SHIM_H */

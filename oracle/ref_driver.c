@@ -1,0 +1,70 @@
+/* Greedy-generation driver around the reference forward — TEST INFRASTRUCTURE.
+ *
+ * Compiled only together with the reference's own qwen3.c + a kernels_*.c +
+ * ops_scalar.c into oracle/_ref/ (see the "ref" target of the Makefile here),
+ * so that tests can run the reference model on a random-init QW3M blob.
+ * The loop follows fpga_bringup/src/src/main.c:227-256: one batched prefill
+ * of the prompt (chunked by QWEN3_MAX_BATCH), argmax of the last logits,
+ * then one qwen3_forward per generated token.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "qwen3.h"
+
+size_t refdrv_scratch_bytes(void) { return qwen3_scratch_bytes(); }
+int refdrv_max_seq(void) { return QWEN3_MAX_SEQ; }
+int refdrv_max_batch(void) { return QWEN3_MAX_BATCH; }
+
+/* logit gap between the best and the runner-up, for divergence reports */
+static float top2_margin(const float *v, int n) {
+    float b1 = v[0], b2 = -3.0e38f;
+    for (int i = 1; i < n; i++) {
+        if (v[i] > b1) { b2 = b1; b1 = v[i]; }
+        else if (v[i] > b2) b2 = v[i];
+    }
+    return b1 - b2;
+}
+
+/* Returns the number of tokens written to out (<= n_decode + 1), or a
+ * negative QWEN3_ERR_* code.  out[0] comes from the prefill logits; each
+ * decode step i feeds out[i] at position n_prompt + i and yields out[i+1].
+ * If logits_out is non-NULL, the last logits row after the prefill is copied
+ * there (VOCAB floats). */
+int refdrv_generate(const void *blob, size_t blob_size,
+                    const int *prompt, int n_prompt, int n_decode,
+                    int stop_at_eos, int *out, float *margins,
+                    float *logits_out) {
+    static qwen3_t m;
+    void *scratch = malloc(qwen3_scratch_bytes());
+    if (!scratch) return QWEN3_ERR_OOM;
+    int rc = qwen3_init(&m, blob, blob_size, scratch, qwen3_scratch_bytes());
+    if (rc != QWEN3_OK) { free(scratch); return rc; }
+    if (n_prompt < 1 || n_prompt + n_decode > QWEN3_MAX_SEQ) {
+        free(scratch);
+        return QWEN3_ERR_SHAPE;
+    }
+
+    for (int p0 = 0; p0 < n_prompt; p0 += QWEN3_MAX_BATCH) {
+        int nt = n_prompt - p0 < QWEN3_MAX_BATCH ? n_prompt - p0 : QWEN3_MAX_BATCH;
+        qwen3_forward_batch(&m, prompt + p0, nt, p0);
+    }
+    if (logits_out)
+        memcpy(logits_out, qwen3_last_logits(&m), sizeof(float) * QWEN3_VOCAB_SIZE);
+
+    int n_out = 0;
+    int next = qwen3_argmax(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+    if (margins) margins[n_out] = top2_margin(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+    out[n_out++] = next;
+    for (int step = 0; step < n_decode; step++) {
+        if (stop_at_eos &&
+            (next == QWEN3_EOS_TOKEN_ID_0 || next == QWEN3_EOS_TOKEN_ID_1))
+            break;
+        qwen3_forward(&m, next, n_prompt + step);
+        next = qwen3_argmax(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+        if (margins) margins[n_out] = top2_margin(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+        out[n_out++] = next;
+    }
+    free(scratch);
+    return n_out;
+}

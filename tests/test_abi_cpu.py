@@ -1,0 +1,140 @@
+"""The C-ABI library on a machine without a GPU: it builds, loads, exports
+every symbol include/qwen3_hip.h declares, and its host-only logic (layout
+negotiation, argument checks, error reporting) behaves like the reference
+plug-in.  No call here reaches a GPU kernel."""
+import ctypes
+import os
+import subprocess
+import sys
+import textwrap
+
+import numpy as np
+import pytest
+
+from n550_qwen3_bringup_handover_amd import abi, runtime
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_header_symbol():
+    L = runtime.lib()
+    names = runtime.header_symbols()
+    # the four reference plug-in symbols (fpga_bringup/src/src/kernels.h:56-92)
+    for ref in ("qwen3_gemm", "qwen3_gemm_row", "qwen3_set_weight_layout", "qwen3_kernel_name"):
+        assert ref in names
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # and every declared function has a ctypes prototype in runtime.py
+    assert set(names) <= set(runtime._PROTOS), set(names) - set(runtime._PROTOS)
+
+
+def test_library_links_only_the_hip_runtime():
+    out = subprocess.run(["ldd", runtime.LIB_PATH], capture_output=True, text=True).stdout
+    assert "libamdhip64" in out
+    for bad in ("libtorch", "libcuda", "liboracle", "libref_"):
+        assert bad not in out
+
+
+def test_kernel_name():
+    assert abi.kernel_name() == "hip-gfx950"
+
+
+@pytest.mark.parametrize("layout,tn,tk,ok", [
+    (0, 0, 0, True), (0, 128, 32, True),          # ROW ignores tile sizes (qwen3.c:67-73)
+    (1, 128, 32, True),                           # the AME tile (kernels.h:20-23)
+    (1, 64, 16, True), (1, 1024, 1024, True),     # any tile dividing all model dims
+    (1, 100, 32, False), (1, 128, 33, False),     # 2048 % 100, 1024 % 33
+    (1, 0, 32, False), (1, 128, -32, False),
+    (2, 128, 32, False), (-1, 0, 0, False),       # unknown layout codes
+])
+def test_set_weight_layout(layout, tn, tk, ok):
+    L = runtime.lib()
+    try:
+        assert (L.qwen3_set_weight_layout(layout, tn, tk) == 0) == ok
+    finally:
+        L.qwen3_set_weight_layout(0, 0, 0)
+
+
+def test_strerror_table():
+    L = runtime.lib()
+    for code in range(9):
+        assert L.qwen3_hip_strerror(code)
+    assert L.qwen3_hip_strerror(99) == b"unknown error"
+
+
+def test_invalid_arguments_are_reported_not_computed():
+    """M < 0 is rejected before any device work; C is left untouched."""
+    L = runtime.lib()
+    L.qwen3_hip_set_abort(0)
+    L.qwen3_hip_last_error()
+    c = np.full(4, 7.0, np.float32)
+    a = np.zeros(4, np.float32)
+    b = np.zeros(4, np.uint16)
+    L.qwen3_gemm(c.ctypes.data_as(runtime.F32P), a.ctypes.data_as(runtime.F32P),
+                 b.ctypes.data_as(runtime.U16P), -1, 2, 2)
+    assert L.qwen3_hip_last_error() == 1       # QWEN3_HIP_EINVAL
+    assert np.all(c == 7.0)
+    assert L.qwen3_hip_last_error() == 0       # cleared on read
+
+
+def test_empty_shapes_are_no_ops_without_a_device():
+    L = runtime.lib()
+    L.qwen3_hip_set_abort(0)
+    L.qwen3_hip_last_error()
+    c = np.full(4, 7.0, np.float32)
+    L.qwen3_gemm(c.ctypes.data_as(runtime.F32P), None, None, 0, 16, 4)
+    L.qwen3_gemm(c.ctypes.data_as(runtime.F32P), None, None, 4, 16, 0)
+    assert L.qwen3_hip_last_error() == 0
+    assert np.all(c == 7.0)
+
+
+def test_python_mirror_rejects_wrong_dtypes():
+    with pytest.raises(TypeError):
+        abi.gemm(np.zeros(4, np.float64), np.zeros(4, np.float32), np.zeros(4, np.uint16), 2, 2, 2)
+    with pytest.raises(ValueError):
+        abi.gemm(np.zeros(3, np.float32), np.zeros(4, np.float32), np.zeros(4, np.uint16), 2, 2, 2)
+
+
+@pytest.mark.skipif(runtime.gpu_visible(), reason="checks the no-device path")
+def test_no_device_is_a_clear_error():
+    L = runtime.lib()
+    L.qwen3_hip_set_abort(0)
+    L.qwen3_hip_last_error()
+    assert L.qwen3_hip_init(-1) == 2            # QWEN3_HIP_ENODEV
+    with pytest.raises(runtime.Qwen3HipError):
+        runtime.init()
+
+
+def test_void_entry_points_abort_by_default():
+    """The reference ABI cannot return an error, so by default a failure
+    prints one line and aborts (checked in a child process)."""
+    code = textwrap.dedent(f"""
+        import ctypes, sys
+        L = ctypes.CDLL({runtime.LIB_PATH!r})
+        c = (ctypes.c_float * 4)()
+        L.qwen3_gemm(c, c, None, -1, 2, 2)
+        print("not reached")
+    """)
+    env = dict(os.environ)
+    env.pop("QWEN3_HIP_ABORT", None)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env)
+    assert r.returncode != 0
+    assert "not reached" not in r.stdout
+    assert "qwen3_gemm: invalid argument" in r.stderr
+    env["QWEN3_HIP_ABORT"] = "0"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env)
+    assert r.returncode == 0 and "not reached" in r.stdout
+
+
+def test_header_compiles_as_c_and_cpp(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "qwen3_hip.h"\nint main(void){return qwen3_kernel_name()[0]==\'h\'?0:1;}\n')
+    inc = os.path.join(ROOT, "include")
+    for cc, std in (("gcc", "-std=c11"), ("g++", "-std=c++17")):
+        exe = tmp_path / f"t_{cc}"
+        r = subprocess.run([cc, std, "-Wall", "-Werror", "-x", "c" if cc == "gcc" else "c++",
+                            str(src), "-I", inc, "-x", "none", runtime.LIB_PATH, "-o", str(exe),
+                            f"-Wl,-rpath,{os.path.dirname(runtime.LIB_PATH)}"],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+        assert subprocess.run([str(exe)]).returncode == 0
