@@ -1,0 +1,449 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen3-0.6B GEMM/GEMV hot path on one MI355X.
+
+Workload (one "step" = one decode token's projections at M = 1):
+    28 layers x [ fused q|k|v GEMV 1024 -> 4096,  o GEMV 2048 -> 1024,
+                  fused gate|up GEMV 1024 -> 2x3072 with SiLU*mul epilogue,
+                  down GEMV 3072 -> 1024 ]
+    + tied lm_head GEMV 1024 -> 151936
+with distinct random-init bf16 weights per layer (N(0, 0.02); 1.19 GB, more
+than the 256 MB last-level cache) and activations already resident in HBM.
+Algorithmic bytes per step = 1,195,103,744 (bf16 weights + fp32 inputs +
+fp32 outputs of the 197 reference GEMV calls).  value = steps per second =
+decode tokens/s of the GEMV set.
+
+Also reported: per-kernel launch times (HIP events on the library stream),
+the roofline fraction of the dominant kernel, prefill GEMM TFLOP/s at
+M = 512 (fused gate/up included), and a CPU baseline: the reference's
+portable scalar GEMM (fpga_bringup/src/src/kernels_scalar.c, compiled from
+its source into oracle/_ref) running the same step on 1 host core.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "bf16 GEMM TFLOP/s (% MFMA peak); Qwen3-0.6B decode tok/s, 1 GPU"
+HBM_PEAK_GBS = 8000.0               # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2516.6      # 256 CU x 2.4 GHz x 4096 dense bf16 flop/clk
+
+H, Q, KV, I, V, LAYERS = 1024, 2048, 1024, 3072, 151936, 28
+
+
+def gemv_bytes(K, N, nb=1):
+    """algorithmic bytes of an M=1 GEMV: bf16 weights + fp32 in + fp32 out"""
+    return 2 * N * K * nb + 4 * K + 4 * N
+
+
+# the 197 reference GEMV calls of one decode token (cfg 2)
+STEP_BYTES = LAYERS * (gemv_bytes(H, Q) + 2 * gemv_bytes(H, KV) + gemv_bytes(Q, H)
+                       + 2 * gemv_bytes(H, I) + gemv_bytes(I, H)) + gemv_bytes(H, V)
+assert STEP_BYTES == 1195103744
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (child process, pinned to one core, no GPU)
+# ---------------------------------------------------------------------------
+def cpu_baseline_child(budget_s):
+    import numpy as np
+    import oracle
+    os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    L = oracle.ref("ref_scalar")
+    kind = "reference"
+    if L is None:
+        L = oracle.lib()
+        kind = "port"
+        fn = L.orc_gemm_scalar
+    else:
+        fn = L.qwen3_gemm
+    F32P, U16P = oracle.F32P, oracle.U16P
+    rng = np.random.default_rng(1)
+    # content does not change scalar timing; addresses do (distinct per layer)
+    pat = oracle.f32_to_bf16((rng.standard_normal(1 << 22) * 0.02).astype(np.float32))
+
+    def weights(n):
+        reps = -(-n // pat.size)
+        return np.tile(pat, reps)[:n].copy()
+
+    layers = []
+    for _ in range(LAYERS):
+        layers.append({"qkv": weights((Q + 2 * KV) * H), "o": weights(H * Q),
+                       "g": weights(I * H), "u": weights(I * H), "d": weights(H * I)})
+    emb = weights(V * H)
+    x = oracle.f32_bf16_normal(I, 5)
+    out = np.empty(V, np.float32)
+    xp, op = x.ctypes.data_as(F32P), out.ctypes.data_as(F32P)
+
+    def step():
+        for w in layers:
+            # the reference forward calls q, k, v, o, gate, up, down separately
+            q = w["qkv"]
+            fn(op, xp, q.ctypes.data_as(U16P), 1, H, Q)
+            fn(op, xp, q[Q * H:].ctypes.data_as(U16P), 1, H, KV)
+            fn(op, xp, q[(Q + KV) * H:].ctypes.data_as(U16P), 1, H, KV)
+            fn(op, xp, w["o"].ctypes.data_as(U16P), 1, Q, H)
+            fn(op, xp, w["g"].ctypes.data_as(U16P), 1, H, I)
+            fn(op, xp, w["u"].ctypes.data_as(U16P), 1, H, I)
+            fn(op, xp, w["d"].ctypes.data_as(U16P), 1, I, H)
+        fn(op, xp, emb.ctypes.data_as(U16P), 1, H, V)
+
+    step()                                  # warm caches / page in
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    print(json.dumps({"value": n / el, "unit": "tok/s", "cores": 1, "kind": kind,
+                      "sample": f"{n} full decode steps (197 GEMV calls each, distinct weights "
+                                f"per layer) in {el:.1f} s on 1 core of {cpu} "
+                                f"(nproc={os.cpu_count()}); "
+                                + ("reference kernels_scalar.c compiled from source"
+                                   if kind == "reference" else "oracle restatement")}))
+
+
+def run_cpu_baseline(budget_s):
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-baseline-child",
+                        str(budget_s)], capture_output=True, text=True)
+    if r.returncode != 0:
+        return {"value": None, "error": r.stderr.strip()[-400:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+# ---------------------------------------------------------------------------
+# GPU side
+# ---------------------------------------------------------------------------
+class Gpu:
+    def __init__(self):
+        from n550_qwen3_bringup_handover_amd import runtime
+        self.rt = runtime
+        self.L = runtime.init()
+        self.VP = ctypes.c_void_p
+        self.bufs = []
+
+    def alloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.rt.check(self.L.qwen3_hip_malloc(ctypes.byref(p), int(nbytes)), "malloc")
+        self.bufs.append(p.value)
+        return p.value
+
+    def fill_bf16(self, ptr, n, seed):
+        """fill n bf16 weights with a 32 MB random N(0,0.02) block, repeated"""
+        import numpy as np
+        rng = np.random.default_rng(seed)
+        blk = min(n, 1 << 24)
+        pat = ((rng.standard_normal(blk, dtype=np.float32) * np.float32(0.02)).view(np.uint32)
+               + np.uint32(0x8000)) >> np.uint32(16)
+        pat = pat.astype(np.uint16)
+        done = 0
+        while done < n:
+            m = min(blk, n - done)
+            self.rt.check(self.L.qwen3_hip_memcpy_h2d(self.VP(ptr + 2 * done),
+                                                      self.VP(pat.ctypes.data), 2 * m), "h2d")
+            done += m
+        self.rt.check(self.L.qwen3_hip_sync(), "sync")
+
+    def fill_f32(self, ptr, n, seed):
+        import numpy as np
+        rng = np.random.default_rng(seed)
+        x = rng.standard_normal(n, dtype=np.float32)
+        x = ((x.view(np.uint32) + np.uint32(0x8000)) & np.uint32(0xFFFF0000)).view(np.float32)
+        self.rt.check(self.L.qwen3_hip_memcpy_h2d(self.VP(ptr), self.VP(x.ctypes.data), x.nbytes), "h2d")
+        self.rt.check(self.L.qwen3_hip_sync(), "sync")
+
+    def gemm(self, c, a, b, M, K, N):
+        rc = self.L.qwen3_hip_gemm_dev(self.VP(c), self.VP(a), self.VP(b), M, K, N)
+        if rc:
+            self.rt.check(rc, "qwen3_hip_gemm_dev")
+
+    def gated(self, h, x, wg, wu, M, K, N):
+        rc = self.L.qwen3_hip_gemm_gate_up_silu_dev(self.VP(h), self.VP(x), self.VP(wg), self.VP(wu), M, K, N)
+        if rc:
+            self.rt.check(rc, "qwen3_hip_gemm_gate_up_silu_dev")
+
+    def record(self, slot):
+        self.rt.check(self.L.qwen3_hip_timer_record(slot), "timer")
+
+    def elapsed(self, a, b):
+        ms = ctypes.c_float()
+        self.rt.check(self.L.qwen3_hip_timer_elapsed_ms(a, b, ctypes.byref(ms)), "timer")
+        return ms.value
+
+    def sync(self):
+        self.rt.check(self.L.qwen3_hip_sync(), "sync")
+
+    def plan(self, M, K, N, gated=False):
+        return self.L.qwen3_hip_plan(M, K, N, int(gated)).decode()
+
+
+def build_decode_model(g):
+    """device weights in the QW3M tensor order: q|k|v and gate|up contiguous"""
+    layers = []
+    per_layer = (Q + 2 * KV) * H + H * Q + 2 * I * H + H * I
+    base = g.alloc(2 * per_layer * LAYERS)
+    g.fill_bf16(base, per_layer * LAYERS, 11)
+    off = base
+    for _ in range(LAYERS):
+        w = {"qkv": off}
+        off += 2 * (Q + 2 * KV) * H
+        w["o"] = off
+        off += 2 * H * Q
+        w["g"] = off
+        w["u"] = off + 2 * I * H
+        off += 4 * I * H
+        w["d"] = off
+        off += 2 * H * I
+        layers.append(w)
+    emb = g.alloc(2 * V * H)
+    g.fill_bf16(emb, V * H, 12)
+    act = {}
+    for name, n in (("x", H), ("attn", Q), ("h", I), ("qkv", Q + 2 * KV), ("o", H), ("d", H),
+                    ("logits", V)):
+        act[name] = g.alloc(4 * n)
+        g.fill_f32(act[name], n, 13 + len(name))
+    return layers, emb, act
+
+
+def decode_step(g, layers, emb, act):
+    """Each GEMV consumes the previous one's output, so launches form the same
+    dependency chain as the model forward (attention and norms, which sit
+    between them in the model, are outside this hot path): x -> q|k|v; the q
+    part stands in for the attention output -> o -> gate|up -> down -> x of
+    the next layer; the last x -> lm_head."""
+    for w in layers:
+        g.gemm(act["qkv"], act["x"], w["qkv"], 1, H, Q + 2 * KV)
+        g.gemm(act["o"], act["qkv"], w["o"], 1, Q, H)
+        g.gated(act["h"], act["o"], w["g"], w["u"], 1, H, I)
+        g.gemm(act["x"], act["h"], w["d"], 1, I, H)
+    g.gemm(act["logits"], act["x"], emb, 1, H, V)
+
+
+def time_launches(g, launch, reps):
+    """average duration of one launch: HIP events around each launch on the
+    library stream (pairs of slots), after a warm-up launch"""
+    launch(0)
+    g.sync()
+    tot = 0.0
+    n = 0
+    for r in range(reps):
+        s = 2 * (r % 16)
+        g.record(s)
+        launch(r)
+        g.record(s + 1)
+        if s == 30 or r == reps - 1:
+            for k in range(0, s + 2, 2):
+                tot += g.elapsed(k, k + 1)
+                n += 1
+    return tot / n
+
+
+def time_launches_graph(g, launch, reps):
+    """average time per launch of `reps` back-to-back launches replayed from
+    one captured graph (events around the replay, on the library stream)"""
+    g.rt.check(g.L.qwen3_hip_capture_begin(), "capture_begin")
+    for r in range(reps):
+        launch(r)
+    gid = ctypes.c_int(-1)
+    g.rt.check(g.L.qwen3_hip_capture_end(ctypes.byref(gid)), "capture_end")
+    try:
+        g.rt.check(g.L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+        g.sync()
+        best = None
+        for _ in range(3):
+            g.record(56)
+            g.rt.check(g.L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+            g.record(57)
+            ms = g.elapsed(56, 57) / reps
+            best = ms if best is None else min(best, ms)
+        return best
+    finally:
+        g.rt.check(g.L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
+
+
+def kernel_classes(g, layers, emb, act):
+    """per-launch timing of each kernel class of the decode step"""
+    cls = {
+        "qkv_gemv": (LAYERS, gemv_bytes(H, Q + 2 * KV),
+                     lambda r: g.gemm(act["qkv"], act["x"], layers[r % LAYERS]["qkv"], 1, H, Q + 2 * KV)),
+        "o_gemv": (LAYERS, gemv_bytes(Q, H),
+                   lambda r: g.gemm(act["o"], act["attn"], layers[r % LAYERS]["o"], 1, Q, H)),
+        "gate_up_silu_gemv": (LAYERS, 2 * I * H * 2 + 4 * H + 4 * I,
+                              lambda r: g.gated(act["h"], act["x"], layers[r % LAYERS]["g"],
+                                                layers[r % LAYERS]["u"], 1, H, I)),
+        "down_gemv": (LAYERS, gemv_bytes(I, H),
+                      lambda r: g.gemm(act["d"], act["h"], layers[r % LAYERS]["d"], 1, I, H)),
+        "lm_head_gemv": (1, gemv_bytes(H, V),
+                         lambda r: g.gemm(act["logits"], act["x"], emb, 1, H, V)),
+    }
+    out = {}
+    for name, (count, nbytes, fn) in cls.items():
+        ms_ev = time_launches(g, fn, 64 if count > 1 else 32)
+        ms = time_launches_graph(g, fn, 4 * LAYERS if count > 1 else 16)
+        out[name] = {"count_per_step": count, "bytes_per_launch": nbytes,
+                     "us_per_launch": round(ms * 1e3, 3),
+                     "us_per_launch_event_pairs": round(ms_ev * 1e3, 3),
+                     "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "us_per_step": round(ms * 1e3 * count, 2)}
+    return out
+
+
+def prefill_gemms(g):
+    """M = 512 projections (warm: operands resident in L2/MALL)"""
+    M = 512
+    res = {}
+    a = g.alloc(4 * M * I)
+    g.fill_f32(a, M * I, 21)
+    c = g.alloc(4 * M * 2 * I)
+    wmax = g.alloc(2 * 2 * I * H)
+    g.fill_bf16(wmax, 2 * I * H, 22)
+    for name, K, N, gated in (("q", H, Q, False), ("k", H, KV, False), ("o", Q, H, False),
+                              ("gate_up_silu", H, I, True), ("down", I, H, False)):
+        if gated:
+            fn = lambda r, K=K, N=N: g.gated(c, a, wmax, wmax + 2 * I * H, M, K, N)
+            flops = 2.0 * M * 2 * N * K
+            byts = 2 * 2 * N * K + 4 * M * K + 4 * M * N
+        else:
+            fn = lambda r, K=K, N=N: g.gemm(c, a, wmax, M, K, N)
+            flops = 2.0 * M * N * K
+            byts = 2 * N * K + 4 * M * K + 4 * M * N
+        ms = time_launches(g, fn, 32)
+        tf = flops / (ms * 1e-3) / 1e12
+        res[name] = {"M": M, "K": K, "N": N, "kernel": g.plan(M, K, N, gated),
+                     "us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                     "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "cold_hbm_cap": round(min(1.0, flops / byts / (MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9))), 3)}
+    return res
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any"""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    vals = {}
+    for line in open(path):
+        if ":" in line and not line.startswith("#"):
+            k, v = line.split(":", 1)
+            try:
+                vals[k.strip()] = float(v.split()[0])
+            except (ValueError, IndexError):
+                pass
+    return vals.get("traffic_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip per-kernel and prefill tables")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch the 113 kernels of a step one by one instead of replaying a graph")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 64 MiB copy kernel (traffic-counter calibration)")
+    ap.add_argument("--cpu-baseline-child", type=float, default=None, help=argparse.SUPPRESS)
+    args = ap.parse_args()
+
+    if args.cpu_baseline_child is not None:
+        cpu_baseline_child(args.cpu_baseline_child)
+        return 0
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the hot path is a "
+                                   "single-GPU GEMM/GEMV library; see DESIGN.md for how it "
+                                   "would shard", "n_gpus": args.gpus}))
+        return 2
+
+    # CPU baseline first, before this process touches the GPU
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.cpu_budget)
+
+    g = Gpu()
+    layers, emb, act = build_decode_model(g)
+    if args.no_graph:
+        def step():
+            decode_step(g, layers, emb, act)
+    else:
+        # one decode step = one graph replay on the library stream
+        g.rt.check(g.L.qwen3_hip_capture_begin(), "capture_begin")
+        decode_step(g, layers, emb, act)
+        gid = ctypes.c_int(-1)
+        g.rt.check(g.L.qwen3_hip_capture_end(ctypes.byref(gid)), "capture_end")
+
+        def step():
+            g.rt.check(g.L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+    for _ in range(args.warmup):
+        step()
+    g.sync()
+    t0 = time.perf_counter()
+    g.record(60)
+    for _ in range(args.steps):
+        step()
+    g.record(61)
+    g.sync()
+    wall = time.perf_counter() - t0
+    ms_step = g.elapsed(60, 61) / args.steps
+    value = 1000.0 / ms_step
+
+    kclasses = None if args.no_extras else kernel_classes(g, layers, emb, act)
+    roofline = None
+    if kclasses:
+        dom = max(kclasses, key=lambda k: kclasses[k]["us_per_step"])
+        d = kclasses[dom]
+        roofline = {"bound": "hbm", "kernel": dom, "achieved": round(d["GBps"], 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(d["hbm_frac"], 4),
+                    "traffic": read_traffic(dom),
+                    "bytes_per_launch": d["bytes_per_launch"],
+                    "us_per_launch": round(d["us_per_launch"], 3)}
+    prefill = None if args.no_extras else prefill_gemms(g)
+    if args.calibrate_copy:
+        # a kernel of known traffic (64 MiB read + 64 MiB written per launch)
+        # for scaling FETCH_SIZE / WRITE_SIZE counters in profiled runs
+        nb = 64 << 20
+        src, dst = g.alloc(nb), g.alloc(nb)
+        for _ in range(5):
+            g.rt.check(g.L.qwen3_hip_copy_dev(ctypes.c_void_p(dst), ctypes.c_void_p(src), nb), "copy")
+        g.sync()
+
+    line = {
+        "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: random bf16 weights N(0,0.02), fp32 activations N(0,1) rounded to bf16",
+        "config": {"workload": "Qwen3-0.6B decode GEMV set at M=1: 28 layers x (q|k|v 1024->4096, "
+                               "o 2048->1024, gate|up+SiLU 1024->2x3072, down 3072->1024) + "
+                               "lm_head 1024->151936; distinct weights per layer",
+                   "M": 1, "layers": LAYERS, "step_bytes": STEP_BYTES,
+                   "launches_per_step": 4 * LAYERS + 1, "hip_graph": not args.no_graph},
+        "hbm_GBps_step": round(STEP_BYTES / (ms_step * 1e-3) / 1e9, 1),
+        "wall_s": round(wall, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kclasses,
+        "prefill_m512": prefill,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -130,6 +130,20 @@ int qwen3_hip_argmax_dev(int *out_d, const float *v_d, int n);
 int qwen3_hip_tile_to_row_dev(uint16_t *dst_d, const uint16_t *src_d,
                               int N, int K, int tile_n, int tile_k);
 
+/* device-to-device copy by a plain streaming kernel (bytes a multiple of 16,
+ * 16-byte aligned pointers); its traffic is exactly bytes read + bytes
+ * written, which makes it the reference for HBM traffic counters */
+int qwen3_hip_copy_dev(void *dst_d, const void *src_d, size_t bytes);
+
+/* HIP graphs: device-pointer calls made between capture_begin and
+ * capture_end are recorded, not run; graph_launch replays them on the
+ * library stream (a decode step becomes one submission).  Only the _dev
+ * entry points may be captured (the host-pointer ones synchronise). */
+int qwen3_hip_capture_begin(void);
+int qwen3_hip_capture_end(int *graph_id);
+int qwen3_hip_graph_launch(int graph_id);
+int qwen3_hip_graph_destroy(int graph_id);
+
 int qwen3_hip_malloc(void **p_d, size_t bytes);
 int qwen3_hip_free(void *p_d);
 int qwen3_hip_memcpy_h2d(void *dst_d, const void *src, size_t bytes);

@@ -161,6 +161,90 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
     }
 }
 
+// M = 1 fast path (decode).  One wave owns ROWS output rows; lane l owns the
+// 16-byte chunks l, l+64, ..., l+64*(CPL-1) of every row (CPL = chunks per
+// lane, K <= 512*CPL).  All ROWS*CPL weight loads and the 2*CPL activation
+// loads are issued before the first use, so a launch costs one memory round
+// trip; there is no LDS and no barrier.  GATED: rows of Wg and Wu with the
+// same index are both loaded and the epilogue writes silu(gate) * up.
+template <int ROWS, int CPL, bool GATED>
+__global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
+                                                   const float *__restrict__ a,
+                                                   const uint16_t *__restrict__ b,
+                                                   const uint16_t *__restrict__ b2,
+                                                   int K, int N) {
+    constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
+    if (row0 >= N) return;
+    const int nch = K >> 3;
+    const u32x4 *b4 = reinterpret_cast<const u32x4 *>(b);
+    const u32x4 *u4 = reinterpret_cast<const u32x4 *>(b2);
+
+    u32x4 bv[NB][CPL];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+        const size_t rb = (size_t)min(row0 + r, N - 1) * nch;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            if (ch < nch) {
+                bv[r][j] = __builtin_nontemporal_load(b4 + rb + ch);
+                if constexpr (GATED) bv[ROWS + r][j] = __builtin_nontemporal_load(u4 + rb + ch);
+            } else {
+                bv[r][j] = u32x4{0u, 0u, 0u, 0u};
+                if constexpr (GATED) bv[ROWS + r][j] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
+    float av[CPL][8];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int ch = lane + WAVE * j;
+        if (ch < nch) {
+            const f32x4 *ap = reinterpret_cast<const f32x4 *>(a + ch * 8);
+            const f32x4 x0 = ap[0], x1 = ap[1];
+            av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
+            av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; j++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) av[j][e] = round_bf16(av[j][e]);
+
+    constexpr int V = pow2_ceil<NB>::v;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++)
+#pragma unroll
+        for (int r = 0; r < NB; r++) {
+            float s = acc[r];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                s = fmaf(av[j][2 * e], bf16_lo(bv[r][j][e]), s);
+                s = fmaf(av[j][2 * e + 1], bf16_hi(bv[r][j][e]), s);
+            }
+            acc[r] = s;
+        }
+
+    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+    const float tot = wave_transpose_reduce<V>(acc, lane);
+    const int idx = lane >> (6 - LV);
+    const int step = 64 >> LV;                       // lanes holding each value
+    if constexpr (!GATED) {
+        if ((lane & (step - 1)) == 0 && idx < ROWS && row0 + idx < N) c[row0 + idx] = tot;
+    } else {
+        const float up = __shfl(tot, (lane + ROWS * step) & 63);
+        if ((lane & (step - 1)) == 0 && idx < ROWS && row0 + idx < N) c[row0 + idx] = silu_mul(tot, up);
+    }
+}
+
 // Fused gate/up GEMV: rows of Wg and Wu with the same index share a wave, and
 // the epilogue writes silu(gate) * up.  Same constraints as k_gemv.
 template <int MR, int ROWS, int CU>
@@ -535,6 +619,21 @@ __global__ __launch_bounds__(WAVE) void k_argmax_final(int *__restrict__ out,
     if (threadIdx.x == 0) out[0] = (bi == 0x7FFFFFFF || v[0] != v[0]) ? 0 : bi;
 }
 
+// plain 16-byte-vector copy: a kernel of known traffic (bytes read = bytes
+// written = n16 * 16) against which HBM traffic counters are calibrated
+__global__ __launch_bounds__(NTHREADS) void k_copy16(u32x4 *__restrict__ dst,
+                                                    const u32x4 *__restrict__ src, size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n16;
+         i += (size_t)gridDim.x * NTHREADS)
+        dst[i] = __builtin_nontemporal_load(src + i);
+}
+
+__global__ __launch_bounds__(NTHREADS) void k_fill_zero(float *__restrict__ c, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * NTHREADS)
+        c[i] = 0.0f;
+}
+
 // ---------------------------------------------------------------------------
 // host side of the shim
 // ---------------------------------------------------------------------------
@@ -546,6 +645,9 @@ static char g_devname[256];
 static hipEvent_t g_ev[64];
 static int g_ev_made[64];
 static int g_forced_plan = 0;
+#define QH_MAX_GRAPHS 16
+static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
+static int g_capturing = 0;
 static float *g_am_v = nullptr;   // argmax partials (allocated at init)
 static int *g_am_i = nullptr;
 static const int AM_BLOCKS = 1024;
@@ -593,6 +695,8 @@ extern "C" int qh_init(int device) {
 extern "C" void qh_shutdown(void) {
     if (!g_inited) return;
     (void)hipStreamSynchronize(g_stream);
+    for (int i = 0; i < QH_MAX_GRAPHS; i++)
+        if (g_graph_exec[i]) { (void)hipGraphExecDestroy(g_graph_exec[i]); g_graph_exec[i] = nullptr; }
     for (int i = 0; i < 64; i++)
         if (g_ev_made[i]) { (void)hipEventDestroy(g_ev[i]); g_ev_made[i] = 0; }
     (void)hipFree(g_am_v);
@@ -722,9 +826,61 @@ extern "C" int qh_force_plan(int plan_id) {
     return QH_OK;
 }
 
+template <int ROWS, bool GATED>
+static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                             int K, int N, int cpl) {
+    const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
+    // only the (ROWS, CPL) pairs launch_gemv1 can pick: <= 16 loads per lane
+#define QH_GEMV1_CASE(P)                                                                     \
+    case P:                                                                                  \
+        if constexpr (ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16)                         \
+            hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED>), dim3(grid), dim3(NTHREADS), 0,     \
+                               g_stream, c, a, b, b2, K, N);                                 \
+        else                                                                                 \
+            return QH_EINVAL;                                                                \
+        break;
+    switch (cpl) {
+        QH_GEMV1_CASE(1)
+        QH_GEMV1_CASE(2)
+        QH_GEMV1_CASE(3)
+        QH_GEMV1_CASE(4)
+        QH_GEMV1_CASE(5)
+        QH_GEMV1_CASE(6)
+        QH_GEMV1_CASE(7)
+        QH_GEMV1_CASE(8)
+        default: return QH_EINVAL;
+    }
+#undef QH_GEMV1_CASE
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// M = 1 with K <= 4096.  Rows per wave: as many as keep >= 2048 waves in the
+// grid (8 per CU) and <= 16 weight loads of 16 B in flight per lane.
+static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                        int K, int N, bool gated) {
+    const int cpl = (K / 8 + WAVE - 1) / WAVE;
+    const int per_row = gated ? 2 * cpl : cpl;
+    int rows = 8;
+    while (rows > 1 && (long)(N + rows - 1) / rows < 2048) rows /= 2;
+    while (rows > 1 && rows * per_row > 16) rows /= 2;
+    if (gated && rows > 4) rows = 4;
+    switch (rows) {
+        case 1: return gated ? launch_gemv1_rows<1, true>(c, a, b, b2, K, N, cpl)
+                             : launch_gemv1_rows<1, false>(c, a, b, b2, K, N, cpl);
+        case 2: return gated ? launch_gemv1_rows<2, true>(c, a, b, b2, K, N, cpl)
+                             : launch_gemv1_rows<2, false>(c, a, b, b2, K, N, cpl);
+        case 4: return gated ? launch_gemv1_rows<4, true>(c, a, b, b2, K, N, cpl)
+                             : launch_gemv1_rows<4, false>(c, a, b, b2, K, N, cpl);
+        case 8: return launch_gemv1_rows<8, false>(c, a, b, b2, K, N, cpl);
+        default: return QH_EINVAL;
+    }
+}
+
 template <int MR>
 static int launch_gemv_mr(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                           int K, int N, bool gated) {
+    if (MR == 1 && K <= 8 * WAVE * 8) return launch_gemv1(c, a, b, b2, K, N, gated);
     const size_t lds = (size_t)MR * K * sizeof(float);
     // rows per wave: enough waves to cover the GPU for small N, and up to 8
     // rows (16 loads of 16 B in flight per lane at K = 1024) for large N
@@ -807,7 +963,12 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
     if (M == 0 || N == 0) return QH_OK;
     if (!c || !b || !a || (gated && !b2)) return QH_EINVAL;
     if (K == 0) {   // empty sum: the reference writes 0.0f (and silu(0)*0 = 0)
-        HCHECK(hipMemsetAsync(c, 0, (size_t)M * N * sizeof(float), g_stream), QH_ERUNTIME);
+        // a kernel, not hipMemsetAsync: this may be recorded into a graph
+        const size_t n = (size_t)M * N;
+        const size_t want = (n + NTHREADS - 1) / NTHREADS;
+        hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)(want < 4096 ? want : 4096)), dim3(NTHREADS), 0,
+                           g_stream, c, n);
+        HCHECK(hipGetLastError(), QH_ELAUNCH);
         return QH_OK;
     }
     const bool vec = (K % 8) == 0 && aligned16(a) && aligned16(b) && (!gated || aligned16(b2));
@@ -834,6 +995,64 @@ extern "C" int qh_tile_to_row(uint16_t *dst, const uint16_t *src, int N, int K, 
     const size_t total = (size_t)N * K;
     const int grid = (int)((total + NTHREADS - 1) / NTHREADS < 8192 ? (total + NTHREADS - 1) / NTHREADS : 8192);
     hipLaunchKernelGGL(k_tile_to_row, dim3(grid), dim3(NTHREADS), 0, g_stream, dst, src, N, K, tn, tk);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// ---- stream capture into HIP graphs ------------------------------------------
+
+extern "C" int qh_capture_begin(void) {
+    if (!g_inited) return QH_ESTATE;
+    if (g_capturing) return QH_ESTATE;
+    HCHECK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), QH_ERUNTIME);
+    g_capturing = 1;
+    return QH_OK;
+}
+
+extern "C" int qh_capture_end(int *graph_id) {
+    if (!g_inited || !g_capturing) return QH_ESTATE;
+    g_capturing = 0;
+    hipGraph_t graph = nullptr;
+    HCHECK(hipStreamEndCapture(g_stream, &graph), QH_ERUNTIME);
+    int slot = -1;
+    for (int i = 0; i < QH_MAX_GRAPHS; i++)
+        if (!g_graph_exec[i]) { slot = i; break; }
+    if (slot < 0) {
+        (void)hipGraphDestroy(graph);
+        return QH_ETOOBIG;
+    }
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return fail(e, QH_ERUNTIME);
+    g_graph_exec[slot] = exec;
+    if (graph_id) *graph_id = slot;
+    return QH_OK;
+}
+
+extern "C" int qh_graph_launch(int id) {
+    if (!g_inited) return QH_ESTATE;
+    if (id < 0 || id >= QH_MAX_GRAPHS || !g_graph_exec[id]) return QH_EINVAL;
+    HCHECK(hipGraphLaunch(g_graph_exec[id], g_stream), QH_ERUNTIME);
+    return QH_OK;
+}
+
+extern "C" int qh_graph_destroy(int id) {
+    if (id < 0 || id >= QH_MAX_GRAPHS || !g_graph_exec[id]) return QH_EINVAL;
+    HCHECK(hipGraphExecDestroy(g_graph_exec[id]), QH_ERUNTIME);
+    g_graph_exec[id] = nullptr;
+    return QH_OK;
+}
+
+extern "C" int qh_copy(void *dst, const void *src, size_t bytes) {
+    if (!g_inited) return QH_ESTATE;
+    if (!dst || !src || (bytes & 15u) || !aligned16(dst) || !aligned16(src)) return QH_EINVAL;
+    if (bytes == 0) return QH_OK;
+    const size_t n16 = bytes / 16;
+    const size_t want = (n16 + NTHREADS - 1) / NTHREADS;
+    const int grid = (int)(want < 4096 ? want : 4096);
+    hipLaunchKernelGGL(k_copy16, dim3(grid), dim3(NTHREADS), 0, g_stream, (u32x4 *)dst,
+                       (const u32x4 *)src, n16);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }

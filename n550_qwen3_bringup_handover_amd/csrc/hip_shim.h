@@ -57,6 +57,17 @@ int qh_tile_to_row(uint16_t *dst_d, const uint16_t *src_d, int N, int K,
 /* first index of the maximum of v[0..n) (ties -> lowest index) */
 int qh_argmax(int *out_d, const float *v_d, int n);
 
+/* device copy by a plain 16-byte-vector kernel (bytes % 16 == 0, 16-byte
+ * aligned pointers): the known-traffic reference for HBM counter calibration */
+int qh_copy(void *dst_d, const void *src_d, size_t bytes);
+
+/* stream capture: launches between begin and end are recorded (not run)
+ * into a graph that qh_graph_launch replays on the shim stream */
+int qh_capture_begin(void);
+int qh_capture_end(int *graph_id);
+int qh_graph_launch(int graph_id);
+int qh_graph_destroy(int graph_id);
+
 /* kernel choice for a GEMM shape (for logs/tests): returns a static name */
 const char *qh_gemm_plan(int M, int K, int N, int gated);
 /* override the automatic choice: 0 = auto, otherwise a plan id (see

@@ -423,6 +423,16 @@ int qwen3_hip_tile_to_row_dev(uint16_t *dst, const uint16_t *src, int N, int K, 
     return note(qh_tile_to_row(dst, src, N, K, tn, tk));
 }
 
+int qwen3_hip_copy_dev(void *dst, const void *src, size_t bytes) {
+    READY_OR_RETURN();
+    return note(qh_copy(dst, src, bytes));
+}
+
+int qwen3_hip_capture_begin(void) { READY_OR_RETURN(); return note(qh_capture_begin()); }
+int qwen3_hip_capture_end(int *graph_id) { READY_OR_RETURN(); return note(qh_capture_end(graph_id)); }
+int qwen3_hip_graph_launch(int graph_id) { READY_OR_RETURN(); return note(qh_graph_launch(graph_id)); }
+int qwen3_hip_graph_destroy(int graph_id) { READY_OR_RETURN(); return note(qh_graph_destroy(graph_id)); }
+
 int qwen3_hip_malloc(void **p, size_t bytes) { READY_OR_RETURN(); return note(qh_malloc(p, bytes)); }
 int qwen3_hip_free(void *p) { READY_OR_RETURN(); return note(qh_free(p)); }
 int qwen3_hip_memcpy_h2d(void *d, const void *s, size_t n) { READY_OR_RETURN(); return note(qh_h2d(d, s, n)); }

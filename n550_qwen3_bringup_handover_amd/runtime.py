@@ -56,6 +56,11 @@ _PROTOS = {
     "qwen3_hip_gemm_gate_up_silu_dev": (ctypes.c_int, [VP, VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_argmax_dev": (ctypes.c_int, [VP, VP, ctypes.c_int]),
     "qwen3_hip_tile_to_row_dev": (ctypes.c_int, [VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_copy_dev": (ctypes.c_int, [VP, VP, ctypes.c_size_t]),
+    "qwen3_hip_capture_begin": (ctypes.c_int, []),
+    "qwen3_hip_capture_end": (ctypes.c_int, [I32P]),
+    "qwen3_hip_graph_launch": (ctypes.c_int, [ctypes.c_int]),
+    "qwen3_hip_graph_destroy": (ctypes.c_int, [ctypes.c_int]),
     "qwen3_hip_malloc": (ctypes.c_int, [ctypes.POINTER(VP), ctypes.c_size_t]),
     "qwen3_hip_free": (ctypes.c_int, [VP]),
     "qwen3_hip_memcpy_h2d": (ctypes.c_int, [VP, VP, ctypes.c_size_t]),

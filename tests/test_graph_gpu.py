@@ -1,0 +1,61 @@
+"""Captured HIP graphs replay the device-pointer GEMMs exactly as eager calls
+do: several replays, with eager work and synchronisation between them, each
+checked bit-for-bit against the eager result."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from n550_qwen3_bringup_handover_amd import abi, runtime
+from tests import numerics
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_replay_matches_eager():
+    L = runtime.init()
+    shapes = [(1, 1024, 4096, False), (1, 2048, 1024, False), (1, 1024, 3072, True),
+              (1, 3072, 1024, False), (64, 1024, 2048, False), (5, 40, 17, False), (2, 0, 8, False)]
+    bufs = []
+    for i, (M, K, N, gated) in enumerate(shapes):
+        a = oracle.f32_bf16_normal(max(M * K, 1), 40 + i)
+        w = oracle.bf16_normal(max(N * K, 1) * (2 if gated else 1), 50 + i, 0.02)
+        bufs.append((abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(w),
+                     abi.DeviceBuffer(4 * M * N + 4), a, w))
+
+    def issue():
+        for (M, K, N, gated), (ad, wd, cd, _, _) in zip(shapes, bufs):
+            if gated:
+                abi.gemm_gate_up_silu_dev(cd.ptr, ad.ptr, wd.ptr, wd.ptr + 2 * N * K, M, K, N)
+            else:
+                abi.gemm_dev(cd.ptr, ad.ptr, wd.ptr, M, K, N)
+
+    def outputs():
+        abi.sync()
+        return [cd.download(np.float32, M * N) for (M, K, N, _), (_, _, cd, _, _) in zip(shapes, bufs)]
+
+    issue()
+    eager = outputs()
+    for (M, K, N, gated), out, (_, _, _, a, w) in zip(shapes, eager, bufs):
+        if K and not gated:
+            numerics.compare(out, a, w, M, K, N)
+
+    runtime.check(L.qwen3_hip_capture_begin(), "capture_begin")
+    issue()
+    gid = ctypes.c_int(-1)
+    runtime.check(L.qwen3_hip_capture_end(ctypes.byref(gid)), "capture_end")
+    try:
+        scratch = abi.DeviceBuffer(4 * 64 * 2048)
+        for rep in range(4):
+            for _, _, cd, _, _ in bufs:          # poison the outputs first
+                cd.upload(np.full(cd.nbytes // 4, np.nan, np.float32))
+            runtime.check(L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+            got = outputs()
+            for e, g in zip(eager, got):
+                assert np.array_equal(e.view(np.uint32), g.view(np.uint32)), rep
+            # unrelated eager work between replays
+            abi.gemm_dev(scratch.ptr, bufs[4][0].ptr, bufs[4][1].ptr, 64, 1024, 2048)
+            abi.sync()
+    finally:
+        runtime.check(L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
