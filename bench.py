@@ -324,7 +324,7 @@ def prefill_gemms(g):
             fn = lambda r, K=K, N=N: g.gemm(c, a, wmax, M, K, N)
             flops = 2.0 * M * N * K
             byts = 2 * N * K + 4 * M * K + 4 * M * N
-        ms = time_launches(g, fn, 32)
+        ms = time_launches_graph(g, fn, 32)
         tf = flops / (ms * 1e-3) / 1e12
         res[name] = {"M": M, "K": K, "N": N, "kernel": g.plan(M, K, N, gated),
                      "us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),

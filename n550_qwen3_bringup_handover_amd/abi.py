@@ -160,4 +160,10 @@ def force_plan(plan_id):
 
 
 PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4,
-         "mfma32x128": 5, "mfma16x64": 6, "mfma64x64-scalar": 7}
+         "mfma32x128": 5, "mfma16x64": 6, "mfma64x64-scalar": 7,
+         "ring32x64k128s4": 8, "ring64x64k64s4": 9, "ring64x64k64s6": 10, "ring64x64k128s3": 11,
+         "ring64x128k64s4": 12, "ring128x128k64s3": 13, "ring128x64k64s3": 14,
+         "ring32x64k64s6": 15, "ring64x64k32s6": 16, "ring32x64k32s4": 17,
+         "pipe32x64k128s3": 18, "pipe32x64k128s4": 19, "pipe64x64k128s3": 20, "pipe64x64k64s4": 21,
+         "pipe64x128k64s4": 22, "pipe128x128k64s3": 23, "pipe128x64k64s3": 24, "pipe32x64k64s4": 25,
+         "pipe64x64k64s3": 26}

@@ -18,6 +18,7 @@
 //   k_argmax_*           first-max reduction for greedy decoding.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "hip_shim.h"
@@ -378,12 +379,34 @@ __device__ __forceinline__ int b_tile_row(int wn, int j) {
     }
 }
 
+// Output-tile order for a 1-D grid.  Workgroups are handed to the 8 XCDs
+// round-robin (workgroup b runs on XCD b % 8) and each XCD has its own L2, so
+// the MT x NT tile grid is cut into rm x rn = 8 regions, one per XCD, and the
+// workgroups of an XCD walk their region m-major (consecutive ones share an A
+// panel).  Each XCD then pulls only its A and B slabs into its L2.  rm == 0
+// means plain row-major order (used when the grid does not split evenly).
+struct TileMap {
+    int MT, NT, rm, rn;
+};
+
+__device__ __forceinline__ void tile_of(int bid, const TileMap &map, int &tm, int &tn) {
+    if (map.rm == 0) {
+        tm = bid / map.NT;
+        tn = bid % map.NT;
+        return;
+    }
+    const int xcd = bid & 7, local = bid >> 3;
+    const int rmt = map.MT / map.rm, rnt = map.NT / map.rn;    // tiles per region
+    tm = (xcd / map.rn) * rmt + local / rnt;
+    tn = (xcd % map.rn) * rnt + local % rnt;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool VEC>
 __global__ __launch_bounds__(NTHREADS, 2) void k_gemm(float *__restrict__ c,
                                                      const float *__restrict__ a,
                                                      const uint16_t *__restrict__ b,
                                                      const uint16_t *__restrict__ b2,
-                                                     int M, int K, int N) {
+                                                     int M, int K, int N, TileMap map) {
     using C = GemmCfg<BM, BN, BK, WM, WN, GATED, VEC>;
     __shared__ u32x4 sA[2][BM * C::CPR];
     __shared__ u32x4 sB[2][BN * C::CPR];
@@ -391,8 +414,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_gemm(float *__restrict__ c,
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.y * BM;
-    const int n0 = blockIdx.x * C::BNO;
+    int tm, tn;
+    tile_of(blockIdx.x, map, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * C::BNO;
 
     // ---- global -> register staging ----
     float ra[C::A_CHUNKS][8];
@@ -555,6 +580,448 @@ __global__ __launch_bounds__(NTHREADS, 2) void k_gemm(float *__restrict__ c,
 }
 
 // ---------------------------------------------------------------------------
+// Ring-pipelined MFMA GEMM (K % 32 == 0, 16-byte aligned operands)
+// ---------------------------------------------------------------------------
+// A k-loop that waits for one global round trip per step is latency-bound
+// (~0.7 us per step on MI355X).  Here every 32-wide k step of the A tile
+// (fp32) and B tile (bf16) is copied straight from global memory into a ring
+// of STAGES LDS slots by global_load_lds_dwordx4 (no registers involved), and
+// STAGES-1 steps are always in flight.  Per step each wave waits only for its
+// own oldest copies (s_waitcnt vmcnt), one barrier publishes the slot and
+// frees the previous one, the next copy is issued, then MFMAs run on the
+// slot; A is converted to bf16 (RNE) as its fragments are read.
+//
+// LDS slot layout (one step): A rows of 32 fp32 (128 B = 8 chunks of 16 B),
+// then B rows of 32 bf16 (64 B = 4 chunks).  Chunk c of row r sits at
+// c ^ swzA(r) / c ^ swzB(r); both swizzles keep 16 consecutive rows at one
+// logical chunk on distinct banks (checked for 8- and 16-lane LDS passes).
+// A wave's LDS copy always fills 1 KB contiguously (lane i -> bytes 16i..),
+// so each lane picks the global chunk that belongs at its LDS position.
+// Swizzle for rows of CH 16-byte chunks (64, 128, 256 or 512 bytes).
+template <int CH>
+__device__ __forceinline__ int swz(int r) {
+    if constexpr (CH == 4) return ((r >> 1) ^ (r >> 3)) & 3;
+    else if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
+    else return r & 15;                       // 16 or 32 chunks
+}
+
+// s_waitcnt immediate for "at most n vector-memory ops outstanding" (gfx9
+// encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at max)
+#define QH_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
+
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_ = 32>
+struct RingCfg {
+    static constexpr int BK = BK_;                      // k per stage (32, 64, 128)
+    static constexpr int KS = BK / 32;                  // MFMA k-steps per stage
+    static constexpr int CA = BK / 4, CB = BK / 8;      // 16-byte chunks per A / B row
+    static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 2;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int A_DMA = A_BYTES / 1024 / 4;   // 1 KB copies per wave per step
+    static constexpr int B_DMA = B_BYTES / 1024 / 4;
+    static constexpr int LPS = A_DMA + B_DMA;           // copies per wave per step
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int TM = WTM / 16, TN = WTN / 16;
+    static constexpr int BNO = GATED ? BN / 2 : BN;
+    static constexpr int LDS = STAGES * STAGE;
+    static constexpr int vm(int k) { return k * LPS > 63 ? 63 : k * LPS; }
+    static_assert(WM * WN == 4, "4 waves");
+    static_assert(BM % 32 == 0 && BN % 64 == 0, "every wave issues the same number of copies");
+    static_assert(A_DMA >= 1 && B_DMA >= 1, "copies per wave");
+    static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
+    static_assert(STAGES >= 2 && (STAGES - 2) * LPS <= 63, "vmcnt range");
+};
+
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_>
+__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_ring(float *__restrict__ c,
+                                                          const float *__restrict__ a,
+                                                          const uint16_t *__restrict__ b,
+                                                          const uint16_t *__restrict__ b2,
+                                                          int M, int K, int N, TileMap map) {
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_>;
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, map, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * R::BNO;
+    const int nk = K / R::BK;
+
+    // per-lane global source rows/chunks for this wave's copies (fixed over k)
+    const float *asrc[R::A_DMA];
+    const uint16_t *bsrc[R::B_DMA];
+#pragma unroll
+    for (int i = 0; i < R::A_DMA; i++) {
+        const int seg = wave * R::A_DMA + i;            // 64 / CA rows per 1 KB
+        const int r = seg * (64 / R::CA) + lane / R::CA;
+        const int cl = (lane % R::CA) ^ swz<R::CA>(r);
+        const int gm = min(m0 + r, M - 1);              // rows >= M: any valid row
+        asrc[i] = a + (size_t)gm * K + cl * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < R::B_DMA; i++) {
+        const int seg = wave * R::B_DMA + i;            // 64 / CB rows per 1 KB
+        const int r = seg * (64 / R::CB) + lane / R::CB;
+        const int cl = (lane % R::CB) ^ swz<R::CB>(r);
+        const uint16_t *src = b;
+        int gn;
+        if constexpr (GATED) {
+            const bool up = r >= R::BNO;
+            gn = n0 + (up ? r - R::BNO : r);
+            src = up ? b2 : b;
+        } else {
+            gn = n0 + r;
+        }
+        gn = min(gn, N - 1);                            // cols >= N: any valid row
+        bsrc[i] = src + (size_t)gn * K + cl * 8;
+    }
+
+    auto issue = [&](int step) {
+        unsigned char *slot = smem + (step % STAGES) * R::STAGE;
+        const int k0 = step * R::BK;
+#pragma unroll
+        for (int i = 0; i < R::A_DMA; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(asrc[i] + k0),
+                (__attribute__((address_space(3))) void *)(slot + (wave * R::A_DMA + i) * 1024),
+                16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < R::B_DMA; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(bsrc[i] + k0),
+                (__attribute__((address_space(3))) void *)(slot + R::A_BYTES + (wave * R::B_DMA + i) * 1024),
+                16, 0, 0);
+    };
+
+    f32x4 acc[R::TM][R::TN];
+#pragma unroll
+    for (int i = 0; i < R::TM; i++)
+#pragma unroll
+        for (int j = 0; j < R::TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int pro = nk < STAGES - 1 ? nk : STAGES - 1;
+    for (int s = 0; s < pro; s++) issue(s);
+
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    for (int it = 0; it < nk; it++) {
+        // wait for this wave's copies of step `it`: the later steps issued so
+        // far may stay in flight
+        const int later = min(nk - 1 - it, STAGES - 2);
+        // (cases above STAGES-2 are unreachable; their counts are clamped so
+        // every immediate stays a valid encoding)
+        switch (later) {
+            case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
+            case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
+            case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
+            case 4: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
+            case 5: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(5))); break;
+            default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(6))); break;
+        }
+        // all waves' copies of `it` have landed, and all waves are done with
+        // step it-1, whose slot the next copy reuses
+        __builtin_amdgcn_s_barrier();
+        if (it + STAGES - 1 < nk) issue(it + STAGES - 1);
+
+        const unsigned char *slot = smem + (it % STAGES) * R::STAGE;
+        // every fragment read of the stage first (raw fp32 for A), then the
+        // conversions and MFMAs, so LDS latency overlaps across k-steps
+        u32x4 araw[R::KS][R::TM][2], bfr[R::KS][R::TN];
+#pragma unroll
+        for (int t = 0; t < R::KS; t++) {
+#pragma unroll
+            for (int i = 0; i < R::TM; i++) {
+                const int row = wm * R::WTM + 16 * i + lrow;
+                const int sw = swz<R::CA>(row);
+                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + row * (R::CA * 16));
+                araw[t][i][0] = rowp[(8 * t + 2 * lgrp) ^ sw];
+                araw[t][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ sw];
+            }
+#pragma unroll
+            for (int j = 0; j < R::TN; j++) {
+                const int row = b_tile_row<BN, WN, R::TN, GATED>(wn, j) + lrow;
+                const u32x4 *rowp =
+                    reinterpret_cast<const u32x4 *>(slot + R::A_BYTES + row * (R::CB * 16));
+                bfr[t][j] = rowp[(4 * t + lgrp) ^ swz<R::CB>(row)];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < R::KS; t++) {
+            bf16x8 af[R::TM];
+#pragma unroll
+            for (int i = 0; i < R::TM; i++) {
+                const f32x4 x0 = __builtin_bit_cast(f32x4, araw[t][i][0]);
+                const f32x4 x1 = __builtin_bit_cast(f32x4, araw[t][i][1]);
+                u32x4 w;
+                w.x = pack_bf16x2(x0.x, x0.y);
+                w.y = pack_bf16x2(x0.z, x0.w);
+                w.z = pack_bf16x2(x1.x, x1.y);
+                w.w = pack_bf16x2(x1.z, x1.w);
+                af[i] = __builtin_bit_cast(bf16x8, w);
+            }
+#pragma unroll
+            for (int i = 0; i < R::TM; i++)
+#pragma unroll
+                for (int j = 0; j < R::TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        af[i], __builtin_bit_cast(bf16x8, bfr[t][j]), acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
+#pragma unroll
+    for (int i = 0; i < R::TM; i++) {
+        const int rbase = m0 + wm * R::WTM + 16 * i + 4 * lgrp;
+        if constexpr (!GATED) {
+#pragma unroll
+            for (int j = 0; j < R::TN; j++) {
+                const int col = n0 + wn * R::WTN + 16 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (rbase + r < M) c[(size_t)(rbase + r) * N + col] = acc[i][j][r];
+                }
+            }
+        } else {
+            constexpr int TNO = R::TN / 2;
+#pragma unroll
+            for (int j = 0; j < TNO; j++) {
+                const int col = n0 + wn * (R::BNO / WN) + 16 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (rbase + r < M)
+                            c[(size_t)(rbase + r) * N + col] = silu_mul(acc[i][j][r], acc[i][j + TNO][r]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Software-pipelined ring GEMM
+// ---------------------------------------------------------------------------
+template <int V> struct IC { static constexpr int value = V; };
+
+// Same LDS ring and copies as k_gemm_ring, but the phases of consecutive
+// stages overlap inside each wave: while the MFMAs of stage `it` run on
+// fragments already in registers, the LDS reads of stage it+1 fill a second
+// register set and the copies of stage it+STAGES-1 are in flight.  Per stage:
+//   wait (own copies of it+1) -> barrier -> issue copies of it+STAGES-1 ->
+//   read fragments of it+1 -> MFMAs of it.
+// The copy into slot (it-1) % STAGES is safe after the barrier: every wave
+// consumed stage it-1 (its MFMAs ran) before reaching it.  LDS destinations
+// of the copies are wave-uniform and computed from a scalar wave index.
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_>
+__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c,
+                                                          const float *__restrict__ a,
+                                                          const uint16_t *__restrict__ b,
+                                                          const uint16_t *__restrict__ b2,
+                                                          int M, int K, int N, TileMap map) {
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_>;
+    static_assert(STAGES >= 3, "one stage being read, one in use, one or more in flight");
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // scalar
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    tile_of(blockIdx.x, map, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * R::BNO;
+    const int nk = K / R::BK;
+
+    const float *asrc[R::A_DMA];
+    const uint16_t *bsrc[R::B_DMA];
+#pragma unroll
+    for (int i = 0; i < R::A_DMA; i++) {
+        const int seg = wave * R::A_DMA + i;
+        const int r = seg * (64 / R::CA) + lane / R::CA;
+        const int cl = (lane % R::CA) ^ swz<R::CA>(r);
+        const int gm = min(m0 + r, M - 1);
+        asrc[i] = a + (size_t)gm * K + cl * 4;
+    }
+#pragma unroll
+    for (int i = 0; i < R::B_DMA; i++) {
+        const int seg = wave * R::B_DMA + i;
+        const int r = seg * (64 / R::CB) + lane / R::CB;
+        const int cl = (lane % R::CB) ^ swz<R::CB>(r);
+        const uint16_t *src = b;
+        int gn;
+        if constexpr (GATED) {
+            const bool up = r >= R::BNO;
+            gn = n0 + (up ? r - R::BNO : r);
+            src = up ? b2 : b;
+        } else {
+            gn = n0 + r;
+        }
+        gn = min(gn, N - 1);
+        bsrc[i] = src + (size_t)gn * K + cl * 8;
+    }
+    // wave-uniform LDS byte offsets of this wave's copies within a slot
+    const int a_dst = wave * R::A_DMA * 1024;
+    const int b_dst = R::A_BYTES + wave * R::B_DMA * 1024;
+
+    auto issue = [&](int step) {
+        unsigned char *slot = smem + (step % STAGES) * R::STAGE;
+        const int k0 = step * R::BK;
+#pragma unroll
+        for (int i = 0; i < R::A_DMA; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(asrc[i] + k0),
+                (__attribute__((address_space(3))) void *)(slot + a_dst + i * 1024), 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < R::B_DMA; i++)
+            __builtin_amdgcn_global_load_lds(
+                (const void *)(bsrc[i] + k0),
+                (__attribute__((address_space(3))) void *)(slot + b_dst + i * 1024), 16, 0, 0);
+    };
+
+    const int lrow = lane & 15, lgrp = lane >> 4;
+    // per-lane LDS offsets of this lane's fragment rows (within a slot)
+    int arow_off[R::TM], arow_sw[R::TM], brow_off[R::TN], brow_sw[R::TN];
+#pragma unroll
+    for (int i = 0; i < R::TM; i++) {
+        const int row = wm * R::WTM + 16 * i + lrow;
+        arow_off[i] = row * (R::CA * 16);
+        arow_sw[i] = swz<R::CA>(row);
+    }
+#pragma unroll
+    for (int j = 0; j < R::TN; j++) {
+        const int row = b_tile_row<BN, WN, R::TN, GATED>(wn, j) + lrow;
+        brow_off[j] = R::A_BYTES + row * (R::CB * 16);
+        brow_sw[j] = swz<R::CB>(row);
+    }
+
+    u32x4 fa[2][R::KS][R::TM][2], fb[2][R::KS][R::TN];
+    // `SET` selects the register set at compile time (IC<0> / IC<1>)
+    auto read_frags = [&](int step, auto SET) {
+        constexpr int set = decltype(SET)::value;
+        const unsigned char *slot = smem + (step % STAGES) * R::STAGE;
+#pragma unroll
+        for (int t = 0; t < R::KS; t++) {
+#pragma unroll
+            for (int i = 0; i < R::TM; i++) {
+                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + arow_off[i]);
+                fa[set][t][i][0] = rowp[(8 * t + 2 * lgrp) ^ arow_sw[i]];
+                fa[set][t][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ arow_sw[i]];
+            }
+#pragma unroll
+            for (int j = 0; j < R::TN; j++) {
+                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + brow_off[j]);
+                fb[set][t][j] = rowp[(4 * t + lgrp) ^ brow_sw[j]];
+            }
+        }
+    };
+
+    f32x4 acc[R::TM][R::TN];
+#pragma unroll
+    for (int i = 0; i < R::TM; i++)
+#pragma unroll
+        for (int j = 0; j < R::TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto mfmas = [&](auto SET) {
+        constexpr int set = decltype(SET)::value;
+#pragma unroll
+        for (int t = 0; t < R::KS; t++) {
+            bf16x8 af[R::TM];
+#pragma unroll
+            for (int i = 0; i < R::TM; i++) {
+                const f32x4 x0 = __builtin_bit_cast(f32x4, fa[set][t][i][0]);
+                const f32x4 x1 = __builtin_bit_cast(f32x4, fa[set][t][i][1]);
+                u32x4 w;
+                w.x = pack_bf16x2(x0.x, x0.y);
+                w.y = pack_bf16x2(x0.z, x0.w);
+                w.z = pack_bf16x2(x1.x, x1.y);
+                w.w = pack_bf16x2(x1.z, x1.w);
+                af[i] = __builtin_bit_cast(bf16x8, w);
+            }
+#pragma unroll
+            for (int i = 0; i < R::TM; i++)
+#pragma unroll
+                for (int j = 0; j < R::TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        af[i], __builtin_bit_cast(bf16x8, fb[set][t][j]), acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // prologue: copies of stages 0 .. STAGES-2 in flight; stage 0 read
+    const int pro = nk < STAGES - 1 ? nk : STAGES - 1;
+    for (int s = 0; s < pro; s++) issue(s);
+    {
+        const int later = min(nk - 1, STAGES - 2);      // stages issued after stage 0
+        switch (later) {
+            case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
+            case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
+            case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
+            case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
+            case 4: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
+            default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(5))); break;
+        }
+        __builtin_amdgcn_s_barrier();
+        read_frags(0, IC<0>{});
+    }
+
+    // one pipeline step: MFMAs on register set CUR while stage it+1 is read
+    // into the other set
+    auto step = [&](int it, auto CUR) {
+        constexpr int cur = decltype(CUR)::value;
+        if (it + 1 < nk) {
+            // own copies of stage it+1 landed: stages it+2 .. it+STAGES-2 may
+            // still be in flight
+            const int later = min(nk - 2 - it, STAGES - 3);
+            switch (later) {
+                case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
+                case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
+                case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
+                case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
+                default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
+            }
+            __builtin_amdgcn_s_barrier();
+            if (it + STAGES - 1 < nk) issue(it + STAGES - 1);
+            read_frags(it + 1, IC<cur ^ 1>{});
+        }
+        mfmas(CUR);
+    };
+    for (int it = 0; it < nk; it += 2) {
+        step(it, IC<0>{});
+        if (it + 1 < nk) step(it + 1, IC<1>{});
+    }
+
+    // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
+#pragma unroll
+    for (int i = 0; i < R::TM; i++) {
+        const int rbase = m0 + wm * R::WTM + 16 * i + 4 * lgrp;
+        if constexpr (!GATED) {
+#pragma unroll
+            for (int j = 0; j < R::TN; j++) {
+                const int col = n0 + wn * R::WTN + 16 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (rbase + r < M) c[(size_t)(rbase + r) * N + col] = acc[i][j][r];
+                }
+            }
+        } else {
+            constexpr int TNO = R::TN / 2;
+#pragma unroll
+            for (int j = 0; j < TNO; j++) {
+                const int col = n0 + wn * (R::BNO / WN) + 16 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (rbase + r < M)
+                            c[(size_t)(rbase + r) * N + col] = silu_mul(acc[i][j][r], acc[i][j + TNO][r]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // misc kernels
 // ---------------------------------------------------------------------------
 // dst[n][k] = src[tile(n,k)], tile-major as in kernels_ame.c:212-215,269
@@ -645,6 +1112,7 @@ static char g_devname[256];
 static hipEvent_t g_ev[64];
 static int g_ev_made[64];
 static int g_forced_plan = 0;
+static int g_no_xcd_map = 0;      // tuning switch: 1 = row-major tile order
 #define QH_MAX_GRAPHS 16
 static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
 static int g_capturing = 0;
@@ -684,6 +1152,10 @@ extern "C" int qh_init(int device) {
         return QH_ENODEV;             // the code objects are built for gfx950 only
     }
     strncpy(g_devname, prop.gcnArchName, sizeof g_devname - 1);
+    {
+        const char *e = getenv("QWEN3_HIP_NO_XCD_MAP");   // A/B switch for tile order
+        g_no_xcd_map = (e && e[0] == '1') ? 1 : 0;
+    }
     HCHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), QH_ERUNTIME);
     HCHECK(hipMalloc((void **)&g_am_v, AM_BLOCKS * sizeof(float)), QH_ENOMEM);
     HCHECK(hipMalloc((void **)&g_am_i, AM_BLOCKS * sizeof(int)), QH_ENOMEM);
@@ -793,10 +1265,44 @@ enum {
     PLAN_T32x128 = 5,
     PLAN_T16x64 = 6,
     PLAN_SCALAR64 = 7,     // MFMA 64x64 with element-wise loads (any K, any alignment)
-    PLAN_COUNT = 8
+    // ring-pipelined (K % BK == 0): tile, k per stage, LDS stages
+    PLAN_R32x64k128s4 = 8,
+    PLAN_R64x64k64s4 = 9,
+    PLAN_R64x64k64s6 = 10,
+    PLAN_R64x64k128s3 = 11,
+    PLAN_R64x128k64s4 = 12,
+    PLAN_R128x128k64s3 = 13,
+    PLAN_R128x64k64s3 = 14,
+    PLAN_R32x64k64s6 = 15,
+    PLAN_R64x64k32s6 = 16,
+    PLAN_R32x64k32s4 = 17,
+    // software-pipelined ring (K % BK == 0)
+    PLAN_P32x64k128s3 = 18,
+    PLAN_P32x64k128s4 = 19,
+    PLAN_P64x64k128s3 = 20,
+    PLAN_P64x64k64s4 = 21,
+    PLAN_P64x128k64s4 = 22,
+    PLAN_P128x128k64s3 = 23,
+    PLAN_P128x64k64s3 = 24,
+    PLAN_P32x64k64s4 = 25,
+    PLAN_P64x64k64s3 = 26,
+    PLAN_COUNT = 27
 };
 static const char *k_plan_names[PLAN_COUNT] = {
-    "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar"};
+    "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
+    "ring32x64k128s4", "ring64x64k64s4", "ring64x64k64s6", "ring64x64k128s3", "ring64x128k64s4",
+    "ring128x128k64s3", "ring128x64k64s3", "ring32x64k64s6", "ring64x64k32s6", "ring32x64k32s4",
+    "pipe32x64k128s3", "pipe32x64k128s4", "pipe64x64k128s3", "pipe64x64k64s4", "pipe64x128k64s4",
+    "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3"};
+static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p < PLAN_COUNT; }
+static inline int ring_bk(int p) {
+    switch (p) {
+        case PLAN_R32x64k128s4: case PLAN_R64x64k128s3:
+        case PLAN_P32x64k128s3: case PLAN_P32x64k128s4: case PLAN_P64x64k128s3: return 128;
+        case PLAN_R64x64k32s6: case PLAN_R32x64k32s4: return 32;
+        default: return 64;
+    }
+}
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -807,6 +1313,17 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     auto blocks = [&](int bm, int bn) {
         return (long)((M + bm - 1) / bm) * (long)((N + bn / bno - 1) / (bn / bno));
     };
+    // Measured on MI355X (Qwen3-0.6B projection shapes, M = 16 .. 4096): the
+    // software-pipelined 32x64 tile with 128-deep stages wins while its tiles
+    // fit one round on the 256 CUs (it holds 128 KB of LDS, one block per
+    // CU); with 64-deep stages (64 KB, two blocks per CU) up to two rounds;
+    // larger grids and large M do better with the register-staged 64- and
+    // 128-wide tiles.
+    if (M <= 128 || (!gated && M <= 512)) {
+        const long t = blocks(32, 64);
+        if (K % 128 == 0 && t <= 256) return PLAN_P32x64k128s4;
+        if (K % 64 == 0 && t <= 512) return PLAN_P32x64k64s4;
+    }
     if (M <= 16) return PLAN_T16x64;
     if (M <= 32) return PLAN_T32x128;
     if (M <= 64) return (blocks(64, 128) >= 256) ? PLAN_T64x128 : PLAN_T64x64;
@@ -922,14 +1439,80 @@ static int launch_gemv_mr(float *c, const float *a, const uint16_t *b, const uin
     return QH_OK;
 }
 
+// Tile grid of an M x N output in BM x BNO tiles, with the 8-way XCD split
+// whose per-XCD A + B slabs are smallest (row-major order when no split
+// divides the grid).  Returns the number of tiles, or -1 if too many.
+static long make_map(TileMap &map, int M, int N, int K, int BM, int BN, int BNO) {
+    map.MT = (M + BM - 1) / BM;
+    map.NT = (N + BNO - 1) / BNO;
+    const long tiles = (long)map.MT * map.NT;
+    if (tiles > 0x7FFFFFFFL) return -1;
+    map.rm = 0;
+    map.rn = 0;
+    if (!g_no_xcd_map) {
+        double best = 0.0;
+        for (int rm = 1; rm <= 8; rm *= 2) {
+            const int rn = 8 / rm;
+            if (map.MT % rm || map.NT % rn) continue;
+            const double slab = (double)(map.MT / rm) * BM * K * 4.0 +
+                                (double)(map.NT / rn) * BN * K * 2.0;
+            if (map.rm == 0 || slab < best) { best = slab; map.rm = rm; map.rn = rn; }
+        }
+    }
+    return tiles;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool VEC>
 static int launch_tile(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                        int M, int K, int N) {
-    constexpr int BNO = GATED ? BN / 2 : BN;
-    const dim3 grid((N + BNO - 1) / BNO, (M + BM - 1) / BM);
-    if (grid.y > 65535u) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm<BM, BN, BK, WM, WN, GATED, VEC>), grid, dim3(NTHREADS), 0,
-                       g_stream, c, a, b, b2, M, K, N);
+    TileMap map;
+    const long tiles = make_map(map, M, N, K, BM, BN, GATED ? BN / 2 : BN);
+    if (tiles < 0) return QH_ETOOBIG;
+    hipLaunchKernelGGL((k_gemm<BM, BN, BK, WM, WN, GATED, VEC>), dim3((unsigned)tiles),
+                       dim3(NTHREADS), 0, g_stream, c, a, b, b2, M, K, N, map);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// requires K % 32 == 0 and 16-byte aligned a, b, b2 (checked by the caller)
+// requires K % BK == 0 and 16-byte aligned a, b, b2 (checked by the caller)
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32>
+static int launch_ring(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                       int M, int K, int N) {
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK>;
+    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
+    if (!attr_set) {
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_ring<BM, BN, WM, WN, STAGES, GATED, BK>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS),
+               QH_ELAUNCH);
+        attr_set = true;
+    }
+    TileMap map;
+    const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
+    if (tiles < 0) return QH_ETOOBIG;
+    hipLaunchKernelGGL((k_gemm_ring<BM, BN, WM, WN, STAGES, GATED, BK>), dim3((unsigned)tiles),
+                       dim3(NTHREADS), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// requires K % BK == 0 and 16-byte aligned a, b, b2 (checked by the caller)
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32>
+static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                       int M, int K, int N) {
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK>;
+    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
+    if (!attr_set) {
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS),
+               QH_ELAUNCH);
+        attr_set = true;
+    }
+    TileMap map;
+    const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
+    if (tiles < 0) return QH_ETOOBIG;
+    hipLaunchKernelGGL((k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK>), dim3((unsigned)tiles),
+                       dim3(NTHREADS), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
@@ -952,6 +1535,25 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_T32x128:  return launch_tile<32, 128, 64, 2, 2, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_T16x64:   return launch_tile<16, 128, 64, 1, 4, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_SCALAR64: return launch_tile<64, 64, 64, 2, 2, GATED, false>(c, a, b, b2, M, K, N);
+        case PLAN_R32x64k128s4:  return launch_ring<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_R64x64k64s4:   return launch_ring<64, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R64x64k64s6:   return launch_ring<64, 64, 2, 2, 6, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R64x64k128s3:  return launch_ring<64, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_R64x128k64s4:  return launch_ring<64, 128, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R128x128k64s3: return launch_ring<128, 128, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R128x64k64s3:  return launch_ring<128, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R32x64k64s6:   return launch_ring<32, 64, 2, 2, 6, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_R64x64k32s6:   return launch_ring<64, 64, 2, 2, 6, GATED, 32>(c, a, b, b2, M, K, N);
+        case PLAN_R32x64k32s4:   return launch_ring<32, 64, 2, 2, 4, GATED, 32>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k128s3:  return launch_pipe<32, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k128s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P64x64k128s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P64x64k64s4:   return launch_pipe<64, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P64x128k64s4:  return launch_pipe<64, 128, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P128x128k64s3: return launch_pipe<128, 128, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P128x64k64s3:  return launch_pipe<128, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k64s4:   return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P64x64k64s3:   return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
     }
 }
@@ -975,6 +1577,8 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
     int plan = g_forced_plan ? g_forced_plan : choose_plan(M, K, N, gated, vec);
     if (!vec) plan = PLAN_SCALAR64;   // forced plans still need vector-safe inputs
     if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
+    if (is_ring_plan(plan) && (K % ring_bk(plan)) != 0)           // ring copies whole k stages
+        plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
     return gated ? dispatch<true>(plan, c, a, b, b2, M, K, N)
                  : dispatch<false>(plan, c, a, b, nullptr, M, K, N);
 }

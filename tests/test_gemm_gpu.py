@@ -145,12 +145,16 @@ def test_edge_n(M, N):
     numerics.compare(run_gemm(a, b, M, K, N), a, b, M, K, N)
 
 
-@pytest.mark.parametrize("plan", ["gemv", "mfma128x128", "mfma64x128", "mfma64x64",
-                                  "mfma32x128", "mfma16x64", "mfma64x64-scalar"])
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 384), (3, 520, 200), (77, 1024, 300), (200, 2048, 257)])
+ALL_PLANS = [p for p in abi.PLANS if p != "auto"]
+
+
+@pytest.mark.parametrize("plan", ALL_PLANS)
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 384), (3, 520, 200), (77, 1024, 300), (200, 2048, 257),
+                                   (130, 96, 1000), (64, 32, 64)])
 def test_every_kernel_variant(plan, M, K, N):
     """Force each kernel variant on the same shapes (the gemv plan only
-    applies to M <= 4; larger M falls back to a tiled kernel)."""
+    applies to M <= 4 and ring plans to K % 32 == 0; other cases fall back to
+    a tiled kernel)."""
     a, b = inputs(M, K, N, 4000 + M + K + N)
     abi.force_plan(abi.PLANS[plan])
     try:
@@ -158,6 +162,21 @@ def test_every_kernel_variant(plan, M, K, N):
     finally:
         abi.force_plan(0)
     numerics.compare(c, a, b, M, K, N, rows=numerics.pick_rows(M, 40))
+
+
+@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe")) or p == "gemv"])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96)])
+def test_every_kernel_variant_gated(plan, M, K, N):
+    x = oracle.f32_bf16_normal(M * K, 4100 + M)
+    wg = oracle.bf16_normal(N * K, 4101 + M, 0.02)
+    wu = oracle.bf16_normal(N * K, 4102 + M, 0.02)
+    h = np.full(M * N, np.nan, np.float32)
+    abi.force_plan(abi.PLANS[plan])
+    try:
+        abi.gemm_gate_up_silu(h, x, wg, wu, M, K, N)
+    finally:
+        abi.force_plan(0)
+    numerics.compare_gated(h, x, wg, wu, M, K, N, rows=numerics.pick_rows(M, 24))
 
 
 def test_non_bf16_activations_are_rounded_rne():
