@@ -14,9 +14,11 @@ decode tokens/s of the GEMV set.
 
 Also reported: per-kernel launch times (HIP events on the library stream),
 the roofline fraction of the dominant kernel, prefill GEMM TFLOP/s at
-M = 512 (fused gate/up included), and a CPU baseline: the reference's
-portable scalar GEMM (fpga_bringup/src/src/kernels_scalar.c, compiled from
-its source into oracle/_ref) running the same step on 1 host core.
+M = 512 (fused gate/up included), a CPU baseline: the reference's portable
+scalar GEMM (fpga_bringup/src/src/kernels_scalar.c, compiled from its source
+into oracle/_ref) running the same step on 1 host core, and the full
+device-resident Qwen3-0.6B forward (128-token prefill + 128 greedy decode
+steps) beside the reference forward timed on 1 host core.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -125,6 +127,72 @@ def run_cpu_baseline(budget_s):
     if r.returncode != 0:
         return {"value": None, "error": r.stderr.strip()[-400:]}
     return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+MODEL_SEED = 0x03550040      # random-init weights of the full-forward workload
+
+
+def cpu_model_child():
+    """The reference forward (qwen3.c + kernels_scalar.c + ops_scalar.c,
+    compiled from source into oracle/_ref) on 1 core: a 1-token prefill and
+    one decode step, i.e. two M = 1 forwards."""
+    import numpy as np
+    import oracle
+    from n550_qwen3_bringup_handover_amd import model as M
+    L = oracle.ref("ref_model_scalar")
+    if L is None:
+        print(json.dumps({"value": None, "error": "oracle/_ref/libref_model_scalar.so not built"}))
+        return
+    blob = M.qw3m_random(MODEL_SEED, M.LAYOUT_ROW, threads=16)   # before pinning to one core
+    os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    L.refdrv_generate.restype = ctypes.c_int
+    L.refdrv_generate.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                  ctypes.c_void_p, ctypes.c_void_p]
+    prompt = np.array([1234], np.int32)
+    out = np.zeros(2, np.int32)
+    t0 = time.perf_counter()
+    n = L.refdrv_generate(blob.ctypes.data_as(ctypes.c_void_p), blob.nbytes,
+                          prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), 1, 1, 0,
+                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), None, None)
+    el = time.perf_counter() - t0
+    print(json.dumps({"value": 2 / el if n == 2 else None, "unit": "tok/s", "cores": 1, "kind": "reference",
+                      "sample": f"reference forward qwen3.c + kernels_scalar.c + ops_scalar.c: a 1-token "
+                                f"prefill and 1 decode step (2 forwards at M=1) in {el:.2f} s on 1 core"}))
+
+
+def run_cpu_model():
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-model-child"],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        return {"value": None, "error": r.stderr.strip()[-400:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def model_cfg4(n_prompt=128, n_decode=128):
+    """Full Qwen3-0.6B forward on the device (include/qwen3_hip_model.h):
+    random-init weights, a 128-token random prompt in one prefill chunk, then
+    128 greedy decode steps (one graph replay each)."""
+    import numpy as np
+    from n550_qwen3_bringup_handover_amd import model as M
+    blob = M.qw3m_random(MODEL_SEED, M.LAYOUT_ROW, threads=16)
+    prompt = np.random.default_rng(4).integers(0, V, n_prompt).astype(np.int32)
+    with M.Model(blob, max_seq=n_prompt + n_decode) as m:
+        del blob
+        m.generate(prompt, 8)                       # warm-up: graph capture, caches
+        best = None
+        for _ in range(3):
+            toks = m.generate(prompt, n_decode)
+            pre, dec = m.timing()
+            if best is None or dec < best[1]:
+                best = (pre, dec, toks)
+    pre, dec, toks = best
+    return {"workload": f"Qwen3-0.6B full forward, random-init bf16 weights, batch 1: {n_prompt}-token "
+                        f"prompt (one prefill chunk) + {n_decode} greedy decode steps (graph replay each); "
+                        "best of 3",
+            "prefill_ms": round(pre, 3), "prefill_tok_s": round(n_prompt / pre * 1e3, 1),
+            "decode_ms": round(dec, 3), "decode_tok_s": round(n_decode / dec * 1e3, 2),
+            "ms_per_decode_token": round(dec / n_decode, 4), "first_tokens": [int(t) for t in toks[:8]]}
 
 
 # ---------------------------------------------------------------------------
@@ -361,11 +429,16 @@ def main():
                     help="launch the 113 kernels of a step one by one instead of replaying a graph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 64 MiB copy kernel (traffic-counter calibration)")
+    ap.add_argument("--no-model", action="store_true", help="skip the full-forward (cfg 4) measurement")
     ap.add_argument("--cpu-baseline-child", type=float, default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-model-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.cpu_baseline_child is not None:
         cpu_baseline_child(args.cpu_baseline_child)
+        return 0
+    if args.cpu_model_child:
+        cpu_model_child()
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -374,8 +447,9 @@ def main():
                                    "would shard", "n_gpus": args.gpus}))
         return 2
 
-    # CPU baseline first, before this process touches the GPU
+    # CPU baselines first, before this process touches the GPU
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.cpu_budget)
+    cpu_model = None if (args.no_cpu_baseline or args.no_model) else run_cpu_model()
 
     g = Gpu()
     layers, emb, act = build_decode_model(g)
@@ -424,6 +498,11 @@ def main():
             g.rt.check(g.L.qwen3_hip_copy_dev(ctypes.c_void_p(dst), ctypes.c_void_p(src), nb), "copy")
         g.sync()
 
+    model = None
+    if not args.no_model:
+        model = model_cfg4()
+        model["cpu_baseline"] = cpu_model
+
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
@@ -440,6 +519,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kclasses,
         "prefill_m512": prefill,
+        "model_cfg4": model,
     }
     print(json.dumps(line))
     return 0

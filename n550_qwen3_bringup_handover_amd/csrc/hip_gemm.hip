@@ -162,18 +162,38 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
     }
 }
 
+// Activation prologue of the M = 1 GEMV (decode): the GEMV input is
+//   a = rmsnorm(x + r) * nw       (fpga_bringup/src/src/ops_scalar.c:11-16,
+//                                  residual add ops_scalar.c:53-55)
+// where x is either an fp32 row or, when emb is set, the bf16 embedding row
+// emb[*tok] (qwen3.c:295-298).  Every wave loads the whole row and reduces
+// its sum of squares itself, so no barrier is needed; wave 0 of block 0
+// stores x + r to x_out when x_out is set (the updated residual stream).
+struct GemvPro {
+    const float *x;
+    const uint16_t *emb;
+    const int *tok;
+    int emb_rows;
+    const float *r;
+    const uint16_t *nw;
+    float *x_out;
+    float eps;
+};
+
 // M = 1 fast path (decode).  One wave owns ROWS output rows; lane l owns the
 // 16-byte chunks l, l+64, ..., l+64*(CPL-1) of every row (CPL = chunks per
 // lane, K <= 512*CPL).  All ROWS*CPL weight loads and the 2*CPL activation
 // loads are issued before the first use, so a launch costs one memory round
 // trip; there is no LDS and no barrier.  GATED: rows of Wg and Wu with the
 // same index are both loaded and the epilogue writes silu(gate) * up.
-template <int ROWS, int CPL, bool GATED>
+// PRO: the activation row is produced by the GemvPro prologue instead of
+// being read from a.
+template <int ROWS, int CPL, bool GATED, bool PRO = false>
 __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                    const float *__restrict__ a,
                                                    const uint16_t *__restrict__ b,
                                                    const uint16_t *__restrict__ b2,
-                                                   int K, int N) {
+                                                   int K, int N, GemvPro pro) {
     constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
@@ -199,17 +219,83 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
         }
     }
     float av[CPL][8];
+    if constexpr (!PRO) {
 #pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int ch = lane + WAVE * j;
-        if (ch < nch) {
-            const f32x4 *ap = reinterpret_cast<const f32x4 *>(a + ch * 8);
-            const f32x4 x0 = ap[0], x1 = ap[1];
-            av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
-            av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
-        } else {
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            if (ch < nch) {
+                const f32x4 *ap = reinterpret_cast<const f32x4 *>(a + ch * 8);
+                const f32x4 x0 = ap[0], x1 = ap[1];
+                av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
+                av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
+            } else {
 #pragma unroll
-            for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
+                for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
+            }
+        }
+    } else {
+        const u32x4 *e4 = nullptr;
+        if (pro.emb) {
+            int t = *pro.tok;
+            t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
+            e4 = reinterpret_cast<const u32x4 *>(pro.emb + (size_t)t * K);
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            if (ch < nch) {
+                if (e4) {
+                    const u32x4 w = e4[ch];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        av[j][2 * e] = bf16_lo(w[e]);
+                        av[j][2 * e + 1] = bf16_hi(w[e]);
+                    }
+                } else {
+                    const f32x4 *xp = reinterpret_cast<const f32x4 *>(pro.x + ch * 8);
+                    f32x4 x0 = xp[0], x1 = xp[1];
+                    if (pro.r) {
+                        const f32x4 *rp = reinterpret_cast<const f32x4 *>(pro.r + ch * 8);
+                        x0 += rp[0];
+                        x1 += rp[1];
+                    }
+                    av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
+                    av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += av[j][e] * av[j][e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+        if (pro.x_out && blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+            for (int j = 0; j < CPL; j++) {
+                const int ch = lane + WAVE * j;
+                if (ch < nch) {
+                    f32x4 *op = reinterpret_cast<f32x4 *>(pro.x_out + ch * 8);
+                    op[0] = f32x4{av[j][0], av[j][1], av[j][2], av[j][3]};
+                    op[1] = f32x4{av[j][4], av[j][5], av[j][6], av[j][7]};
+                }
+            }
+        }
+        const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
+        const u32x4 *w4 = reinterpret_cast<const u32x4 *>(pro.nw);
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            if (ch < nch) {
+                const u32x4 w = w4[ch];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    av[j][2 * e] = (av[j][2 * e] * scale) * bf16_lo(w[e]);
+                    av[j][2 * e + 1] = (av[j][2 * e + 1] * scale) * bf16_hi(w[e]);
+                }
+            }
         }
     }
 #pragma unroll
@@ -1343,16 +1429,16 @@ extern "C" int qh_force_plan(int plan_id) {
     return QH_OK;
 }
 
-template <int ROWS, bool GATED>
+template <int ROWS, bool GATED, bool PRO>
 static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
-                             int K, int N, int cpl) {
+                             int K, int N, int cpl, const GemvPro &pro) {
     const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
     // only the (ROWS, CPL) pairs launch_gemv1 can pick: <= 16 loads per lane
 #define QH_GEMV1_CASE(P)                                                                     \
     case P:                                                                                  \
         if constexpr (ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16)                         \
-            hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED>), dim3(grid), dim3(NTHREADS), 0,     \
-                               g_stream, c, a, b, b2, K, N);                                 \
+            hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED, PRO>), dim3(grid), dim3(NTHREADS),   \
+                               0, g_stream, c, a, b, b2, K, N, pro);                         \
         else                                                                                 \
             return QH_EINVAL;                                                                \
         break;
@@ -1374,8 +1460,9 @@ static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const 
 
 // M = 1 with K <= 4096.  Rows per wave: as many as keep >= 2048 waves in the
 // grid (8 per CU) and <= 16 weight loads of 16 B in flight per lane.
-static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
-                        int K, int N, bool gated) {
+template <bool PRO>
+static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                          int K, int N, bool gated, const GemvPro &pro) {
     const int cpl = (K / 8 + WAVE - 1) / WAVE;
     const int per_row = gated ? 2 * cpl : cpl;
     int rows = 8;
@@ -1383,15 +1470,19 @@ static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint1
     while (rows > 1 && rows * per_row > 16) rows /= 2;
     if (gated && rows > 4) rows = 4;
     switch (rows) {
-        case 1: return gated ? launch_gemv1_rows<1, true>(c, a, b, b2, K, N, cpl)
-                             : launch_gemv1_rows<1, false>(c, a, b, b2, K, N, cpl);
-        case 2: return gated ? launch_gemv1_rows<2, true>(c, a, b, b2, K, N, cpl)
-                             : launch_gemv1_rows<2, false>(c, a, b, b2, K, N, cpl);
-        case 4: return gated ? launch_gemv1_rows<4, true>(c, a, b, b2, K, N, cpl)
-                             : launch_gemv1_rows<4, false>(c, a, b, b2, K, N, cpl);
-        case 8: return launch_gemv1_rows<8, false>(c, a, b, b2, K, N, cpl);
+        case 1: return gated ? launch_gemv1_rows<1, true, PRO>(c, a, b, b2, K, N, cpl, pro)
+                             : launch_gemv1_rows<1, false, PRO>(c, a, b, b2, K, N, cpl, pro);
+        case 2: return gated ? launch_gemv1_rows<2, true, PRO>(c, a, b, b2, K, N, cpl, pro)
+                             : launch_gemv1_rows<2, false, PRO>(c, a, b, b2, K, N, cpl, pro);
+        case 4: return gated ? launch_gemv1_rows<4, true, PRO>(c, a, b, b2, K, N, cpl, pro)
+                             : launch_gemv1_rows<4, false, PRO>(c, a, b, b2, K, N, cpl, pro);
+        case 8: return launch_gemv1_rows<8, false, PRO>(c, a, b, b2, K, N, cpl, pro);
         default: return QH_EINVAL;
     }
+}
+static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                        int K, int N, bool gated) {
+    return launch_gemv1_t<false>(c, a, b, b2, K, N, gated, GemvPro{});
 }
 
 template <int MR>
@@ -1672,4 +1763,64 @@ extern "C" int qh_argmax(int *out, const float *v, int n) {
     hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(WAVE), 0, g_stream, out, g_am_v, g_am_i, blocks, v);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
+}
+
+// Greedy step bookkeeping on the device (so a decode step can be replayed as
+// a graph with no host round trip): token = argmax, out[*step] = token when
+// *step < cap, *step += 1, *pos += adv.
+__global__ __launch_bounds__(WAVE) void k_argmax_step(int *__restrict__ tok, int *__restrict__ out,
+                                                     int *__restrict__ step, int cap,
+                                                     int *__restrict__ pos, int adv,
+                                                     const float *__restrict__ pv,
+                                                     const int *__restrict__ pi, int np,
+                                                     const float *__restrict__ v) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    for (int i = threadIdx.x; i < np; i += WAVE) am_merge(bv, bi, pv[i], pi[i]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        float ov = __shfl_xor(bv, m);
+        int oi = __shfl_xor(bi, m);
+        am_merge(bv, bi, ov, oi);
+    }
+    if (threadIdx.x == 0) {
+        const int t = (bi == 0x7FFFFFFF || v[0] != v[0]) ? 0 : bi;
+        tok[0] = t;
+        const int s = step[0];
+        if (s >= 0 && s < cap) out[s] = t;
+        step[0] = s + 1;
+        pos[0] += adv;
+    }
+}
+
+extern "C" int qh_argmax_step(int *tok, int *out, int *step, int cap, int *pos, int adv,
+                              const float *v, int n) {
+    if (!g_inited) return QH_ESTATE;
+    if (n <= 0 || !tok || !out || !step || !pos || !v || cap < 0) return QH_EINVAL;
+    int blocks = (n + NTHREADS * 4 - 1) / (NTHREADS * 4);
+    if (blocks > AM_BLOCKS) blocks = AM_BLOCKS;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(k_argmax_partial, dim3(blocks), dim3(NTHREADS), 0, g_stream, g_am_v, g_am_i, v, n);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    hipLaunchKernelGGL(k_argmax_step, dim3(1), dim3(WAVE), 0, g_stream, tok, out, step, cap, pos, adv,
+                       g_am_v, g_am_i, blocks, v);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// M = 1 GEMV whose activation row comes from the rmsnorm prologue (GemvPro).
+// Requires K % 8 == 0, K <= 4096 and 16-byte aligned pointers.
+extern "C" int qh_gemv_pro(float *c, const qh_gemv_pro_t *p, const uint16_t *b, const uint16_t *b2,
+                           int K, int N, int gated) {
+    if (!g_inited) return QH_ESTATE;
+    if (!c || !p || !b || (gated && !b2) || !p->nw || (!p->x && !(p->emb && p->tok))) return QH_EINVAL;
+    if (K <= 0 || N <= 0 || K % 8 || K > 8 * WAVE * 8) return QH_EINVAL;
+    if (p->emb && p->emb_rows <= 0) return QH_EINVAL;
+    if (!aligned16(c) || !aligned16(b) || (gated && !aligned16(b2)) || !aligned16(p->nw) ||
+        (p->x && !aligned16(p->x)) || (p->r && !aligned16(p->r)) ||
+        (p->x_out && !aligned16(p->x_out)) || (p->emb && !aligned16(p->emb)))
+        return QH_EINVAL;
+    const GemvPro pro{p->emb ? nullptr : p->x, p->emb, p->tok, p->emb_rows,
+                      p->emb ? nullptr : p->r, p->nw, p->x_out, p->eps};
+    return launch_gemv1_t<true>(c, nullptr, b, b2, K, N, gated != 0, pro);
 }

@@ -1,0 +1,339 @@
+// CDNA4 (gfx950) kernels of the device-resident Qwen3-0.6B forward besides
+// the projection GEMMs: row-wise residual + RMSNorm (with the embedding
+// gather folded in) and the fused attention step.  The arithmetic follows the
+// reference's scalar ops (fpga_bringup/src/src/ops_scalar.c) and forward
+// (fpga_bringup/src/src/qwen3.c:276-576); sums are reduced in parallel, so
+// results agree to rounding, not bit for bit.
+//
+// Device layouts (all fp32 unless noted):
+//   activations   [nt][dim] row-major (the GEMM A/C layout)
+//   qkv           [nt][4096] = q (16 heads x 128) | k (8 x 128) | v (8 x 128)
+//   K cache       [layer][kv_head][128/4][max_seq][4]   (d-chunk major: one
+//                 thread per position reads 16 contiguous bytes per chunk, so
+//                 a wave's score loads are one 1 KB contiguous run)
+//   V cache       [layer][kv_head][max_seq][128]        (as qwen3.h:62-76)
+//   rope tables   [max_seq][64] cos and sin, built on the host with the
+//                 reference formula (ops_scalar.c:21-35)
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hip_shim.h"
+#include "model_shim.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+#define WAVE 64
+#define NTH 256
+#define HD 128                 // head_dim
+#define NKV 8                  // kv heads
+#define GRP 2                  // q heads per kv head (qwen3_config.h:22)
+#define QKV_LD 4096            // q 2048 | k 1024 | v 1024
+#define KOFF 2048
+#define VOFF 3072
+#define KST 132                // LDS row stride of chunk k rows (floats)
+
+__device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// rows: x[row] = emb[tok[row]] (bf16 -> fp32)   when emb is set, else
+//       x[row] = x[row] + r[row]                 when r is set;
+//       xb[row] = rmsnorm(x[row]) * nw           (ops_scalar.c:11-16)
+// grid = nt blocks of 256 threads; K % 4 == 0, K <= 4096.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTH) void k_rows_norm(float *__restrict__ x, const float *__restrict__ r,
+                                                   const uint16_t *__restrict__ emb,
+                                                   const int *__restrict__ tok, int emb_rows,
+                                                   const uint16_t *__restrict__ nw,
+                                                   float *__restrict__ xb, int K, float eps) {
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const int n4 = K >> 2;
+    f32x4 v[4];
+    float ss = 0.0f;
+    int t = 0;
+    if (emb) {
+        t = tok[row];
+        t = t < 0 ? 0 : (t >= emb_rows ? emb_rows - 1 : t);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c = tid + NTH * j;
+        v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (c < n4) {
+            if (emb) {
+                const uint16_t *e = emb + (size_t)t * K + c * 4;
+                v[j] = f32x4{bf16f(e[0]), bf16f(e[1]), bf16f(e[2]), bf16f(e[3])};
+            } else {
+                v[j] = reinterpret_cast<const f32x4 *>(x + (size_t)row * K)[c];
+                if (r) v[j] += reinterpret_cast<const f32x4 *>(r + (size_t)row * K)[c];
+            }
+            if (emb || r) reinterpret_cast<f32x4 *>(x + (size_t)row * K)[c] = v[j];
+            ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+        }
+    }
+    __shared__ float red[NTH / WAVE];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = red[0] + red[1] + red[2] + red[3];
+    const float scale = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int c = tid + NTH * j;
+        if (c < n4) {
+            const uint16_t *w = nw + c * 4;
+            f32x4 o;
+            o.x = (v[j].x * scale) * bf16f(w[0]);
+            o.y = (v[j].y * scale) * bf16f(w[1]);
+            o.z = (v[j].z * scale) * bf16f(w[2]);
+            o.w = (v[j].w * scale) * bf16f(w[3]);
+            reinterpret_cast<f32x4 *>(xb + (size_t)row * K)[c] = o;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention for a chunk of nt tokens at positions pos0 .. pos0+nt-1, where
+// pos0 = *pos_d (read on the device so a decode step can be graph-replayed).
+// Block (i, g): token i, kv head g and its GRP query heads (qwen3.c:377-436).
+//   1. q heads of token i and the k rows of kv head g for chunk tokens
+//      0..i get QK-norm (qwen3.c:298-305) then RoPE (ops_scalar.c:21-35),
+//      into LDS; the block writes the cache entry of its own token.
+//   2. scores s[h][t] = q_h . k_t / sqrt(128) for t <= pos0+i (causal):
+//      t < pos0 from the cache, t >= pos0 from the chunk rows in LDS.
+//   3. softmax over t (ops_scalar.c:37-44), normalised as there.
+//   4. out_h = sum_t p[h][t] v_t (v of chunk tokens read from qkv).
+// No block reads a cache entry that another block of the same launch writes.
+// grid = (nt, NKV), 256 threads, dynamic LDS = attn_lds_bytes(nt, max_seq).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv,
+                                                   float *__restrict__ out,
+                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   const uint16_t *__restrict__ qn,
+                                                   const uint16_t *__restrict__ kn,
+                                                   const float *__restrict__ rcos,
+                                                   const float *__restrict__ rsin,
+                                                   const int *__restrict__ pos_d, int nt,
+                                                   int max_seq, float eps, float scale) {
+    const int i = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int pos0 = *pos_d;
+    const int pos = pos0 + i;
+    if (pos0 < 0 || pos >= max_seq) return;   // uniform per block, before any barrier
+    const int ctx = pos + 1;
+
+    extern __shared__ float sm[];
+    float *sq = sm;                            // [GRP][HD]
+    float *red = sq + GRP * HD;                // [4][GRP][HD] partial outputs
+    float *sred = red + 4 * GRP * HD;          // [2][4] block reductions
+    float *kch = sred + 8;                     // [nt][KST]
+    float *p = kch + (size_t)nt * KST;         // [GRP][max_seq]
+
+    // 1. QK-norm + RoPE of GRP q rows and i+1 chunk k rows
+    for (int rr = wave; rr < GRP + i + 1; rr += NTH / WAVE) {
+        const float *src;
+        const uint16_t *w;
+        float *dst;
+        int tp;
+        if (rr < GRP) {
+            src = qkv + (size_t)i * QKV_LD + (size_t)(g * GRP + rr) * HD;
+            w = qn;
+            dst = sq + rr * HD;
+            tp = pos;
+        } else {
+            const int t = rr - GRP;
+            src = qkv + (size_t)t * QKV_LD + KOFF + (size_t)g * HD;
+            w = kn;
+            dst = kch + (size_t)t * KST;
+            tp = pos0 + t;
+        }
+        const float x0 = src[lane], x1 = src[lane + 64];
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+        const float y0 = (x0 * sc) * bf16f(w[lane]);
+        const float y1 = (x1 * sc) * bf16f(w[lane + 64]);
+        const float c = rcos[(size_t)tp * (HD / 2) + lane], s = rsin[(size_t)tp * (HD / 2) + lane];
+        // rotate_half pairing (i, i + 64), as ops_scalar.c:29-33
+        dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, s));
+        dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, s));
+    }
+    __syncthreads();
+    if (tid < HD) {                            // this block's own cache entry
+        const float kv = kch[(size_t)i * KST + tid];
+        kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = kv;
+        vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[(size_t)i * QKV_LD + VOFF + (size_t)g * HD + tid];
+    }
+
+    // 2. scores
+    for (int t = tid; t < ctx; t += NTH) {
+        float s0 = 0.0f, s1 = 0.0f;
+        if (t < pos0) {
+            const f32x4 *kp = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq + t;
+            f32x4 kv[HD / 4];
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kp[(size_t)d4 * max_seq];
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
+                const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
+                s0 = fmaf(q0.x, kv[d4].x, s0); s0 = fmaf(q0.y, kv[d4].y, s0);
+                s0 = fmaf(q0.z, kv[d4].z, s0); s0 = fmaf(q0.w, kv[d4].w, s0);
+                s1 = fmaf(q1.x, kv[d4].x, s1); s1 = fmaf(q1.y, kv[d4].y, s1);
+                s1 = fmaf(q1.z, kv[d4].z, s1); s1 = fmaf(q1.w, kv[d4].w, s1);
+            }
+        } else {
+            const f32x4 *kr = reinterpret_cast<const f32x4 *>(kch + (size_t)(t - pos0) * KST);
+#pragma unroll 8
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const f32x4 kv = kr[d4];
+                const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
+                const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
+                s0 = fmaf(q0.x, kv.x, s0); s0 = fmaf(q0.y, kv.y, s0);
+                s0 = fmaf(q0.z, kv.z, s0); s0 = fmaf(q0.w, kv.w, s0);
+                s1 = fmaf(q1.x, kv.x, s1); s1 = fmaf(q1.y, kv.y, s1);
+                s1 = fmaf(q1.z, kv.z, s1); s1 = fmaf(q1.w, kv.w, s1);
+            }
+        }
+        p[t] = s0 * scale;
+        p[max_seq + t] = s1 * scale;
+    }
+    __syncthreads();
+
+    // 3. softmax per query head
+    float m0 = -INFINITY, m1 = -INFINITY;
+    for (int t = tid; t < ctx; t += NTH) {
+        m0 = fmaxf(m0, p[t]);
+        m1 = fmaxf(m1, p[max_seq + t]);
+    }
+    m0 = wave_max(m0);
+    m1 = wave_max(m1);
+    if (lane == 0) { sred[wave] = m0; sred[4 + wave] = m1; }
+    __syncthreads();
+    m0 = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+    m1 = fmaxf(fmaxf(sred[4], sred[5]), fmaxf(sred[6], sred[7]));
+    __syncthreads();
+    float e0 = 0.0f, e1 = 0.0f;
+    for (int t = tid; t < ctx; t += NTH) {
+        const float a0 = expf(p[t] - m0), a1 = expf(p[max_seq + t] - m1);
+        p[t] = a0;
+        p[max_seq + t] = a1;
+        e0 += a0;
+        e1 += a1;
+    }
+    e0 = wave_sum(e0);
+    e1 = wave_sum(e1);
+    if (lane == 0) { sred[wave] = e0; sred[4 + wave] = e1; }
+    __syncthreads();
+    e0 = (sred[0] + sred[1]) + (sred[2] + sred[3]);
+    e1 = (sred[4] + sred[5]) + (sred[6] + sred[7]);
+    for (int t = tid; t < ctx; t += NTH) {
+        p[t] = p[t] / e0;
+        p[max_seq + t] = p[max_seq + t] / e1;
+    }
+    __syncthreads();
+
+    // 4. out_h[d] = sum_t p[h][t] v_t[d]: wave w takes t = w, w+4, ...; lane
+    //    l owns d = 2l, 2l+1 of both heads
+    f32x2 o0 = {0.f, 0.f}, o1 = {0.f, 0.f};
+    const f32x2 *vcache = reinterpret_cast<const f32x2 *>(vc + (size_t)g * max_seq * HD) + lane;
+    const f32x2 *vchunk = reinterpret_cast<const f32x2 *>(qkv + VOFF + (size_t)g * HD) + lane;
+    int t = wave;
+    for (; t + 4 * 7 < ctx; t += 4 * 8) {      // 8 loads in flight per lane
+        f32x2 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int tt = t + 4 * u;
+            v[u] = tt < pos0 ? vcache[(size_t)tt * (HD / 2)] : vchunk[(size_t)(tt - pos0) * (QKV_LD / 2)];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const float p0 = p[t + 4 * u], p1 = p[max_seq + t + 4 * u];
+            o0.x = __fadd_rn(o0.x, __fmul_rn(p0, v[u].x));
+            o0.y = __fadd_rn(o0.y, __fmul_rn(p0, v[u].y));
+            o1.x = __fadd_rn(o1.x, __fmul_rn(p1, v[u].x));
+            o1.y = __fadd_rn(o1.y, __fmul_rn(p1, v[u].y));
+        }
+    }
+    for (; t < ctx; t += 4) {
+        const f32x2 v = t < pos0 ? vcache[(size_t)t * (HD / 2)] : vchunk[(size_t)(t - pos0) * (QKV_LD / 2)];
+        const float p0 = p[t], p1 = p[max_seq + t];
+        o0.x = __fadd_rn(o0.x, __fmul_rn(p0, v.x));
+        o0.y = __fadd_rn(o0.y, __fmul_rn(p0, v.y));
+        o1.x = __fadd_rn(o1.x, __fmul_rn(p1, v.x));
+        o1.y = __fadd_rn(o1.y, __fmul_rn(p1, v.y));
+    }
+    red[(wave * GRP + 0) * HD + 2 * lane] = o0.x;
+    red[(wave * GRP + 0) * HD + 2 * lane + 1] = o0.y;
+    red[(wave * GRP + 1) * HD + 2 * lane] = o1.x;
+    red[(wave * GRP + 1) * HD + 2 * lane + 1] = o1.y;
+    __syncthreads();
+    {
+        const int h = tid >> 7, d = tid & (HD - 1);   // 256 threads = GRP x HD
+        const float s = (red[(0 * GRP + h) * HD + d] + red[(1 * GRP + h) * HD + d]) +
+                        (red[(2 * GRP + h) * HD + d] + red[(3 * GRP + h) * HD + d]);
+        out[(size_t)i * (NKV * GRP * HD) + (size_t)(g * GRP + h) * HD + d] = s;
+    }
+}
+
+__global__ void k_set_i32(int *p, int v) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) p[0] = v;
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+static inline hipStream_t stream() { return (hipStream_t)qh_stream(); }
+
+extern "C" size_t qm_attention_lds_bytes(int nt, int max_seq) {
+    return sizeof(float) * ((size_t)GRP * HD + 4 * GRP * HD + 8 + (size_t)nt * KST + (size_t)GRP * max_seq);
+}
+
+extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const int *tok, int emb_rows,
+                            const uint16_t *nw, float *xb, int nt, int K, float eps) {
+    if (!stream()) return QH_ESTATE;
+    if (!x || !nw || !xb || nt <= 0 || K <= 0 || K % 4 || K > 4 * 4 * NTH) return QH_EINVAL;
+    if (emb && (!tok || emb_rows <= 0)) return QH_EINVAL;
+    hipLaunchKernelGGL(k_rows_norm, dim3(nt), dim3(NTH), 0, stream(), x, emb ? nullptr : r, emb, tok,
+                       emb_rows, nw, xb, K, eps);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" int qm_attention(const float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
+                            const uint16_t *kn, const float *rcos, const float *rsin, const int *pos_d,
+                            int nt, int max_seq, float eps) {
+    if (!stream()) return QH_ESTATE;
+    if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
+    if (nt <= 0 || max_seq <= 0 || nt > QM_MAX_CHUNK || max_seq > QM_MAX_SEQ) return QH_EINVAL;
+    const size_t lds = qm_attention_lds_bytes(nt, max_seq);
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)qm_attention_lds_bytes(QM_MAX_CHUNK, QM_MAX_SEQ)) != hipSuccess)
+            return QH_ELAUNCH;
+        attr_set = true;
+    }
+    // 1 / sqrt(head_dim), the constant of qwen3.c:311
+    const float scale = 0.08838834764831845f;
+    hipLaunchKernelGGL(k_attention, dim3(nt, NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn, rcos,
+                       rsin, pos_d, nt, max_seq, eps, scale);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" int qm_set_i32(int *p, int v) {
+    if (!stream()) return QH_ESTATE;
+    if (!p) return QH_EINVAL;
+    hipLaunchKernelGGL(k_set_i32, dim3(1), dim3(WAVE), 0, stream(), p, v);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}

@@ -56,6 +56,29 @@ int qh_tile_to_row(uint16_t *dst_d, const uint16_t *src_d, int N, int K,
                    int tile_n, int tile_k);
 /* first index of the maximum of v[0..n) (ties -> lowest index) */
 int qh_argmax(int *out_d, const float *v_d, int n);
+/* greedy-step bookkeeping on the device: *tok = argmax(v), out[*step] = *tok
+ * when *step < cap, then *step += 1 and *pos += adv */
+int qh_argmax_step(int *tok_d, int *out_d, int *step_d, int cap, int *pos_d, int adv,
+                   const float *v_d, int n);
+
+/* M = 1 GEMV with an rmsnorm prologue: the activation row is
+ *   a = rmsnorm(x + r) * nw     (x fp32, or the bf16 row emb[*tok] when emb
+ *                                is set, in which case r is ignored)
+ * and, when x_out is set, x + r is stored there (one writer).  c[N] =
+ * a . B^T, or silu(a . Wg^T) * (a . Wu^T) when gated (b2 = Wu).  K % 8 == 0,
+ * K <= 4096, 16-byte aligned pointers. */
+typedef struct {
+    const float *x;
+    const uint16_t *emb;
+    const int *tok;
+    int emb_rows;
+    const float *r;
+    const uint16_t *nw;
+    float *x_out;
+    float eps;
+} qh_gemv_pro_t;
+int qh_gemv_pro(float *c_d, const qh_gemv_pro_t *pro, const uint16_t *b_d, const uint16_t *b2_d,
+                int K, int N, int gated);
 
 /* device copy by a plain 16-byte-vector kernel (bytes % 16 == 0, 16-byte
  * aligned pointers): the known-traffic reference for HBM counter calibration */

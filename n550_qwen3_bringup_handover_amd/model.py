@@ -1,0 +1,132 @@
+"""Python mirror of the device-resident forward and the QW3M blob
+(include/qwen3_hip_model.h), over ctypes.
+
+`Model` follows the reference runtime's entry points
+(fpga_bringup/src/src/qwen3.h:203-241): open a blob (qwen3_init), run a
+batched forward (qwen3_forward_batch), read logits / argmax, and greedy
+generation as the reference driver does (fpga_bringup/src/src/main.c:227-256).
+All compute runs in libqwen3_hip.so on the GPU; there is no CPU path.
+"""
+import ctypes
+
+import numpy as np
+
+from . import runtime
+from .runtime import F32P, I32P, VP
+
+LAYOUT_ROW = 0
+LAYOUT_TILE = 1
+VOCAB = 151936
+EOS = (151645, 151643)
+
+# QWEN3_ERR_* of fpga_bringup/src/src/qwen3.h:188-200
+QW3M_ERRORS = {-1: "bad magic", -2: "version", -3: "dtype", -4: "shape", -5: "size",
+               -6: "out of memory", -7: "layout"}
+
+
+def qw3m_size(layout=LAYOUT_ROW):
+    return int(runtime.lib().qwen3_hip_qw3m_size(layout))
+
+
+def qw3m_random(seed, layout=LAYOUT_ROW, threads=8):
+    """A complete random-init Qwen3-0.6B blob as a uint8 array (~1.19 GB)."""
+    n = qw3m_size(layout)
+    if n == 0:
+        raise ValueError(f"unknown layout {layout}")
+    blob = np.empty(n, dtype=np.uint8)
+    runtime.check(runtime.lib().qwen3_hip_qw3m_write_random(
+        blob.ctypes.data_as(VP), n, ctypes.c_uint64(seed), layout, threads), "qw3m_write_random")
+    return blob
+
+
+def qw3m_check(blob):
+    """0, or the reference's QWEN3_ERR_* code for a blob that does not parse."""
+    return int(runtime.lib().qwen3_hip_qw3m_check(blob.ctypes.data_as(VP), blob.nbytes))
+
+
+class Qwen3ModelError(RuntimeError):
+    pass
+
+
+def _rc(rc, what):
+    if rc < 0:
+        raise Qwen3ModelError(f"{what}: blob rejected ({QW3M_ERRORS.get(rc, rc)}, code {rc})")
+    runtime.check(rc, what)
+
+
+def _i32(x):
+    a = np.ascontiguousarray(np.asarray(x, dtype=np.int32))
+    return a
+
+
+class Model:
+    """A Qwen3-0.6B model resident on the GPU."""
+
+    def __init__(self, blob, max_seq=0):
+        runtime.init()
+        L = runtime.lib()
+        h = VP()
+        _rc(L.qwen3_hip_model_open(ctypes.byref(h), blob.ctypes.data_as(VP), blob.nbytes, max_seq),
+            "qwen3_hip_model_open")
+        self._h = h
+        self.max_seq = int(L.qwen3_hip_model_max_seq(h))
+
+    def close(self):
+        if self._h:
+            runtime.lib().qwen3_hip_model_close(self._h)
+            self._h = VP()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def forward(self, tokens, pos0):
+        t = _i32(tokens)
+        _rc(runtime.lib().qwen3_hip_model_forward(self._h, t.ctypes.data_as(I32P), t.size, pos0),
+            "qwen3_hip_model_forward")
+
+    def logits(self):
+        out = np.empty(VOCAB, dtype=np.float32)
+        _rc(runtime.lib().qwen3_hip_model_logits(self._h, out.ctypes.data_as(F32P)), "qwen3_hip_model_logits")
+        return out
+
+    def argmax(self):
+        t = ctypes.c_int(-1)
+        _rc(runtime.lib().qwen3_hip_model_argmax(self._h, ctypes.byref(t)), "qwen3_hip_model_argmax")
+        return t.value
+
+    def set_graph(self, on):
+        _rc(runtime.lib().qwen3_hip_model_set_graph(self._h, 1 if on else 0), "qwen3_hip_model_set_graph")
+
+    def generate(self, prompt, n_decode, stop_at_eos=False):
+        p = _i32(prompt)
+        out = np.zeros(n_decode + 1, dtype=np.int32)
+        n = ctypes.c_int(0)
+        _rc(runtime.lib().qwen3_hip_model_generate(self._h, p.ctypes.data_as(I32P), p.size, n_decode,
+                                                   1 if stop_at_eos else 0, out.ctypes.data_as(I32P),
+                                                   ctypes.byref(n)), "qwen3_hip_model_generate")
+        return out[:n.value]
+
+    def forward_dump(self, tokens, pos0=0):
+        """forward() with every materialised intermediate captured:
+        {(layer, name): float32 array} (reference dump names)."""
+        got = {}
+
+        def cb(_ctx, layer, name, data, n):
+            got[(layer, name.decode())] = np.ctypeslib.as_array(data, shape=(n,)).copy()
+
+        fn = runtime.DUMP_FN(cb)
+        L = runtime.lib()
+        _rc(L.qwen3_hip_model_set_dump(self._h, ctypes.cast(fn, VP), None), "qwen3_hip_model_set_dump")
+        try:
+            self.forward(tokens, pos0)
+        finally:
+            L.qwen3_hip_model_set_dump(self._h, None, None)
+        return got
+
+    def timing(self):
+        a, b = ctypes.c_double(), ctypes.c_double()
+        _rc(runtime.lib().qwen3_hip_model_timing(self._h, ctypes.byref(a), ctypes.byref(b)), "qwen3_hip_model_timing")
+        return a.value, b.value

@@ -1,5 +1,5 @@
-"""Loader for libqwen3_hip.so — the MI355X GEMM plug-in (C ABI in
-include/qwen3_hip.h).
+"""Loader for libqwen3_hip.so — the MI355X GEMM plug-in and device-resident
+forward (C ABI in include/qwen3_hip.h and include/qwen3_hip_model.h).
 
 The library is built in-tree (`build()`, or `make -C <pkg>/csrc`) and loaded
 from this directory only.  There is no CPU fallback: if the library is
@@ -13,6 +13,8 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_PATH = os.path.join(PKG_DIR, "libqwen3_hip.so")
 HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "qwen3_hip.h")
+MODEL_HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "qwen3_hip_model.h")
+HEADERS = (HEADER, MODEL_HEADER)
 
 F32P = ctypes.POINTER(ctypes.c_float)
 U16P = ctypes.POINTER(ctypes.c_uint16)
@@ -71,15 +73,35 @@ _PROTOS = {
     "qwen3_hip_plan": (ctypes.c_char_p, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_force_plan": (ctypes.c_int, [ctypes.c_int]),
     "qwen3_hip_device_name": (ctypes.c_char_p, []),
+    # include/qwen3_hip_model.h
+    "qwen3_hip_qw3m_size": (ctypes.c_size_t, [ctypes.c_int]),
+    "qwen3_hip_qw3m_write_random": (ctypes.c_int, [VP, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_qw3m_check": (ctypes.c_int, [VP, ctypes.c_size_t]),
+    "qwen3_hip_model_open": (ctypes.c_int, [ctypes.POINTER(VP), VP, ctypes.c_size_t, ctypes.c_int]),
+    "qwen3_hip_model_close": (None, [VP]),
+    "qwen3_hip_model_max_seq": (ctypes.c_int, [VP]),
+    "qwen3_hip_model_forward": (ctypes.c_int, [VP, I32P, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_model_logits": (ctypes.c_int, [VP, F32P]),
+    "qwen3_hip_model_argmax": (ctypes.c_int, [VP, I32P]),
+    "qwen3_hip_model_generate": (ctypes.c_int, [VP, I32P, ctypes.c_int, ctypes.c_int, ctypes.c_int, I32P, I32P]),
+    "qwen3_hip_model_timing": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
+    "qwen3_hip_model_set_graph": (ctypes.c_int, [VP, ctypes.c_int]),
+    "qwen3_hip_model_set_dump": (ctypes.c_int, [VP, VP, VP]),
 }
+
+# qwen3_hip_dump_fn
+DUMP_FN = ctypes.CFUNCTYPE(None, VP, ctypes.c_int, ctypes.c_char_p, F32P, ctypes.c_size_t)
 
 
 def header_symbols():
-    """Function names declared in include/qwen3_hip.h."""
+    """Function names declared in include/qwen3_hip.h and qwen3_hip_model.h."""
     import re
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(qwen3_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", " ", text, flags=re.S)
+        names.update(re.findall(r"\b(qwen3_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def lib():

@@ -16,6 +16,52 @@ size_t refdrv_scratch_bytes(void) { return qwen3_scratch_bytes(); }
 int refdrv_max_seq(void) { return QWEN3_MAX_SEQ; }
 int refdrv_max_batch(void) { return QWEN3_MAX_BATCH; }
 
+/* ---- intermediate dumps (qwen3_set_dump, qwen3.h:166-178) ---------------- */
+typedef struct {
+    int layer;
+    char name[44];
+    size_t off, n;
+} refdrv_rec_t;
+
+typedef struct {
+    float *buf;
+    size_t cap, used;
+    refdrv_rec_t *recs;
+    int max_recs, n_recs, overflow;
+} capture_t;
+
+static void capture_cb(void *ctx, int layer, const char *name, const float *data, size_t n) {
+    capture_t *c = (capture_t *)ctx;
+    if (c->n_recs >= c->max_recs || c->used + n > c->cap) { c->overflow = 1; return; }
+    refdrv_rec_t *r = &c->recs[c->n_recs++];
+    r->layer = layer;
+    strncpy(r->name, name, sizeof r->name - 1);
+    r->name[sizeof r->name - 1] = 0;
+    r->off = c->used;
+    r->n = n;
+    memcpy(c->buf + c->used, data, n * sizeof(float));
+    c->used += n;
+}
+
+/* One qwen3_forward_batch of tokens[0..n_token) at position 0 with every
+ * EMIT of qwen3.c captured into buf (records in recs).  Returns the number
+ * of records, -100 if buf or recs were too small, or a QWEN3_ERR_* code. */
+int refdrv_forward_dump(const void *blob, size_t blob_size, const int *tokens, int n_token,
+                        float *buf, size_t cap, refdrv_rec_t *recs, int max_recs) {
+    static qwen3_t m;
+    void *scratch = malloc(qwen3_scratch_bytes());
+    if (!scratch) return QWEN3_ERR_OOM;
+    int rc = qwen3_init(&m, blob, blob_size, scratch, qwen3_scratch_bytes());
+    if (rc != QWEN3_OK) { free(scratch); return rc; }
+    if (n_token < 1 || n_token > QWEN3_MAX_BATCH) { free(scratch); return QWEN3_ERR_SHAPE; }
+    capture_t c = {buf, cap, 0, recs, max_recs, 0, 0};
+    qwen3_set_dump(&m, capture_cb, &c);
+    qwen3_forward_batch(&m, tokens, n_token, 0);
+    qwen3_set_dump(&m, NULL, NULL);
+    free(scratch);
+    return c.overflow ? -100 : c.n_recs;
+}
+
 /* logit gap between the best and the runner-up, for divergence reports */
 static float top2_margin(const float *v, int n) {
     float b1 = v[0], b2 = -3.0e38f;
