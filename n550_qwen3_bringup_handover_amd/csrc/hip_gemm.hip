@@ -240,6 +240,14 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
             t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
             e4 = reinterpret_cast<const u32x4 *>(pro.emb + (size_t)t * K);
         }
+        // norm weights are independent of the reduction: load them first
+        const u32x4 *w4 = reinterpret_cast<const u32x4 *>(pro.nw);
+        u32x4 nwv[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            nwv[j] = ch < nch ? w4[ch] : u32x4{0u, 0u, 0u, 0u};
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
@@ -284,12 +292,11 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
             }
         }
         const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
-        const u32x4 *w4 = reinterpret_cast<const u32x4 *>(pro.nw);
 #pragma unroll
         for (int j = 0; j < CPL; j++) {
             const int ch = lane + WAVE * j;
             if (ch < nch) {
-                const u32x4 w = w4[ch];
+                const u32x4 w = nwv[j];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
                     av[j][2 * e] = (av[j][2 * e] * scale) * bf16_lo(w[e]);

@@ -14,6 +14,8 @@
 //   V cache       [layer][kv_head][max_seq][128]        (as qwen3.h:62-76)
 //   rope tables   [max_seq][64] cos and sin, built on the host with the
 //                 reference formula (ops_scalar.c:21-35)
+// The chunk attention keeps 2 x max_seq scores in LDS (up to 69 KB at
+// QM_MAX_SEQ), above the default 64 KB limit that it raises once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -32,7 +34,6 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 #define QKV_LD 4096            // q 2048 | k 1024 | v 1024
 #define KOFF 2048
 #define VOFF 3072
-#define KST 132                // LDS row stride of chunk k rows (floats)
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -105,28 +106,65 @@ __global__ __launch_bounds__(NTH) void k_rows_norm(float *__restrict__ x, const 
 }
 
 // ---------------------------------------------------------------------------
-// Attention for a chunk of nt tokens at positions pos0 .. pos0+nt-1, where
-// pos0 = *pos_d (read on the device so a decode step can be graph-replayed).
-// Block (i, g): token i, kv head g and its GRP query heads (qwen3.c:377-436).
-//   1. q heads of token i and the k rows of kv head g for chunk tokens
-//      0..i get QK-norm (qwen3.c:298-305) then RoPE (ops_scalar.c:21-35),
-//      into LDS; the block writes the cache entry of its own token.
-//   2. scores s[h][t] = q_h . k_t / sqrt(128) for t <= pos0+i (causal):
-//      t < pos0 from the cache, t >= pos0 from the chunk rows in LDS.
-//   3. softmax over t (ops_scalar.c:37-44), normalised as there.
-//   4. out_h = sum_t p[h][t] v_t (v of chunk tokens read from qkv).
-// No block reads a cache entry that another block of the same launch writes.
-// grid = (nt, NKV), 256 threads, dynamic LDS = attn_lds_bytes(nt, max_seq).
+// Chunk of nt tokens at positions pos0 .. pos0+nt-1 (pos0 = *pos_d), step 1:
+// QK-norm (qwen3.c:298-305) then RoPE (ops_scalar.c:21-35) of every q and k
+// head; q is written back in place, k and v go to the KV cache entry of
+// their position (qwen3.c:497-512).  grid = (nt, 6): block (i, b), wave w
+// handles row 4b + w of token i (rows 0-15 q heads, 16-23 k heads + v copy).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTH) void k_qk_rope_cache(float *__restrict__ qkv, float *__restrict__ kc,
+                                                       float *__restrict__ vc,
+                                                       const uint16_t *__restrict__ qn,
+                                                       const uint16_t *__restrict__ kn,
+                                                       const float *__restrict__ rcos,
+                                                       const float *__restrict__ rsin,
+                                                       const int *__restrict__ pos_d, int max_seq,
+                                                       float eps) {
+    const int i = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int rr = blockIdx.y * 4 + wave;      // 0 .. 23
+    const int pos = *pos_d + i;
+    if (*pos_d < 0 || pos >= max_seq) return;
+    float *row = qkv + (size_t)i * QKV_LD;
+    const bool isq = rr < NKV * GRP;
+    const int hd = isq ? rr : rr - NKV * GRP;
+    float *src = isq ? row + (size_t)hd * HD : row + KOFF + (size_t)hd * HD;
+    const uint16_t *w = isq ? qn : kn;
+    const float x0 = src[lane], x1 = src[lane + 64];
+    const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
+    const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+    const float y0 = (x0 * sc) * w0, y1 = (x1 * sc) * w1;
+    const float o0 = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
+    const float o1 = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
+    if (isq) {
+        src[lane] = o0;
+        src[lane + 64] = o1;
+    } else {
+        float *kb = kc + (size_t)hd * (HD / 4) * max_seq * 4;
+        kb[((size_t)(lane >> 2) * max_seq + pos) * 4 + (lane & 3)] = o0;
+        kb[((size_t)((lane + 64) >> 2) * max_seq + pos) * 4 + (lane & 3)] = o1;
+        float *vb = vc + ((size_t)hd * max_seq + pos) * HD;
+        const float *vs = row + VOFF + (size_t)hd * HD;
+        vb[lane] = vs[lane];
+        vb[lane + 64] = vs[lane + 64];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Chunk step 2: causal GQA attention (qwen3.c:377-436) for token i of the
+// chunk and kv head g (block (i, g), its GRP query heads), with roped q in
+// qkv and every key/value t <= pos0 + i in the cache (written by step 1).
+//   scores s[h][t] = q_h . k_t / sqrt(128); softmax over t (ops_scalar.c:
+//   37-44), normalised as there; out_h = sum_t p[h][t] v_t.
+// grid = (nt, NKV), 256 threads, dynamic LDS = qm_attention_lds_bytes().
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv,
                                                    float *__restrict__ out,
-                                                   float *__restrict__ kc, float *__restrict__ vc,
-                                                   const uint16_t *__restrict__ qn,
-                                                   const uint16_t *__restrict__ kn,
-                                                   const float *__restrict__ rcos,
-                                                   const float *__restrict__ rsin,
-                                                   const int *__restrict__ pos_d, int nt,
-                                                   int max_seq, float eps, float scale) {
+                                                   const float *__restrict__ kc,
+                                                   const float *__restrict__ vc,
+                                                   const int *__restrict__ pos_d, int max_seq,
+                                                   float scale) {
     const int i = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int pos0 = *pos_d;
@@ -138,80 +176,33 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
     float *sq = sm;                            // [GRP][HD]
     float *red = sq + GRP * HD;                // [4][GRP][HD] partial outputs
     float *sred = red + 4 * GRP * HD;          // [2][4] block reductions
-    float *kch = sred + 8;                     // [nt][KST]
-    float *p = kch + (size_t)nt * KST;         // [GRP][max_seq]
+    float *p = sred + 8;                       // [GRP][max_seq]
 
-    // 1. QK-norm + RoPE of GRP q rows and i+1 chunk k rows
-    for (int rr = wave; rr < GRP + i + 1; rr += NTH / WAVE) {
-        const float *src;
-        const uint16_t *w;
-        float *dst;
-        int tp;
-        if (rr < GRP) {
-            src = qkv + (size_t)i * QKV_LD + (size_t)(g * GRP + rr) * HD;
-            w = qn;
-            dst = sq + rr * HD;
-            tp = pos;
-        } else {
-            const int t = rr - GRP;
-            src = qkv + (size_t)t * QKV_LD + KOFF + (size_t)g * HD;
-            w = kn;
-            dst = kch + (size_t)t * KST;
-            tp = pos0 + t;
-        }
-        const float x0 = src[lane], x1 = src[lane + 64];
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        const float y0 = (x0 * sc) * bf16f(w[lane]);
-        const float y1 = (x1 * sc) * bf16f(w[lane + 64]);
-        const float c = rcos[(size_t)tp * (HD / 2) + lane], s = rsin[(size_t)tp * (HD / 2) + lane];
-        // rotate_half pairing (i, i + 64), as ops_scalar.c:29-33
-        dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, s));
-        dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, s));
-    }
+    sq[tid] = qkv[(size_t)i * QKV_LD + (size_t)g * GRP * HD + tid];   // 256 threads = GRP x HD
     __syncthreads();
-    if (tid < HD) {                            // this block's own cache entry
-        const float kv = kch[(size_t)i * KST + tid];
-        kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = kv;
-        vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[(size_t)i * QKV_LD + VOFF + (size_t)g * HD + tid];
-    }
 
-    // 2. scores
+    // scores
+    const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
     for (int t = tid; t < ctx; t += NTH) {
+        f32x4 kv[HD / 4];
+#pragma unroll
+        for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
         float s0 = 0.0f, s1 = 0.0f;
-        if (t < pos0) {
-            const f32x4 *kp = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq + t;
-            f32x4 kv[HD / 4];
 #pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kp[(size_t)d4 * max_seq];
-#pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) {
-                const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
-                const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
-                s0 = fmaf(q0.x, kv[d4].x, s0); s0 = fmaf(q0.y, kv[d4].y, s0);
-                s0 = fmaf(q0.z, kv[d4].z, s0); s0 = fmaf(q0.w, kv[d4].w, s0);
-                s1 = fmaf(q1.x, kv[d4].x, s1); s1 = fmaf(q1.y, kv[d4].y, s1);
-                s1 = fmaf(q1.z, kv[d4].z, s1); s1 = fmaf(q1.w, kv[d4].w, s1);
-            }
-        } else {
-            const f32x4 *kr = reinterpret_cast<const f32x4 *>(kch + (size_t)(t - pos0) * KST);
-#pragma unroll 8
-            for (int d4 = 0; d4 < HD / 4; d4++) {
-                const f32x4 kv = kr[d4];
-                const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
-                const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
-                s0 = fmaf(q0.x, kv.x, s0); s0 = fmaf(q0.y, kv.y, s0);
-                s0 = fmaf(q0.z, kv.z, s0); s0 = fmaf(q0.w, kv.w, s0);
-                s1 = fmaf(q1.x, kv.x, s1); s1 = fmaf(q1.y, kv.y, s1);
-                s1 = fmaf(q1.z, kv.z, s1); s1 = fmaf(q1.w, kv.w, s1);
-            }
+        for (int d4 = 0; d4 < HD / 4; d4++) {
+            const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
+            const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
+            s0 = fmaf(q0.x, kv[d4].x, s0); s0 = fmaf(q0.y, kv[d4].y, s0);
+            s0 = fmaf(q0.z, kv[d4].z, s0); s0 = fmaf(q0.w, kv[d4].w, s0);
+            s1 = fmaf(q1.x, kv[d4].x, s1); s1 = fmaf(q1.y, kv[d4].y, s1);
+            s1 = fmaf(q1.z, kv[d4].z, s1); s1 = fmaf(q1.w, kv[d4].w, s1);
         }
         p[t] = s0 * scale;
         p[max_seq + t] = s1 * scale;
     }
     __syncthreads();
 
-    // 3. softmax per query head
+    // softmax per query head
     float m0 = -INFINITY, m1 = -INFINITY;
     for (int t = tid; t < ctx; t += NTH) {
         m0 = fmaxf(m0, p[t]);
@@ -244,19 +235,15 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
     }
     __syncthreads();
 
-    // 4. out_h[d] = sum_t p[h][t] v_t[d]: wave w takes t = w, w+4, ...; lane
-    //    l owns d = 2l, 2l+1 of both heads
+    // out_h[d] = sum_t p[h][t] v_t[d]: wave w takes t = w, w+4, ...; lane l
+    // owns d = 2l, 2l+1 of both heads
     f32x2 o0 = {0.f, 0.f}, o1 = {0.f, 0.f};
     const f32x2 *vcache = reinterpret_cast<const f32x2 *>(vc + (size_t)g * max_seq * HD) + lane;
-    const f32x2 *vchunk = reinterpret_cast<const f32x2 *>(qkv + VOFF + (size_t)g * HD) + lane;
     int t = wave;
     for (; t + 4 * 7 < ctx; t += 4 * 8) {      // 8 loads in flight per lane
         f32x2 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int tt = t + 4 * u;
-            v[u] = tt < pos0 ? vcache[(size_t)tt * (HD / 2)] : vchunk[(size_t)(tt - pos0) * (QKV_LD / 2)];
-        }
+        for (int u = 0; u < 8; u++) v[u] = vcache[(size_t)(t + 4 * u) * (HD / 2)];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
             const float p0 = p[t + 4 * u], p1 = p[max_seq + t + 4 * u];
@@ -267,7 +254,7 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
         }
     }
     for (; t < ctx; t += 4) {
-        const f32x2 v = t < pos0 ? vcache[(size_t)t * (HD / 2)] : vchunk[(size_t)(t - pos0) * (QKV_LD / 2)];
+        const f32x2 v = vcache[(size_t)t * (HD / 2)];
         const float p0 = p[t], p1 = p[max_seq + t];
         o0.x = __fadd_rn(o0.x, __fmul_rn(p0, v.x));
         o0.y = __fadd_rn(o0.y, __fmul_rn(p0, v.y));
@@ -281,9 +268,157 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
     __syncthreads();
     {
         const int h = tid >> 7, d = tid & (HD - 1);   // 256 threads = GRP x HD
-        const float s = (red[(0 * GRP + h) * HD + d] + red[(1 * GRP + h) * HD + d]) +
-                        (red[(2 * GRP + h) * HD + d] + red[(3 * GRP + h) * HD + d]);
-        out[(size_t)i * (NKV * GRP * HD) + (size_t)(g * GRP + h) * HD + d] = s;
+        const float sacc = (red[(0 * GRP + h) * HD + d] + red[(1 * GRP + h) * HD + d]) +
+                           (red[(2 * GRP + h) * HD + d] + red[(3 * GRP + h) * HD + d]);
+        out[(size_t)i * (NKV * GRP * HD) + (size_t)(g * GRP + h) * HD + d] = sacc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention: one token at position pos = *pos_d.  Block b handles
+// query head 2g + r with g = b % NKV, r = b / NKV, so the two heads of a kv
+// group run on the same XCD (block b runs on XCD b % 8) and share its L2.
+// The kernel is built for latency: every thread issues the K loads of its
+// position (32 x 16 B, one contiguous 1 KB run per wave in the d-chunk-major
+// cache) before QK-norm and RoPE of q and k start, and the V loads of the
+// weighted sum go out before the softmax reductions.  Positions are taken
+// 256 at a time (one per thread); scores live in LDS.
+// grid = 2 * NKV blocks of 256 threads; dynamic LDS = decode_lds(max_seq).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ qkv,
+                                                     float *__restrict__ out,
+                                                     float *__restrict__ kc, float *__restrict__ vc,
+                                                     const uint16_t *__restrict__ qn,
+                                                     const uint16_t *__restrict__ kn,
+                                                     const float *__restrict__ rcos,
+                                                     const float *__restrict__ rsin,
+                                                     const int *__restrict__ pos_d, int max_seq,
+                                                     float eps, float scale) {
+    const int g = blockIdx.x % NKV, r = blockIdx.x / NKV, hq = g * GRP + r;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int pos = *pos_d;
+    if (pos < 0 || pos >= max_seq) return;      // uniform per launch
+    const int ctx = pos + 1;
+
+    extern __shared__ float sm[];
+    float *sq = sm;                              // [HD]
+    float *sk = sq + HD;                         // [HD] k of the new token
+    float *red = sk + HD;                        // [8][HD]
+    float *sred = red + 8 * HD;                  // [8]
+    float *p = sred + 8;                         // [max_seq] scores, then weights
+
+    const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
+
+    // K loads of the first 256 positions go out before anything else
+    f32x4 kv[HD / 4];
+    {
+        const int t = tid;
+        if (t < pos) {
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
+        }
+    }
+
+    // QK-norm + RoPE: wave 0 the query head, wave 1 the new k
+    if (wave < 2) {
+        const float *src = wave == 0 ? qkv + (size_t)hq * HD : qkv + KOFF + (size_t)g * HD;
+        const uint16_t *w = wave == 0 ? qn : kn;
+        float *dst = wave == 0 ? sq : sk;
+        const float x0 = src[lane], x1 = src[lane + 64];
+        const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
+        const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
+        const float y0 = (x0 * sc) * w0, y1 = (x1 * sc) * w1;
+        dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
+        dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
+    }
+    __syncthreads();
+    if (r == 0 && tid < HD) {                    // one block per kv head writes the new entry
+        kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = sk[tid];
+        vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[VOFF + (size_t)g * HD + tid];
+    }
+
+    // scores, 256 positions per pass
+    for (int base = 0; base < ctx; base += NTH) {
+        const int t = base + tid;
+        if (base > 0 && t < pos) {
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
+        }
+        if (t < ctx) {
+            const float *kr = t < pos ? nullptr : sk;
+            float s0 = 0.0f;
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const f32x4 q = reinterpret_cast<const f32x4 *>(sq)[d4];
+                const f32x4 k = kr ? reinterpret_cast<const f32x4 *>(kr)[d4] : kv[d4];
+                s0 = fmaf(q.x, k.x, s0); s0 = fmaf(q.y, k.y, s0);
+                s0 = fmaf(q.z, k.z, s0); s0 = fmaf(q.w, k.w, s0);
+            }
+            p[t] = s0 * scale;
+        }
+    }
+
+    // V loads of the first pass (8 row groups x 32 chunks of 16 B) before the softmax
+    const int tg = tid >> 5, d4 = tid & 31;
+    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD) + d4;
+    const f32x4 vnew = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD)[d4];
+    constexpr int VB = NTH / 8;                  // positions per thread and pass
+    f32x4 vv[VB];
+#pragma unroll
+    for (int u = 0; u < VB; u++) {
+        const int t = tg + 8 * u;
+        vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
+    }
+    __syncthreads();
+
+    // softmax (ops_scalar.c:37-44)
+    float m = -INFINITY;
+    for (int t = tid; t < ctx; t += NTH) m = fmaxf(m, p[t]);
+    m = wave_max(m);
+    if (lane == 0) sred[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+    float e = 0.0f;
+    for (int t = tid; t < ctx; t += NTH) {
+        const float a = expf(p[t] - m);
+        p[t] = a;
+        e += a;
+    }
+    e = wave_sum(e);
+    if (lane == 0) sred[4 + wave] = e;
+    __syncthreads();
+    e = (sred[4] + sred[5]) + (sred[6] + sred[7]);
+    const float inv = 1.0f / e;
+
+    // out[d] = sum_t p[t] v_t[d] / e
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int base = 0; base < ctx; base += NTH) {
+        if (base > 0) {
+#pragma unroll
+            for (int u = 0; u < VB; u++) {
+                const int t = base + tg + 8 * u;
+                vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < VB; u++) {
+            const int t = base + tg + 8 * u;
+            if (t < ctx) {
+                const float w = p[t];
+                o.x = fmaf(w, vv[u].x, o.x); o.y = fmaf(w, vv[u].y, o.y);
+                o.z = fmaf(w, vv[u].z, o.z); o.w = fmaf(w, vv[u].w, o.w);
+            }
+        }
+    }
+    reinterpret_cast<f32x4 *>(red + tg * HD)[d4] = o;
+    __syncthreads();
+    if (tid < HD) {
+        float sacc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) sacc += red[k * HD + tid];
+        out[(size_t)hq * HD + tid] = sacc * inv;
     }
 }
 
@@ -291,13 +426,17 @@ __global__ void k_set_i32(int *p, int v) {
     if (threadIdx.x == 0 && blockIdx.x == 0) p[0] = v;
 }
 
+__global__ void k_zero_i32(int *p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 static inline hipStream_t stream() { return (hipStream_t)qh_stream(); }
 
-extern "C" size_t qm_attention_lds_bytes(int nt, int max_seq) {
-    return sizeof(float) * ((size_t)GRP * HD + 4 * GRP * HD + 8 + (size_t)nt * KST + (size_t)GRP * max_seq);
+extern "C" size_t qm_attention_lds_bytes(int max_seq) {
+    return sizeof(float) * ((size_t)GRP * HD + 4 * GRP * HD + 8 + (size_t)GRP * max_seq);
 }
 
 extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const int *tok, int emb_rows,
@@ -310,24 +449,53 @@ extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 
-extern "C" int qm_attention(const float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
+extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
                             const uint16_t *kn, const float *rcos, const float *rsin, const int *pos_d,
                             int nt, int max_seq, float eps) {
     if (!stream()) return QH_ESTATE;
     if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (nt <= 0 || max_seq <= 0 || nt > QM_MAX_CHUNK || max_seq > QM_MAX_SEQ) return QH_EINVAL;
-    const size_t lds = qm_attention_lds_bytes(nt, max_seq);
+    const size_t lds = qm_attention_lds_bytes(max_seq);
     static bool attr_set = false;
     if (!attr_set) {
         if (hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)qm_attention_lds_bytes(QM_MAX_CHUNK, QM_MAX_SEQ)) != hipSuccess)
+                                (int)qm_attention_lds_bytes(QM_MAX_SEQ)) != hipSuccess)
             return QH_ELAUNCH;
         attr_set = true;
     }
     // 1 / sqrt(head_dim), the constant of qwen3.c:311
     const float scale = 0.08838834764831845f;
-    hipLaunchKernelGGL(k_attention, dim3(nt, NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn, rcos,
-                       rsin, pos_d, nt, max_seq, eps, scale);
+    hipLaunchKernelGGL(k_qk_rope_cache, dim3(nt, (NKV * GRP + NKV) / 4), dim3(NTH), 0, stream(), qkv, kc, vc,
+                       qn, kn, rcos, rsin, pos_d, max_seq, eps);
+    if (hipGetLastError() != hipSuccess) return QH_ELAUNCH;
+    hipLaunchKernelGGL(k_attention, dim3(nt, NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, pos_d, max_seq,
+                       scale);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" size_t qm_attention_decode_lds_bytes(int max_seq) {
+    return sizeof(float) * ((size_t)2 * HD + 8 * HD + 8 + (size_t)max_seq);
+}
+
+extern "C" int qm_attention_decode(const float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
+                                   const uint16_t *kn, const float *rcos, const float *rsin,
+                                   const int *pos_d, int max_seq, float eps) {
+    if (!stream()) return QH_ESTATE;
+    if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
+    if (max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
+    const size_t lds = qm_attention_decode_lds_bytes(max_seq);
+    const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
+    hipLaunchKernelGGL(k_attn_decode, dim3(GRP * NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn,
+                       rcos, rsin, pos_d, max_seq, eps, scale);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" int qm_zero_i32(int *p, int n) {
+    if (!stream()) return QH_ESTATE;
+    if (!p || n < 0) return QH_EINVAL;
+    if (n == 0) return QH_OK;
+    hipLaunchKernelGGL(k_zero_i32, dim3((n + NTH - 1) / NTH < 1024 ? (n + NTH - 1) / NTH : 1024), dim3(NTH), 0,
+                       stream(), p, n);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

@@ -351,9 +351,9 @@ static int decode_step(qwen3_hip_model *m) {
         qh_gemv_pro_t pro = {m->x0, NULL, NULL, 0, m->dn, L->in_norm, m->x1, eps};
         if (l == 0) { pro.x = NULL; pro.r = NULL; pro.emb = m->embed; pro.tok = m->state; pro.emb_rows = V; }
         rc = qh_gemv_pro(m->qkv, &pro, L->wqkv, NULL, H, QKV_N, 0);
-        if (!rc) rc = qm_attention(m->qkv, m->att, m->kc + l * kv_layer_floats(m),
-                                   m->vc + l * kv_layer_floats(m), L->qn, L->kn, m->rcos, m->rsin,
-                                   m->state + 1, 1, m->max_seq, eps);
+        if (!rc) rc = qm_attention_decode(m->qkv, m->att, m->kc + l * kv_layer_floats(m),
+                                          m->vc + l * kv_layer_floats(m), L->qn, L->kn, m->rcos, m->rsin,
+                                          m->state + 1, m->max_seq, eps);
         if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, 1, QW3M_Q_DIM, H);
         const qh_gemv_pro_t pro2 = {m->x1, NULL, NULL, 0, m->ob, L->post_norm, m->x0, eps};
         if (!rc) rc = qh_gemv_pro(m->hb, &pro2, L->wg, L->wu, H, QW3M_INTER, 1);

@@ -39,6 +39,24 @@ def qw3m_random(seed, layout=LAYOUT_ROW, threads=8):
     return blob
 
 
+def qw3m_tensors(blob):
+    """[(byte offset, rows, cols)] of the 310 tensors in blob order
+    (fpga_bringup/src/src/qwen3_config.h:63-78), from the blob's header."""
+    import struct
+    ds, al = struct.unpack("<ii", blob[68:76].tobytes())
+    H, Q, KV, I, HD = 1024, 2048, 1024, 3072, 128
+    shapes = [(VOCAB, H)]
+    for _ in range(28):
+        shapes += [(1, H), (Q, H), (KV, H), (KV, H), (1, HD), (1, HD), (H, Q), (1, H), (I, H), (I, H), (H, I)]
+    shapes.append((1, H))
+    out, pos = [], ds
+    for r, c in shapes:
+        pos = (pos + al - 1) // al * al
+        out.append((pos, r, c))
+        pos += r * c * 2
+    return out
+
+
 def qw3m_check(blob):
     """0, or the reference's QWEN3_ERR_* code for a blob that does not parse."""
     return int(runtime.lib().qwen3_hip_qw3m_check(blob.ctypes.data_as(VP), blob.nbytes))

@@ -172,7 +172,7 @@ def test_chunked_prefill_matches_two_calls(model):
 def test_tile_layout_blob_gives_identical_results(blob, model):
     fx = fixture("short")
     tb = M.qw3m_random(int(fx["seed"]), M.LAYOUT_TILE, threads=16)
-    with M.Model(tb, max_seq=64) as mt:
+    with M.Model(tb, max_seq=model.max_seq) as mt:
         a = mt.generate(fx["prompt"], 4)
         la = mt.logits()
     b = model.generate(fx["prompt"], 4)
