@@ -166,9 +166,8 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
 //   a = rmsnorm(x + r) * nw       (fpga_bringup/src/src/ops_scalar.c:11-16,
 //                                  residual add ops_scalar.c:53-55)
 // where x is either an fp32 row or, when emb is set, the bf16 embedding row
-// emb[*tok] (qwen3.c:295-298).  Every wave loads the whole row and reduces
-// its sum of squares itself, so no barrier is needed; wave 0 of block 0
-// stores x + r to x_out when x_out is set (the updated residual stream).
+// emb[*tok] (qwen3.c:295-298).  Block 0 stores x + r to x_out when x_out is
+// set (the updated residual stream).
 struct GemvPro {
     const float *x;
     const uint16_t *emb;
@@ -182,12 +181,17 @@ struct GemvPro {
 
 // M = 1 fast path (decode).  One wave owns ROWS output rows; lane l owns the
 // 16-byte chunks l, l+64, ..., l+64*(CPL-1) of every row (CPL = chunks per
-// lane, K <= 512*CPL).  All ROWS*CPL weight loads and the 2*CPL activation
-// loads are issued before the first use, so a launch costs one memory round
-// trip; there is no LDS and no barrier.  GATED: rows of Wg and Wu with the
-// same index are both loaded and the epilogue writes silu(gate) * up.
-// PRO: the activation row is produced by the GemvPro prologue instead of
-// being read from a.
+// lane, K <= 512*CPL).  The block's 256 threads first load the activation
+// row once between them (a quarter per wave, 16 B per thread per 4 KB of
+// row), then every wave issues all of its ROWS*CPL non-temporal weight
+// loads; the activation (rounded to bf16, and for PRO normalised first) is
+// exchanged through LDS while the weights are still in flight, so a launch
+// costs one HBM round trip and each block reads the activation from L2
+// once instead of once per wave.  GATED: rows of Wg and Wu with the same
+// index are both loaded and the epilogue writes silu(gate) * up.  PRO: the
+// activation row comes from the GemvPro prologue instead of a.
+// Dynamic LDS: (K + 8) floats.  Waves without rows still take part in the
+// barriers.
 template <int ROWS, int CPL, bool GATED, bool PRO = false>
 __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                    const float *__restrict__ a,
@@ -195,120 +199,123 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                    const uint16_t *__restrict__ b2,
                                                    int K, int N, GemvPro pro) {
     constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    constexpr int QMAX = (CPL * 8 * WAVE + 4 * NTHREADS - 1) / (4 * NTHREADS);   // f32x4 per thread
+    extern __shared__ float sact[];                  // [K] activation, then [4] partial sums
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
-    if (row0 >= N) return;
-    const int nch = K >> 3;
-    const u32x4 *b4 = reinterpret_cast<const u32x4 *>(b);
-    const u32x4 *u4 = reinterpret_cast<const u32x4 *>(b2);
+    const bool active = row0 < N;
+    const int nch = K >> 3, nq = K >> 2;
 
-    u32x4 bv[NB][CPL];
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-        const size_t rb = (size_t)min(row0 + r, N - 1) * nch;
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            if (ch < nch) {
-                bv[r][j] = __builtin_nontemporal_load(b4 + rb + ch);
-                if constexpr (GATED) bv[ROWS + r][j] = __builtin_nontemporal_load(u4 + rb + ch);
-            } else {
-                bv[r][j] = u32x4{0u, 0u, 0u, 0u};
-                if constexpr (GATED) bv[ROWS + r][j] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-    }
-    float av[CPL][8];
+    // 1. this thread's share of the activation row (issued before the weights)
+    f32x4 xa[QMAX];
+    uint2 wn[QMAX];
     if constexpr (!PRO) {
 #pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            if (ch < nch) {
-                const f32x4 *ap = reinterpret_cast<const f32x4 *>(a + ch * 8);
-                const f32x4 x0 = ap[0], x1 = ap[1];
-                av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
-                av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
-            }
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            xa[q] = i < nq ? reinterpret_cast<const f32x4 *>(a)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
     } else {
-        const u32x4 *e4 = nullptr;
+        const uint2 *e2 = nullptr;
         if (pro.emb) {
             int t = *pro.tok;
             t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
-            e4 = reinterpret_cast<const u32x4 *>(pro.emb + (size_t)t * K);
+            e2 = reinterpret_cast<const uint2 *>(pro.emb + (size_t)t * K);
         }
-        // norm weights are independent of the reduction: load them first
-        const u32x4 *w4 = reinterpret_cast<const u32x4 *>(pro.nw);
-        u32x4 nwv[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            nwv[j] = ch < nch ? w4[ch] : u32x4{0u, 0u, 0u, 0u};
-        }
-        float ss = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            if (ch < nch) {
-                if (e4) {
-                    const u32x4 w = e4[ch];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        av[j][2 * e] = bf16_lo(w[e]);
-                        av[j][2 * e + 1] = bf16_hi(w[e]);
-                    }
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            xa[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+            wn[q] = uint2{0u, 0u};
+            if (i < nq) {
+                wn[q] = reinterpret_cast<const uint2 *>(pro.nw)[i];
+                if (e2) {
+                    const uint2 e = e2[i];
+                    xa[q] = f32x4{bf16_lo(e.x), bf16_hi(e.x), bf16_lo(e.y), bf16_hi(e.y)};
                 } else {
-                    const f32x4 *xp = reinterpret_cast<const f32x4 *>(pro.x + ch * 8);
-                    f32x4 x0 = xp[0], x1 = xp[1];
-                    if (pro.r) {
-                        const f32x4 *rp = reinterpret_cast<const f32x4 *>(pro.r + ch * 8);
-                        x0 += rp[0];
-                        x1 += rp[1];
-                    }
-                    av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
-                    av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
+                    xa[q] = reinterpret_cast<const f32x4 *>(pro.x)[i];
+                    if (pro.r) xa[q] += reinterpret_cast<const f32x4 *>(pro.r)[i];
                 }
-#pragma unroll
-                for (int e = 0; e < 8; e++) ss += av[j][e] * av[j][e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
             }
         }
+    }
+
+    // 2. all weight loads of this wave
+    const u32x4 *b4 = reinterpret_cast<const u32x4 *>(b);
+    const u32x4 *u4 = reinterpret_cast<const u32x4 *>(b2);
+    u32x4 bv[NB][CPL];
+    if (active) {
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
-        if (pro.x_out && blockIdx.x == 0 && wave == 0) {
+        for (int r = 0; r < ROWS; r++) {
+            const size_t rb = (size_t)min(row0 + r, N - 1) * nch;
 #pragma unroll
             for (int j = 0; j < CPL; j++) {
                 const int ch = lane + WAVE * j;
                 if (ch < nch) {
-                    f32x4 *op = reinterpret_cast<f32x4 *>(pro.x_out + ch * 8);
-                    op[0] = f32x4{av[j][0], av[j][1], av[j][2], av[j][3]};
-                    op[1] = f32x4{av[j][4], av[j][5], av[j][6], av[j][7]};
-                }
-            }
-        }
-        const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            if (ch < nch) {
-                const u32x4 w = nwv[j];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    av[j][2 * e] = (av[j][2 * e] * scale) * bf16_lo(w[e]);
-                    av[j][2 * e + 1] = (av[j][2 * e + 1] * scale) * bf16_hi(w[e]);
+                    bv[r][j] = __builtin_nontemporal_load(b4 + rb + ch);
+                    if constexpr (GATED) bv[ROWS + r][j] = __builtin_nontemporal_load(u4 + rb + ch);
+                } else {
+                    bv[r][j] = u32x4{0u, 0u, 0u, 0u};
+                    if constexpr (GATED) bv[ROWS + r][j] = u32x4{0u, 0u, 0u, 0u};
                 }
             }
         }
     }
+
+    // 3. activation through LDS, rounded to bf16 (normalised first for PRO)
+    f32x4 *sa4 = reinterpret_cast<f32x4 *>(sact);
+    if constexpr (PRO) {
+        float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < CPL; j++)
+        for (int q = 0; q < QMAX; q++)
+            ss += xa[q].x * xa[q].x + xa[q].y * xa[q].y + xa[q].z * xa[q].z + xa[q].w * xa[q].w;
 #pragma unroll
-        for (int e = 0; e < 8; e++) av[j][e] = round_bf16(av[j][e]);
+        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+        if (lane == 0) sact[K + wave] = ss;
+        if (pro.x_out && blockIdx.x == 0) {
+#pragma unroll
+            for (int q = 0; q < QMAX; q++) {
+                const int i = tid + NTHREADS * q;
+                if (i < nq) reinterpret_cast<f32x4 *>(pro.x_out)[i] = xa[q];
+            }
+        }
+        __syncthreads();
+        ss = (sact[K] + sact[K + 1]) + (sact[K + 2] + sact[K + 3]);
+        const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
+#pragma unroll
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            if (i < nq)
+                sa4[i] = f32x4{round_bf16((xa[q].x * scale) * bf16_lo(wn[q].x)),
+                               round_bf16((xa[q].y * scale) * bf16_hi(wn[q].x)),
+                               round_bf16((xa[q].z * scale) * bf16_lo(wn[q].y)),
+                               round_bf16((xa[q].w * scale) * bf16_hi(wn[q].y))};
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            if (i < nq)
+                sa4[i] = f32x4{round_bf16(xa[q].x), round_bf16(xa[q].y), round_bf16(xa[q].z),
+                               round_bf16(xa[q].w)};
+        }
+    }
+    __syncthreads();
+    if (!active) return;                             // no barrier below this point
+
+    float av[CPL][8];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        const int ch = lane + WAVE * j;
+        if (ch < nch) {
+            const f32x4 x0 = sa4[2 * ch], x1 = sa4[2 * ch + 1];
+            av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
+            av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
+        }
+    }
 
     constexpr int V = pow2_ceil<NB>::v;
     float acc[V];
@@ -1440,12 +1447,13 @@ template <int ROWS, bool GATED, bool PRO>
 static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                              int K, int N, int cpl, const GemvPro &pro) {
     const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
+    const size_t lds = (size_t)(K + 8) * sizeof(float);
     // only the (ROWS, CPL) pairs launch_gemv1 can pick: <= 16 loads per lane
 #define QH_GEMV1_CASE(P)                                                                     \
     case P:                                                                                  \
         if constexpr (ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16)                         \
             hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED, PRO>), dim3(grid), dim3(NTHREADS),   \
-                               0, g_stream, c, a, b, b2, K, N, pro);                         \
+                               lds, g_stream, c, a, b, b2, K, N, pro);                       \
         else                                                                                 \
             return QH_EINVAL;                                                                \
         break;

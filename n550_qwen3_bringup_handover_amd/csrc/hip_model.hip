@@ -14,8 +14,8 @@
 //   V cache       [layer][kv_head][max_seq][128]        (as qwen3.h:62-76)
 //   rope tables   [max_seq][64] cos and sin, built on the host with the
 //                 reference formula (ops_scalar.c:21-35)
-// The chunk attention keeps 2 x max_seq scores in LDS (up to 69 KB at
-// QM_MAX_SEQ), above the default 64 KB limit that it raises once.
+// The attention kernels keep 2 x max_seq scores in LDS (up to 69 KB at
+// QM_MAX_SEQ), above the default 64 KB limit that they raise once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -275,16 +275,22 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention: one token at position pos = *pos_d.  Block b handles
-// query head 2g + r with g = b % NKV, r = b / NKV, so the two heads of a kv
-// group run on the same XCD (block b runs on XCD b % 8) and share its L2.
-// The kernel is built for latency: every thread issues the K loads of its
-// position (32 x 16 B, one contiguous 1 KB run per wave in the d-chunk-major
-// cache) before QK-norm and RoPE of q and k start, and the V loads of the
-// weighted sum go out before the softmax reductions.  Positions are taken
-// 256 at a time (one per thread); scores live in LDS.
-// grid = 2 * NKV blocks of 256 threads; dynamic LDS = decode_lds(max_seq).
+// Decode attention: one token at position pos = *pos_d.  Block b = g + 8*q
+// handles kv head g (its GRP query heads) and quarter q of the head
+// dimension: it computes the full scores of both query heads (K is read
+// once for the pair), the softmax, and out[h][32q .. 32q+32) from a quarter
+// of every V row, so no block needs another's result.  The 4 blocks of a kv
+// head share XCD g (block b runs on XCD b % 8) and so its L2 for the K rows.
+// Built for latency: every thread issues its K loads (32 x 16 B of one
+// position, a contiguous 1 KB run per wave in the d-chunk-major cache) and
+// its V loads at entry, before QK-norm and RoPE start.  Positions are taken
+// 256 at a time; scores live in LDS.  Block (g, 0) writes the new token's
+// cache entry.  grid = 4 * NKV blocks of 256 threads; dynamic LDS =
+// qm_attention_decode_lds_bytes(max_seq).
 // ---------------------------------------------------------------------------
+#define DQ 4                      // head-dimension quarters
+#define DQW (HD / DQ)             // 32 dims per block
+
 __global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ qkv,
                                                      float *__restrict__ out,
                                                      float *__restrict__ kc, float *__restrict__ vc,
@@ -294,36 +300,44 @@ __global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ q
                                                      const float *__restrict__ rsin,
                                                      const int *__restrict__ pos_d, int max_seq,
                                                      float eps, float scale) {
-    const int g = blockIdx.x % NKV, r = blockIdx.x / NKV, hq = g * GRP + r;
+    const int g = blockIdx.x % NKV, q = blockIdx.x / NKV;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int pos = *pos_d;
     if (pos < 0 || pos >= max_seq) return;      // uniform per launch
     const int ctx = pos + 1;
 
     extern __shared__ float sm[];
-    float *sq = sm;                              // [HD]
-    float *sk = sq + HD;                         // [HD] k of the new token
-    float *red = sk + HD;                        // [8][HD]
-    float *sred = red + 8 * HD;                  // [8]
-    float *p = sred + 8;                         // [max_seq] scores, then weights
+    float *sq = sm;                              // [GRP][HD]
+    float *sk = sq + GRP * HD;                   // [HD] k of the new token
+    float *red = sk + HD;                        // [32 groups][GRP][DQW]
+    float *sred = red + 32 * GRP * DQW;          // [16]
+    float *p = sred + 16;                        // [GRP][max_seq]
 
     const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
+    // V: thread (tg = tid / 8, c = tid % 8) owns dims 32q + 4c .. +4 of positions tg, tg + 32, ...
+    const int tg = tid >> 3, c4 = tid & 7;
+    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD + q * DQW) + c4;
+    const f32x4 vnew = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD + q * DQW)[c4];
+    constexpr int VB = NTH / 32;                 // positions per thread and pass of 256
 
-    // K loads of the first 256 positions go out before anything else
+    // loads of the first pass go out before anything else
     f32x4 kv[HD / 4];
-    {
-        const int t = tid;
-        if (t < pos) {
+    if (tid < pos) {
 #pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
-        }
+        for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + tid];
+    }
+    f32x4 vv[VB];
+#pragma unroll
+    for (int u = 0; u < VB; u++) {
+        const int t = tg + 32 * u;
+        vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
     }
 
-    // QK-norm + RoPE: wave 0 the query head, wave 1 the new k
-    if (wave < 2) {
-        const float *src = wave == 0 ? qkv + (size_t)hq * HD : qkv + KOFF + (size_t)g * HD;
-        const uint16_t *w = wave == 0 ? qn : kn;
-        float *dst = wave == 0 ? sq : sk;
+    // QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
+    if (wave < GRP + 1) {
+        const float *src = wave < GRP ? qkv + (size_t)(g * GRP + wave) * HD : qkv + KOFF + (size_t)g * HD;
+        const uint16_t *w = wave < GRP ? qn : kn;
+        float *dst = wave < GRP ? sq + wave * HD : sk;
         const float x0 = src[lane], x1 = src[lane + 64];
         const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
         const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
@@ -334,91 +348,104 @@ __global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ q
         dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
     }
     __syncthreads();
-    if (r == 0 && tid < HD) {                    // one block per kv head writes the new entry
+    if (q == 0 && tid < HD) {                    // one block per kv head writes the new entry
         kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = sk[tid];
         vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[VOFF + (size_t)g * HD + tid];
     }
 
-    // scores, 256 positions per pass
-    for (int base = 0; base < ctx; base += NTH) {
-        const int t = base + tid;
-        if (base > 0 && t < pos) {
+    // scores of both query heads: the first 256 positions from the registers
+    // loaded at entry, later ones (ctx > 256) in further passes
+    auto dot2 = [&](const f32x4 *k, float &s0, float &s1) {
 #pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
+        for (int d4 = 0; d4 < HD / 4; d4++) {
+            const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
+            const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
+            s0 = fmaf(q0.x, k[d4].x, s0); s0 = fmaf(q0.y, k[d4].y, s0);
+            s0 = fmaf(q0.z, k[d4].z, s0); s0 = fmaf(q0.w, k[d4].w, s0);
+            s1 = fmaf(q1.x, k[d4].x, s1); s1 = fmaf(q1.y, k[d4].y, s1);
+            s1 = fmaf(q1.z, k[d4].z, s1); s1 = fmaf(q1.w, k[d4].w, s1);
         }
-        if (t < ctx) {
-            const float *kr = t < pos ? nullptr : sk;
-            float s0 = 0.0f;
-#pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) {
-                const f32x4 q = reinterpret_cast<const f32x4 *>(sq)[d4];
-                const f32x4 k = kr ? reinterpret_cast<const f32x4 *>(kr)[d4] : kv[d4];
-                s0 = fmaf(q.x, k.x, s0); s0 = fmaf(q.y, k.y, s0);
-                s0 = fmaf(q.z, k.z, s0); s0 = fmaf(q.w, k.w, s0);
-            }
-            p[t] = s0 * scale;
-        }
+    };
+    if (tid < ctx) {
+        float s0 = 0.0f, s1 = 0.0f;
+        if (tid < pos) dot2(kv, s0, s1);
+        else dot2(reinterpret_cast<const f32x4 *>(sk), s0, s1);   // the new token
+        p[tid] = s0 * scale;
+        p[max_seq + tid] = s1 * scale;
     }
-
-    // V loads of the first pass (8 row groups x 32 chunks of 16 B) before the softmax
-    const int tg = tid >> 5, d4 = tid & 31;
-    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD) + d4;
-    const f32x4 vnew = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD)[d4];
-    constexpr int VB = NTH / 8;                  // positions per thread and pass
-    f32x4 vv[VB];
+    for (int t = NTH + tid; t < ctx; t += NTH) {
+        float s0 = 0.0f, s1 = 0.0f;
+        if (t < pos) {
+            f32x4 k2[HD / 4];
 #pragma unroll
-    for (int u = 0; u < VB; u++) {
-        const int t = tg + 8 * u;
-        vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
+            for (int d4 = 0; d4 < HD / 4; d4++) k2[d4] = kbase[(size_t)d4 * max_seq + t];
+            dot2(k2, s0, s1);
+        } else {
+            dot2(reinterpret_cast<const f32x4 *>(sk), s0, s1);
+        }
+        p[t] = s0 * scale;
+        p[max_seq + t] = s1 * scale;
     }
     __syncthreads();
 
-    // softmax (ops_scalar.c:37-44)
-    float m = -INFINITY;
-    for (int t = tid; t < ctx; t += NTH) m = fmaxf(m, p[t]);
-    m = wave_max(m);
-    if (lane == 0) sred[wave] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-    float e = 0.0f;
+    // softmax of both heads (ops_scalar.c:37-44)
+    float m0 = -INFINITY, m1 = -INFINITY;
     for (int t = tid; t < ctx; t += NTH) {
-        const float a = expf(p[t] - m);
-        p[t] = a;
-        e += a;
+        m0 = fmaxf(m0, p[t]);
+        m1 = fmaxf(m1, p[max_seq + t]);
     }
-    e = wave_sum(e);
-    if (lane == 0) sred[4 + wave] = e;
+    m0 = wave_max(m0);
+    m1 = wave_max(m1);
+    if (lane == 0) { sred[wave] = m0; sred[4 + wave] = m1; }
     __syncthreads();
-    e = (sred[4] + sred[5]) + (sred[6] + sred[7]);
-    const float inv = 1.0f / e;
+    m0 = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
+    m1 = fmaxf(fmaxf(sred[4], sred[5]), fmaxf(sred[6], sred[7]));
+    float e0 = 0.0f, e1 = 0.0f;
+    for (int t = tid; t < ctx; t += NTH) {
+        const float a0 = expf(p[t] - m0), a1 = expf(p[max_seq + t] - m1);
+        p[t] = a0;
+        p[max_seq + t] = a1;
+        e0 += a0;
+        e1 += a1;
+    }
+    e0 = wave_sum(e0);
+    e1 = wave_sum(e1);
+    if (lane == 0) { sred[8 + wave] = e0; sred[12 + wave] = e1; }
+    __syncthreads();
+    const float inv0 = 1.0f / ((sred[8] + sred[9]) + (sred[10] + sred[11]));
+    const float inv1 = 1.0f / ((sred[12] + sred[13]) + (sred[14] + sred[15]));
 
-    // out[d] = sum_t p[t] v_t[d] / e
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
+    // out[h][32q + d] = sum_t p[h][t] v_t[32q + d] / e_h
+    f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     for (int base = 0; base < ctx; base += NTH) {
         if (base > 0) {
 #pragma unroll
             for (int u = 0; u < VB; u++) {
-                const int t = base + tg + 8 * u;
+                const int t = base + tg + 32 * u;
                 vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
             }
         }
 #pragma unroll
         for (int u = 0; u < VB; u++) {
-            const int t = base + tg + 8 * u;
+            const int t = base + tg + 32 * u;
             if (t < ctx) {
-                const float w = p[t];
-                o.x = fmaf(w, vv[u].x, o.x); o.y = fmaf(w, vv[u].y, o.y);
-                o.z = fmaf(w, vv[u].z, o.z); o.w = fmaf(w, vv[u].w, o.w);
+                const float w0 = p[t], w1 = p[max_seq + t];
+                o0.x = fmaf(w0, vv[u].x, o0.x); o0.y = fmaf(w0, vv[u].y, o0.y);
+                o0.z = fmaf(w0, vv[u].z, o0.z); o0.w = fmaf(w0, vv[u].w, o0.w);
+                o1.x = fmaf(w1, vv[u].x, o1.x); o1.y = fmaf(w1, vv[u].y, o1.y);
+                o1.z = fmaf(w1, vv[u].z, o1.z); o1.w = fmaf(w1, vv[u].w, o1.w);
             }
         }
     }
-    reinterpret_cast<f32x4 *>(red + tg * HD)[d4] = o;
+    reinterpret_cast<f32x4 *>(red + (tg * GRP + 0) * DQW)[c4] = o0;
+    reinterpret_cast<f32x4 *>(red + (tg * GRP + 1) * DQW)[c4] = o1;
     __syncthreads();
-    if (tid < HD) {
+    if (tid < GRP * DQW) {
+        const int h = tid / DQW, d = tid % DQW;
         float sacc = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; k++) sacc += red[k * HD + tid];
-        out[(size_t)hq * HD + tid] = sacc * inv;
+#pragma unroll 8
+        for (int k = 0; k < 32; k++) sacc += red[(k * GRP + h) * DQW + d];
+        out[(size_t)(g * GRP + h) * HD + q * DQW + d] = sacc * (h ? inv1 : inv0);
     }
 }
 
@@ -474,7 +501,7 @@ extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const 
 }
 
 extern "C" size_t qm_attention_decode_lds_bytes(int max_seq) {
-    return sizeof(float) * ((size_t)2 * HD + 8 * HD + 8 + (size_t)max_seq);
+    return sizeof(float) * ((size_t)GRP * HD + HD + 32 * GRP * DQW + 16 + (size_t)GRP * max_seq);
 }
 
 extern "C" int qm_attention_decode(const float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
@@ -484,8 +511,15 @@ extern "C" int qm_attention_decode(const float *qkv, float *out, float *kc, floa
     if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
     const size_t lds = qm_attention_decode_lds_bytes(max_seq);
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void *)k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)qm_attention_decode_lds_bytes(QM_MAX_SEQ)) != hipSuccess)
+            return QH_ELAUNCH;
+        attr_set = true;
+    }
     const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
-    hipLaunchKernelGGL(k_attn_decode, dim3(GRP * NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn,
+    hipLaunchKernelGGL(k_attn_decode, dim3(DQ * NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn,
                        rcos, rsin, pos_d, max_seq, eps, scale);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
