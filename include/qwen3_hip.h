@@ -123,6 +123,17 @@ int qwen3_hip_gemm_dev(float *c_d, const float *a_d, const uint16_t *b_d,
 int qwen3_hip_gemm_gate_up_silu_dev(float *h_d, const float *x_d,
                                     const uint16_t *wg_d, const uint16_t *wu_d,
                                     int M, int K, int N);
+/* The same two products with A already bf16 (uint16_t bits, [M,K]
+ * row-major): for callers that hold bf16 activations, so no rounding pass
+ * is needed.  Results equal the fp32-A calls on A = bf16(A).  Large-tile
+ * MFMA kernels; K % 64 == 0 and 16-byte aligned pointers, else
+ * QWEN3_HIP_EINVAL.  No counterpart in the reference ABI
+ * (SRC/kernels.h:44-57 takes fp32 A only). */
+int qwen3_hip_gemm_bf16a_dev(float *c_d, const uint16_t *a_d, const uint16_t *b_d,
+                             int M, int K, int N);
+int qwen3_hip_gemm_gate_up_silu_bf16a_dev(float *h_d, const uint16_t *x_d,
+                                          const uint16_t *wg_d, const uint16_t *wu_d,
+                                          int M, int K, int N);
 /* device counterpart of qwen3_op_argmax (SRC/ops.h:36-37,
  * SRC/ops_scalar.c:57-62): first index of the maximum, ties -> lowest index,
  * a NaN at index 0 wins as in the reference's strict ">" scan */

@@ -143,6 +143,18 @@ def gemm_gate_up_silu_dev(h_d, x_d, wg_d, wu_d, M, K, N):
           "qwen3_hip_gemm_gate_up_silu_dev")
 
 
+def gemm_bf16a_dev(c_d, a_d, b_d, M, K, N):
+    """C = A.B^T with A already bf16 bits on the device (K % 64 == 0)."""
+    check(runtime.lib().qwen3_hip_gemm_bf16a_dev(VP(c_d), VP(a_d), VP(b_d), M, K, N),
+          "qwen3_hip_gemm_bf16a_dev")
+
+
+def gemm_gate_up_silu_bf16a_dev(h_d, x_d, wg_d, wu_d, M, K, N):
+    check(runtime.lib().qwen3_hip_gemm_gate_up_silu_bf16a_dev(VP(h_d), VP(x_d), VP(wg_d), VP(wu_d),
+                                                              M, K, N),
+          "qwen3_hip_gemm_gate_up_silu_bf16a_dev")
+
+
 def argmax_dev(out_d, v_d, n):
     check(runtime.lib().qwen3_hip_argmax_dev(VP(out_d), VP(v_d), n), "qwen3_hip_argmax_dev")
 
@@ -166,4 +178,5 @@ PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4
          "ring32x64k64s6": 15, "ring64x64k32s6": 16, "ring32x64k32s4": 17,
          "pipe32x64k128s3": 18, "pipe32x64k128s4": 19, "pipe64x64k128s3": 20, "pipe64x64k64s4": 21,
          "pipe64x128k64s4": 22, "pipe128x128k64s3": 23, "pipe128x64k64s3": 24, "pipe32x64k64s4": 25,
-         "pipe64x64k64s3": 26}
+         "pipe64x64k64s3": 26, "xl128x256": 27, "xl256x256": 28, "xl256x128": 29, "xl128x128": 30, "xl128x256k32": 31, "xl256x128k32": 32,
+         "xb256x256": 33, "xb256x256k32": 34, "xb128x256": 35, "xb256x128": 36, "xb128x128": 37}

@@ -36,11 +36,12 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
 
-// two fp32 -> packed bf16 pair (low half = first), RNE (v_cvt_pk_bf16_f32)
+// two fp32 -> packed bf16 pair (low half = first), RNE: one v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
-    uint32_t lo = __builtin_bit_cast(uint16_t, (__bf16)x);
-    uint32_t hi = __builtin_bit_cast(uint16_t, (__bf16)y);
-    return lo | (hi << 16);
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t f = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
 }
 __device__ __forceinline__ float round_bf16(float x) {
     return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
@@ -1122,6 +1123,333 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 }
 
 // ---------------------------------------------------------------------------
+// Large-tile MFMA GEMM: 32x32x16 bf16 MFMA, 2 x 2 waves, two stages in flight
+// ---------------------------------------------------------------------------
+// Block tile BM x BN, k stages of BK (32 or 64).  Each wave owns a
+// (BM/2) x (BN/2) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
+// Operands move global -> registers -> LDS with 16-byte buffer loads (a
+// fixed 32-bit offset per lane and load, the stage's k offset in a scalar
+// register): A as fp32, rounded to bf16 (RNE) on the way into LDS; B as
+// bf16.  Registers hold two stages (two sets), LDS two slots; stage `it` is
+// one scheduling region in which the MFMAs of stage it (fragments from slot
+// it&1), the loads of stage it+2 and the conversion and LDS stores of stage
+// it+1 (into the other slot) are interleaved, followed by one barrier.
+// With one wave per SIMD the MFMA pipe only stays busy if the loads and
+// stores issue between MFMAs; run back to back they leave it idle half the
+// time.  Two stages of loads stay in flight, which covers the ~1 us load
+// latency seen under load.
+// Register sets and LDS slots are picked at compile time (loop unrolled by
+// two; each slot is its own LDS array), so the compiler can tell that the
+// stores of stage it+1 do not touch what the MFMAs of stage it read, and its
+// wait analysis follows each register.
+// LDS rows are BK bf16 (CPR = BK/8 chunks of 16 bytes); chunk c of row r
+// sits at slot c ^ f(r), f chosen so that the 32-row fragment reads are
+// conflict-free at both 8 lanes per 128-byte pass and 16 lanes per 256-byte
+// pass.
+// Per block per stage the CU moves (4*BM + 2*BN)*BK bytes through its vector
+// memory path for 2*BM*BN*BK flops: 256 x 256 tiles need 3/256 byte per
+// flop, inside the ~64 B/clk a CU loads against its 4096 flop/clk.
+// Requires K % BK == 0, 16-byte aligned a, b, b2, and fewer than 2^32 bytes
+// in A and in each weight matrix.  Rows >= M and columns >= N are clamped for
+// loading and never stored.
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false>
+struct XlCfg {
+    static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
+    static constexpr int WTM = BM / 2, WTN = BN / 2;            // wave tile
+    static constexpr int TM = WTM / 32, TN = WTN / 32;          // 32x32 blocks per wave
+    static constexpr int BNO = GATED ? BN / 2 : BN;             // output columns per block
+    static constexpr int A_SLOT = BM * BK * 2, B_SLOT = BN * BK * 2;
+    static constexpr int LDS = 2 * (A_SLOT + B_SLOT);
+    static constexpr int A_CPR = ABF16 ? CPR : BK / 4;          // 16-byte A chunks per row
+    static constexpr int A_LOADS = BM * A_CPR / NTHREADS;       // 16-byte A loads per lane
+    static constexpr int B_LOADS = BN * CPR / NTHREADS;         // 16-byte bf16 loads per lane
+    static constexpr int B_ROWS_PER_LOAD = NTHREADS / CPR;
+    static constexpr int MFMAS = TM * TN * (BK / 16);           // per wave per stage
+    static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
+    static_assert(BK == 32 || BK == 64, "k stage");
+    static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
+    static_assert(A_LOADS >= 1 && B_LOADS >= 1, "loads per lane");
+    static_assert(!GATED || BNO % B_ROWS_PER_LOAD == 0, "a load never mixes Wg and Wu rows");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <int CPR>
+__device__ __forceinline__ int xl_swz(int r) {
+    if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
+    else return ((r >> 1) ^ (r >> 3)) & 3;
+}
+
+// B-tile row of 32-column block j of wave column wn (gated: the first TN/2
+// blocks are Wg rows, the rest the Wu rows of the same outputs)
+template <int BN, int TN, bool GATED>
+__device__ __forceinline__ int xl_brow(int wn, int j) {
+    if constexpr (!GATED) {
+        return wn * (BN / 2) + 32 * j;
+    } else {
+        constexpr int TNO = TN / 2;
+        const int base = wn * (BN / 4);
+        return (j < TNO) ? base + 32 * j : BN / 2 + base + 32 * (j - TNO);
+    }
+}
+
+// Scheduling pattern of one stage (one wave's instruction order).  The
+// fragments of the first k-step are read first; then every MFMA is followed
+// by its share of: the fragment reads of the next k-step (spread over the
+// MFMAs of the k-step before), the global loads (first half of the MFMAs)
+// and the LDS stores (second half).  Waiting on a fragment read right before
+// its MFMA would expose the LDS latency on every MFMA pair.
+template <int N, int SLOTS, int I>
+struct XlShare {   // how many of N items go after MFMA I of SLOTS (even spread)
+    static constexpr int v = ((I + 1) * N) / SLOTS - (I * N) / SLOTS;
+};
+template <int I, int MFMAS, int KS, int FR, int LOADS>
+struct XlSched {
+    static constexpr int PER_K = MFMAS / KS;           // MFMAs per k-step
+    static constexpr int H = MFMAS / 2;
+    static __device__ __forceinline__ void run() {
+        if constexpr (I == 0) __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);   // first fragments
+        if constexpr (I < MFMAS) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
+            if constexpr (I < MFMAS - PER_K) {                                      // next fragments
+                constexpr int n = XlShare<FR * (KS - 1), MFMAS - PER_K, I>::v;
+                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+            }
+            if constexpr (I < H) {
+                constexpr int n = XlShare<LOADS, H, I>::v;
+                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);   // global loads
+            } else {
+                constexpr int n = XlShare<LOADS, MFMAS - H, I - H>::v;
+                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x200, n, 0);   // LDS stores
+            }
+            XlSched<I + 1, MFMAS, KS, FR, LOADS>::run();
+        }
+    }
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t bytes) {
+    // raw buffer: stride 0, num_records = bytes, default data format
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+
+// ABF16: A is already bf16 (a points to uint16_t bits): it is copied into LDS
+// like B, with no conversion.
+template <int BM, int BN, int BK, bool GATED, bool ABF16>
+__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_xl(float *__restrict__ c,
+                                                        const void *__restrict__ a,
+                                                        const uint16_t *__restrict__ b,
+                                                        const uint16_t *__restrict__ b2,
+                                                        int M, int K, int N, TileMap map) {
+    using X = XlCfg<BM, BN, BK, GATED, ABF16>;
+    constexpr int CPR = X::CPR;
+    __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
+    __shared__ __align__(16) unsigned char sa1[X::A_SLOT];
+    __shared__ __align__(16) unsigned char sb0[X::B_SLOT];
+    __shared__ __align__(16) unsigned char sb1[X::B_SLOT];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_of(blockIdx.x, map, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * X::BNO;
+    const int nk = K / BK;
+
+    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * (ABF16 ? 2 : 4));
+    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = GATED ? xl_rsrc(b2, (size_t)N * K * 2) : rb;
+
+    // A: load i of this lane is fp32 chunk q = i*256 + tid of the tile (BK/4
+    // chunks of 4 floats per row); B: bf16 chunk q (CPR chunks of 8 per row)
+    uint32_t aoffs[X::A_LOADS];
+    int adst[X::A_LOADS];
+#pragma unroll
+    for (int i = 0; i < X::A_LOADS; i++) {
+        const int q = i * NTHREADS + tid;
+        const int r = q / X::A_CPR, cq = q % X::A_CPR;
+        const uint32_t row = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K;
+        if constexpr (ABF16) {
+            aoffs[i] = (row + (uint32_t)cq * 8u) * 2u;
+            adst[i] = r * (BK * 2) + ((cq ^ xl_swz<CPR>(r)) << 4);
+        } else {
+            aoffs[i] = (row + (uint32_t)cq * 4u) * 4u;
+            adst[i] = r * (BK * 2) + (((cq >> 1) ^ xl_swz<CPR>(r)) << 4) + ((cq & 1) << 3);
+        }
+    }
+    uint32_t boffs[X::B_LOADS];
+    int bdst[X::B_LOADS];
+#pragma unroll
+    for (int i = 0; i < X::B_LOADS; i++) {
+        const int q = i * NTHREADS + tid;
+        const int r = q / CPR, ch = q % CPR;
+        int gn = n0 + r;
+        if constexpr (GATED) {
+            if (i * X::B_ROWS_PER_LOAD >= X::BNO) gn = n0 + r - X::BNO;   // Wu rows
+        }
+        boffs[i] = ((uint32_t)min(gn, N - 1) * (uint32_t)K + (uint32_t)ch * 8u) * 2u;
+        bdst[i] = r * (BK * 2) + ((ch ^ xl_swz<CPR>(r)) << 4);
+    }
+
+    // fragment read offsets (bytes within an A / B slot) and swizzles
+    const int lrow = lane & 31, lk = lane >> 5;
+    int aoff[X::TM], asw[X::TM], boff[X::TN], bsw[X::TN];
+#pragma unroll
+    for (int i = 0; i < X::TM; i++) {
+        const int r = wm * X::WTM + 32 * i + lrow;
+        aoff[i] = r * (BK * 2);
+        asw[i] = xl_swz<CPR>(r);
+    }
+#pragma unroll
+    for (int j = 0; j < X::TN; j++) {
+        const int r = xl_brow<BN, X::TN, GATED>(wn, j) + lrow;
+        boff[j] = r * (BK * 2);
+        bsw[j] = xl_swz<CPR>(r);
+    }
+
+    u32x4 areg[2][X::A_LOADS];
+    u32x4 breg[2][X::B_LOADS];
+    // SET: register set and LDS slot, both compile-time
+    auto load = [&](int step, auto SET) {
+        constexpr int set = decltype(SET)::value;
+        const int ka = step * BK * (ABF16 ? 2 : 4), kb = step * BK * 2;   // scalar byte offsets
+#pragma unroll
+        for (int i = 0; i < X::A_LOADS; i++)
+            areg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoffs[i], ka, 0);
+#pragma unroll
+        for (int i = 0; i < X::B_LOADS; i++) {
+            const bool up = GATED && i * X::B_ROWS_PER_LOAD >= X::BNO;
+            breg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(up ? rb2 : rb, boffs[i], kb, 0);
+        }
+    };
+    auto store = [&](auto SET) {
+        constexpr int set = decltype(SET)::value;
+        unsigned char *as = set ? sa1 : sa0;
+        unsigned char *bs = set ? sb1 : sb0;
+#pragma unroll
+        for (int i = 0; i < X::A_LOADS; i++) {
+            if constexpr (ABF16) {
+                *reinterpret_cast<u32x4 *>(as + adst[i]) = areg[set][i];
+            } else {
+                const f32x4 x = __builtin_bit_cast(f32x4, areg[set][i]);
+                uint2 w;
+                w.x = pack_bf16x2(x.x, x.y);
+                w.y = pack_bf16x2(x.z, x.w);
+                *reinterpret_cast<uint2 *>(as + adst[i]) = w;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < X::B_LOADS; i++)
+            *reinterpret_cast<u32x4 *>(bs + bdst[i]) = breg[set][i];
+    };
+
+    typedef float f32x16 __attribute__((ext_vector_type(16)));
+    f32x16 acc[X::TM][X::TN];
+#pragma unroll
+    for (int i = 0; i < X::TM; i++)
+#pragma unroll
+        for (int j = 0; j < X::TN; j++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
+
+    // fragments double-buffered across k-steps: those of k-step t+1 are read
+    // while the MFMAs of k-step t run
+    auto compute = [&](auto SET) {
+        constexpr int set = decltype(SET)::value;
+        constexpr int KS = BK / 16;
+        const unsigned char *as = set ? sa1 : sa0;
+        const unsigned char *bs = set ? sb1 : sb0;
+        bf16x8 fa[2][X::TM], fb[2][X::TN];
+        auto read = [&](int t, int f) {
+            const int ch = 2 * t + lk;
+#pragma unroll
+            for (int i = 0; i < X::TM; i++)
+                fa[f][i] = *reinterpret_cast<const bf16x8 *>(as + aoff[i] + ((ch ^ asw[i]) << 4));
+#pragma unroll
+            for (int j = 0; j < X::TN; j++)
+                fb[f][j] = *reinterpret_cast<const bf16x8 *>(bs + boff[j] + ((ch ^ bsw[j]) << 4));
+        };
+        read(0, 0);
+#pragma unroll
+        for (int t = 0; t < KS; t++) {
+            if (t + 1 < KS) read(t + 1, (t + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < X::TM; i++)
+#pragma unroll
+                for (int j = 0; j < X::TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[t & 1][i], fb[t & 1][j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // prologue: stages 0 and 1 in flight, stage 0 stored
+    load(0, IC<0>{});
+    if (nk > 1) load(1, IC<1>{});
+    store(IC<0>{});
+    __syncthreads();
+
+    // steady state (it + 2 < nk): SET = it & 1.  The loads are unconditional
+    // here (conditional loads make the compiler's wait analysis wait for all
+    // of them).
+    auto steady = [&](int it, auto SET) {
+        constexpr int set = decltype(SET)::value;
+        load(it + 2, IC<set>{});
+        compute(IC<set>{});
+        store(IC<set ^ 1>{});
+        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS>::run();
+        __syncthreads();
+    };
+    auto tail = [&](int it, auto SET) {
+        constexpr int set = decltype(SET)::value;
+        if (it + 2 < nk) load(it + 2, IC<set>{});
+        compute(IC<set>{});
+        if (it + 1 < nk) store(IC<set ^ 1>{});
+        __syncthreads();
+    };
+    int it = 0;
+    for (; it + 3 < nk; it += 2) {
+        steady(it, IC<0>{});
+        steady(it + 1, IC<1>{});
+    }
+    // 1 to 3 stages left, it even
+    tail(it, IC<0>{});
+    if (it + 1 < nk) tail(it + 1, IC<1>{});
+    if (it + 2 < nk) tail(it + 2, IC<0>{});
+
+    // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
+    // column lane%32
+#pragma unroll
+    for (int i = 0; i < X::TM; i++) {
+        const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
+        if constexpr (!GATED) {
+#pragma unroll
+            for (int j = 0; j < X::TN; j++) {
+                const int col = n0 + wn * X::WTN + 32 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int row = rbase + 8 * (v >> 2) + (v & 3);
+                        if (row < M) c[(size_t)row * N + col] = acc[i][j][v];
+                    }
+                }
+            }
+        } else {
+            constexpr int TNO = X::TN / 2;
+#pragma unroll
+            for (int j = 0; j < TNO; j++) {
+                const int col = n0 + wn * (X::BNO / 2) + 32 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int row = rbase + 8 * (v >> 2) + (v & 3);
+                        if (row < M) c[(size_t)row * N + col] = silu_mul(acc[i][j][v], acc[i][j + TNO][v]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // misc kernels
 // ---------------------------------------------------------------------------
 // dst[n][k] = src[tile(n,k)], tile-major as in kernels_ame.c:212-215,269
@@ -1195,6 +1523,22 @@ __global__ __launch_bounds__(NTHREADS) void k_copy16(u32x4 *__restrict__ dst,
         dst[i] = __builtin_nontemporal_load(src + i);
 }
 
+// dst[i] = bf16 RNE of src[i]; 8 elements per lane per step (n % 8 == 0,
+// 16-byte aligned src and dst)
+__global__ __launch_bounds__(NTHREADS) void k_cvt_bf16(uint16_t *__restrict__ dst,
+                                                       const float *__restrict__ src, size_t n8) {
+    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n8; i += (size_t)gridDim.x * NTHREADS) {
+        const f32x4 x0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src) + 2 * i);
+        const f32x4 x1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src) + 2 * i + 1);
+        u32x4 w;
+        w.x = pack_bf16x2(x0.x, x0.y);
+        w.y = pack_bf16x2(x0.z, x0.w);
+        w.z = pack_bf16x2(x1.x, x1.y);
+        w.w = pack_bf16x2(x1.z, x1.w);
+        reinterpret_cast<u32x4 *>(dst)[i] = w;
+    }
+}
+
 __global__ __launch_bounds__(NTHREADS) void k_fill_zero(float *__restrict__ c, size_t n) {
     for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n;
          i += (size_t)gridDim.x * NTHREADS)
@@ -1219,6 +1563,10 @@ static int g_capturing = 0;
 static float *g_am_v = nullptr;   // argmax partials (allocated at init)
 static int *g_am_i = nullptr;
 static const int AM_BLOCKS = 1024;
+// bf16 copy of an fp32 A for the large-tile GEMMs (grown outside graph capture)
+static uint16_t *g_abf = nullptr;
+static size_t g_abf_elems = 0;
+static const size_t ABF_INIT_ELEMS = (size_t)8192 * 3072;   // 48 MiB: M x K up to 8192 x 3072
 
 static int fail(hipError_t e, int code) {
     g_last_hip = e;
@@ -1259,6 +1607,8 @@ extern "C" int qh_init(int device) {
     HCHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), QH_ERUNTIME);
     HCHECK(hipMalloc((void **)&g_am_v, AM_BLOCKS * sizeof(float)), QH_ENOMEM);
     HCHECK(hipMalloc((void **)&g_am_i, AM_BLOCKS * sizeof(int)), QH_ENOMEM);
+    HCHECK(hipMalloc((void **)&g_abf, ABF_INIT_ELEMS * sizeof(uint16_t)), QH_ENOMEM);
+    g_abf_elems = ABF_INIT_ELEMS;
     g_device = device;
     g_inited = 1;
     return QH_OK;
@@ -1271,6 +1621,9 @@ extern "C" void qh_shutdown(void) {
         if (g_graph_exec[i]) { (void)hipGraphExecDestroy(g_graph_exec[i]); g_graph_exec[i] = nullptr; }
     for (int i = 0; i < 64; i++)
         if (g_ev_made[i]) { (void)hipEventDestroy(g_ev[i]); g_ev_made[i] = 0; }
+    (void)hipFree(g_abf);
+    g_abf = nullptr;
+    g_abf_elems = 0;
     (void)hipFree(g_am_v);
     (void)hipFree(g_am_i);
     g_am_v = nullptr;
@@ -1386,15 +1739,36 @@ enum {
     PLAN_P128x64k64s3 = 24,
     PLAN_P32x64k64s4 = 25,
     PLAN_P64x64k64s3 = 26,
-    PLAN_COUNT = 27
+    // large tiles, 32x32x16 MFMA (K % BK == 0)
+    PLAN_X128x256 = 27,        // BK 64
+    PLAN_X256x256 = 28,        // BK 32
+    PLAN_X256x128 = 29,        // BK 64
+    PLAN_X128x128 = 30,        // BK 64
+    PLAN_X128x256k32 = 31,
+    PLAN_X256x128k32 = 32,
+    // A converted to bf16 by one extra pass, then bf16 x bf16 large tiles
+    PLAN_XB256x256 = 33,       // BK 64
+    PLAN_XB256x256k32 = 34,
+    PLAN_XB128x256 = 35,       // BK 64
+    PLAN_XB256x128 = 36,       // BK 64
+    PLAN_XB128x128 = 37,       // BK 64
+    PLAN_COUNT = 38
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
     "ring32x64k128s4", "ring64x64k64s4", "ring64x64k64s6", "ring64x64k128s3", "ring64x128k64s4",
     "ring128x128k64s3", "ring128x64k64s3", "ring32x64k64s6", "ring64x64k32s6", "ring32x64k32s4",
     "pipe32x64k128s3", "pipe32x64k128s4", "pipe64x64k128s3", "pipe64x64k64s4", "pipe64x128k64s4",
-    "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3"};
-static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p < PLAN_COUNT; }
+    "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
+    "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
+    "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128"};
+static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
+static inline bool is_xl_plan(int p) { return p >= PLAN_X128x256 && p <= PLAN_XB128x128; }
+static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256 && p <= PLAN_XB128x128; }
+static inline int xl_bk(int p) {
+    return (p == PLAN_X256x256 || p == PLAN_X128x256k32 || p == PLAN_X256x128k32 ||
+            p == PLAN_XB256x256k32) ? 32 : 64;
+}
 static inline int ring_bk(int p) {
     switch (p) {
         case PLAN_R32x64k128s4: case PLAN_R64x64k128s3:
@@ -1405,6 +1779,18 @@ static inline int ring_bk(int p) {
 }
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// bf16-A shapes: 256 x 256 tiles when they fill the chip, else the smaller
+// tiles (measured on MI355X for the Qwen3-0.6B projection shapes)
+static int choose_bf16a_plan(int M, int K, int N, int gated) {
+    (void)K;
+    const int bno = gated ? 2 : 1;
+    auto blocks = [&](int bm, int bn) {
+        return (long)((M + bm - 1) / bm) * (long)((N + bn / bno - 1) / (bn / bno));
+    };
+    if (!gated && blocks(256, 256) >= 256) return PLAN_XB256x256k32;
+    return PLAN_XB128x128;
+}
 
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
@@ -1419,6 +1805,19 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // CU); with 64-deep stages (64 KB, two blocks per CU) up to two rounds;
     // larger grids and large M do better with the register-staged 64- and
     // 128-wide tiles.
+    // Large-tile kernels (32x32x16 MFMA, two stages of loads in flight) win
+    // from M = 1024 on, and at M = 512 wherever 128 x 128 tiles still give
+    // half the chip a tile (fused q|k|v, gate|up): 256 x 256 when they fill
+    // all 256 CUs, gate|up from M = 2048 with A rounded to bf16 by one pass
+    // first, 128 x 128 otherwise.
+    if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
+        if (M >= 1024) {
+            if (!gated && blocks(256, 256) >= 256) return PLAN_X256x256;
+            if (gated && M >= 2048 && (size_t)M * K <= g_abf_elems) return PLAN_XB128x128;
+            return PLAN_X128x128;
+        }
+        if (M > 128 && blocks(128, 128) >= 128) return PLAN_X128x128;
+    }
     if (M <= 128 || (!gated && M <= 512)) {
         const long t = blocks(32, 64);
         if (K % 128 == 0 && t <= 256) return PLAN_P32x64k128s4;
@@ -1623,6 +2022,59 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     return QH_OK;
 }
 
+// requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
+// (checked by the caller)
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false>
+static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
+                     int M, int K, int N) {
+    using X = XlCfg<BM, BN, BK, GATED, ABF16>;
+    TileMap map;
+    const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
+    if (tiles < 0) return QH_ETOOBIG;
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16>), dim3((unsigned)tiles), dim3(NTHREADS), 0,
+                       g_stream, c, a, b, b2, M, K, N, map);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// fp32 -> bf16 (RNE) on the stream; n % 8 == 0, 16-byte aligned pointers
+static int launch_cvt_bf16(uint16_t *dst, const float *src, size_t n) {
+    const size_t n8 = n / 8;
+    size_t blocks = (n8 + NTHREADS - 1) / NTHREADS;
+    if (blocks > 2048) blocks = 2048;
+    if (blocks == 0) return QH_OK;
+    hipLaunchKernelGGL(k_cvt_bf16, dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream, dst, src, n8);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
+// bf16-A large-tile GEMM for plan p (an xb plan); a is bf16 bits
+template <bool GATED>
+static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b, const uint16_t *b2,
+                          int M, int K, int N) {
+    switch (p) {
+        case PLAN_XB256x256:    return launch_xl<256, 256, 64, GATED, true>(c, a, b, b2, M, K, N);
+        case PLAN_XB256x256k32: return launch_xl<256, 256, 32, GATED, true>(c, a, b, b2, M, K, N);
+        case PLAN_XB128x256:    return launch_xl<128, 256, 64, GATED, true>(c, a, b, b2, M, K, N);
+        case PLAN_XB256x128:    return launch_xl<256, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
+        case PLAN_XB128x128:    return launch_xl<128, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
+        default: return QH_EINVAL;
+    }
+}
+
+// the bf16 workspace holds at least n elements (grows only outside capture)
+static bool abf_ensure(size_t n) {
+    if (n <= g_abf_elems) return true;
+    if (g_capturing) return false;
+    uint16_t *p = nullptr;
+    if (hipMalloc((void **)&p, n * sizeof(uint16_t)) != hipSuccess) { (void)hipGetLastError(); return false; }
+    (void)hipStreamSynchronize(g_stream);      // the old buffer may still be read
+    (void)hipFree(g_abf);
+    g_abf = p;
+    g_abf_elems = n;
+    return true;
+}
+
 template <bool GATED>
 static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                     int M, int K, int N) {
@@ -1660,6 +2112,18 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_P128x64k64s3:  return launch_pipe<128, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P32x64k64s4:   return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P64x64k64s3:   return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_XB256x256: case PLAN_XB256x256k32: case PLAN_XB128x256: case PLAN_XB256x128:
+        case PLAN_XB128x128: {
+            const int rc = launch_cvt_bf16(g_abf, a, (size_t)M * K);
+            if (rc) return rc;
+            return dispatch_bf16a<GATED>(plan, c, g_abf, b, b2, M, K, N);
+        }
+        case PLAN_X128x256: return launch_xl<128, 256, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X256x128: return launch_xl<256, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X128x256k32: return launch_xl<128, 256, 32, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X256x128k32: return launch_xl<256, 128, 32, GATED>(c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
     }
 }
@@ -1685,8 +2149,41 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
     if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
     if (is_ring_plan(plan) && (K % ring_bk(plan)) != 0)           // ring copies whole k stages
         plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
+    if (is_xl_plan(plan) && ((K % xl_bk(plan)) != 0 ||           // xl copies whole k stages and
+                             (size_t)M * K * 4 >= (1ull << 32) ||   // addresses with 32-bit offsets
+                             (size_t)N * K * 2 >= (1ull << 32)))
+        plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
+    if (is_xb_plan(plan) && !abf_ensure((size_t)M * K))            // no room for the bf16 copy of A
+        plan = PLAN_X128x256;
     return gated ? dispatch<true>(plan, c, a, b, b2, M, K, N)
                  : dispatch<false>(plan, c, a, b, nullptr, M, K, N);
+}
+
+// C = A.B^T with A already bf16 (bits), for callers that hold bf16
+// activations: the large-tile kernels without the conversion pass.  Needs
+// K % 64 == 0 and 16-byte aligned a, b, b2.
+static int gemm_bf16a_common(float *c, const uint16_t *a, const uint16_t *b, const uint16_t *b2,
+                             int M, int K, int N, bool gated) {
+    if (!g_inited) return QH_ESTATE;
+    if (M < 0 || K < 0 || N < 0) return QH_EINVAL;
+    if (M == 0 || N == 0) return QH_OK;
+    if (!c || !a || !b || (gated && !b2)) return QH_EINVAL;
+    if (K % 64 != 0 || K == 0 || !aligned16(a) || !aligned16(b) || (gated && !aligned16(b2)))
+        return QH_EINVAL;
+    if ((size_t)M * K * 2 >= (1ull << 32) || (size_t)N * K * 2 >= (1ull << 32)) return QH_ETOOBIG;
+    int plan = g_forced_plan;
+    if (!is_xb_plan(plan)) plan = choose_bf16a_plan(M, K, N, gated);
+    return gated ? dispatch_bf16a<true>(plan, c, a, b, b2, M, K, N)
+                 : dispatch_bf16a<false>(plan, c, a, b, nullptr, M, K, N);
+}
+
+extern "C" int qh_gemm_bf16a(float *c, const uint16_t *a, const uint16_t *b, int M, int K, int N) {
+    return gemm_bf16a_common(c, a, b, nullptr, M, K, N, false);
+}
+
+extern "C" int qh_gemm_gate_up_silu_bf16a(float *h, const uint16_t *x, const uint16_t *wg,
+                                          const uint16_t *wu, int M, int K, int N) {
+    return gemm_bf16a_common(h, x, wg, wu, M, K, N, true);
 }
 
 extern "C" int qh_gemm(float *c, const float *a, const uint16_t *b, int M, int K, int N) {

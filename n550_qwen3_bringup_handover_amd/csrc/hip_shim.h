@@ -51,6 +51,12 @@ int qh_gemm(float *c_d, const float *a_d, const uint16_t *b_d,
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */
 int qh_gemm_gate_up_silu(float *h_d, const float *x_d, const uint16_t *wg_d,
                          const uint16_t *wu_d, int M, int K, int N);
+/* the same with A already bf16 bits [M,K] (no rounding pass): large-tile
+ * MFMA kernels; K % 64 == 0 and 16-byte aligned pointers */
+int qh_gemm_bf16a(float *c_d, const uint16_t *a_d, const uint16_t *b_d,
+                  int M, int K, int N);
+int qh_gemm_gate_up_silu_bf16a(float *h_d, const uint16_t *x_d, const uint16_t *wg_d,
+                               const uint16_t *wu_d, int M, int K, int N);
 /* tile-major [N/tn][K/tk][tn][tk] -> row-major [N][K] */
 int qh_tile_to_row(uint16_t *dst_d, const uint16_t *src_d, int N, int K,
                    int tile_n, int tile_k);

@@ -413,6 +413,17 @@ int qwen3_hip_gemm_gate_up_silu_dev(float *h, const float *x, const uint16_t *wg
     return note(qh_gemm_gate_up_silu(h, x, wg, wu, M, K, N));
 }
 
+int qwen3_hip_gemm_bf16a_dev(float *c, const uint16_t *a, const uint16_t *b, int M, int K, int N) {
+    READY_OR_RETURN();
+    return note(qh_gemm_bf16a(c, a, b, M, K, N));
+}
+
+int qwen3_hip_gemm_gate_up_silu_bf16a_dev(float *h, const uint16_t *x, const uint16_t *wg,
+                                          const uint16_t *wu, int M, int K, int N) {
+    READY_OR_RETURN();
+    return note(qh_gemm_gate_up_silu_bf16a(h, x, wg, wu, M, K, N));
+}
+
 int qwen3_hip_argmax_dev(int *out, const float *v, int n) {
     READY_OR_RETURN();
     return note(qh_argmax(out, v, n));

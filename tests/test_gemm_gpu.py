@@ -150,7 +150,7 @@ ALL_PLANS = [p for p in abi.PLANS if p != "auto"]
 
 @pytest.mark.parametrize("plan", ALL_PLANS)
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 384), (3, 520, 200), (77, 1024, 300), (200, 2048, 257),
-                                   (130, 96, 1000), (64, 32, 64)])
+                                   (130, 96, 1000), (64, 32, 64), (520, 1024, 600)])
 def test_every_kernel_variant(plan, M, K, N):
     """Force each kernel variant on the same shapes (the gemv plan only
     applies to M <= 4 and ring plans to K % 32 == 0; other cases fall back to
@@ -164,8 +164,8 @@ def test_every_kernel_variant(plan, M, K, N):
     numerics.compare(c, a, b, M, K, N, rows=numerics.pick_rows(M, 40))
 
 
-@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe")) or p == "gemv"])
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96)])
+@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe", "xl")) or p == "gemv"])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400)])
 def test_every_kernel_variant_gated(plan, M, K, N):
     x = oracle.f32_bf16_normal(M * K, 4100 + M)
     wg = oracle.bf16_normal(N * K, 4101 + M, 0.02)
@@ -278,6 +278,64 @@ def test_device_api_matches_host_api():
     c_dev = cd.download(np.float32, M * N)
     c_host = run_gemm(a, b, M, K, N)
     assert np.array_equal(c_dev.view(np.uint32), c_host.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,N", [(300, 1024, 640), (1024, 2048, 1024), (77, 64, 130)])
+def test_bf16a_entry_matches_fp32a_path(M, K, N):
+    """A given as bf16 bits equals the fp32-A call on the same (bf16-valued) A:
+    bit for bit on the same kernel plan, and within the GEMM bounds of the
+    oracle on the automatic plan."""
+    a, b = inputs(M, K, N, 950 + M)
+    a_bits = oracle.f32_to_bf16(a)
+    ad, bd = abi.DeviceBuffer.from_array(a_bits), abi.DeviceBuffer.from_array(b)
+    cd = abi.DeviceBuffer(M * N * 4)
+    abi.gemm_bf16a_dev(cd.ptr, ad.ptr, bd.ptr, M, K, N)
+    abi.sync()
+    c_auto = cd.download(np.float32, M * N)
+    numerics.compare(c_auto, a, b, M, K, N, rows=numerics.pick_rows(M, 40))
+    for plan in ("xb128x128", "xb256x256k32"):
+        abi.force_plan(abi.PLANS[plan])
+        try:
+            abi.gemm_bf16a_dev(cd.ptr, ad.ptr, bd.ptr, M, K, N)
+            abi.sync()
+            c_b = cd.download(np.float32, M * N)
+            c_f = run_gemm(a, b, M, K, N)            # fp32 A: rounding pass + the same kernel
+        finally:
+            abi.force_plan(0)
+        assert np.array_equal(c_b.view(np.uint32), c_f.view(np.uint32)), plan
+
+
+def test_bf16a_gated_and_rejects_bad_k():
+    M, K, N = 600, 1024, 384
+    x = oracle.f32_bf16_normal(M * K, 960)
+    wg = oracle.bf16_normal(N * K, 961, 0.02)
+    wu = oracle.bf16_normal(N * K, 962, 0.02)
+    xd = abi.DeviceBuffer.from_array(oracle.f32_to_bf16(x))
+    gd, ud = abi.DeviceBuffer.from_array(wg), abi.DeviceBuffer.from_array(wu)
+    hd = abi.DeviceBuffer(M * N * 4)
+    abi.gemm_gate_up_silu_bf16a_dev(hd.ptr, xd.ptr, gd.ptr, ud.ptr, M, K, N)
+    abi.sync()
+    numerics.compare_gated(hd.download(np.float32, M * N), x, wg, wu, M, K, N,
+                           rows=numerics.pick_rows(M, 24))
+    with pytest.raises(runtime.Qwen3HipError):
+        abi.gemm_bf16a_dev(hd.ptr, xd.ptr, gd.ptr, 8, 96, 16)     # K % 64 != 0
+
+
+@pytest.mark.parametrize("M,K,N,gated", [(1024, 1024, 4096, False), (2048, 1024, 3072, True),
+                                         (1536, 3072, 1024, False)])
+def test_large_m_automatic_plans(M, K, N, gated):
+    """The plans chosen from M = 1024 on (256 x 256 tiles, bf16 rounding pass
+    + 128 x 128 tiles for gate|up, 128 x 128) on a row subset."""
+    a = oracle.f32_bf16_normal(M * K, 970 + M)
+    if not gated:
+        b = oracle.bf16_normal(N * K, 971, 0.02)
+        numerics.compare(run_gemm(a, b, M, K, N), a, b, M, K, N, rows=numerics.pick_rows(M, 24))
+    else:
+        wg = oracle.bf16_normal(N * K, 972, 0.02)
+        wu = oracle.bf16_normal(N * K, 973, 0.02)
+        h = np.full(M * N, np.nan, np.float32)
+        abi.gemm_gate_up_silu(h, a, wg, wu, M, K, N)
+        numerics.compare_gated(h, a, wg, wu, M, K, N, rows=numerics.pick_rows(M, 16))
 
 
 def test_results_are_deterministic():
