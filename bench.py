@@ -13,8 +13,10 @@ fp32 outputs of the 197 reference GEMV calls).  value = steps per second =
 decode tokens/s of the GEMV set.
 
 Also reported: per-kernel launch times (HIP events on the library stream),
-the roofline fraction of the dominant kernel, prefill GEMM TFLOP/s at
-M = 512 (fused gate/up included), a CPU baseline: the reference's portable
+the roofline fraction of the dominant kernel, the GEMM tables of the other
+configurations (M = 16 gate_proj; M = 512 projections warm and cold, fused
+gate/up included; M = 1024 .. 4096; M = 64 batched decode incl. the
+64 x 1024 x 151936 lm_head), a CPU baseline: the reference's portable
 scalar GEMM (fpga_bringup/src/src/kernels_scalar.c, compiled from its source
 into oracle/_ref) running the same step on 1 host core, and the full
 device-resident Qwen3-0.6B forward (128-token prefill + 128 greedy decode
@@ -417,32 +419,75 @@ def kernel_classes(g, layers, emb, act):
     return out
 
 
-def prefill_gemms(g):
-    """M = 512 projections (warm: operands resident in L2/MALL)"""
-    M = 512
-    res = {}
-    a = g.alloc(4 * M * I)
-    g.fill_f32(a, M * I, 21)
-    c = g.alloc(4 * M * 2 * I)
-    wmax = g.alloc(2 * 2 * I * H)
-    g.fill_bf16(wmax, 2 * I * H, 22)
-    for name, K, N, gated in (("q", H, Q, False), ("k", H, KV, False), ("o", Q, H, False),
-                              ("gate_up_silu", H, I, True), ("down", I, H, False)):
-        if gated:
-            fn = lambda r, K=K, N=N: g.gated(c, a, wmax, wmax + 2 * I * H, M, K, N)
-            flops = 2.0 * M * 2 * N * K
-            byts = 2 * 2 * N * K + 4 * M * K + 4 * M * N
-        else:
-            fn = lambda r, K=K, N=N: g.gemm(c, a, wmax, M, K, N)
-            flops = 2.0 * M * N * K
-            byts = 2 * N * K + 4 * M * K + 4 * M * N
-        ms = time_launches_graph(g, fn, 32)
-        tf = flops / (ms * 1e-3) / 1e12
-        res[name] = {"M": M, "K": K, "N": N, "kernel": g.plan(M, K, N, gated),
-                     "us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
-                     "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "cold_hbm_cap": round(min(1.0, flops / byts / (MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9))), 3)}
-    return res
+def gemm_entry(g, M, K, N, gated, a, c, w, wrot=None, reps=32):
+    """time one GEMM shape on the automatic plan: graph of back-to-back
+    launches (each launch includes its ~1.6 us dependent-launch gap).  With
+    wrot, launch r uses weight copy r % len(wrot) (cold: the copies exceed
+    the 256 MB last-level cache)."""
+    ws = wrot or [w]
+    if gated:
+        fn = lambda r: g.gated(c, a, ws[r % len(ws)], ws[r % len(ws)] + 2 * N * K, M, K, N)
+        flops = 2.0 * M * 2 * N * K
+        byts = 2 * 2 * N * K + 4 * M * K + 4 * M * N
+    else:
+        fn = lambda r: g.gemm(c, a, ws[r % len(ws)], M, K, N)
+        flops = 2.0 * M * N * K
+        byts = 2 * N * K + 4 * M * K + 4 * M * N
+    ms = time_launches_graph(g, fn, reps)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"M": M, "K": K, "N": N, "gated": gated, "kernel": g.plan(M, K, N, gated),
+            "us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+            "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "cold_hbm_cap": round(min(1.0, flops / byts / (MFMA_BF16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9))), 3)}
+
+
+# projection shapes (K, N, gated); qkv is the fused q|k|v the forward uses
+SHAPES = {"q": (H, Q, False), "k_v": (H, KV, False), "o": (Q, H, False),
+          "gate_up_silu": (H, I, True), "down": (I, H, False), "qkv_fused": (H, Q + 2 * KV, False)}
+
+
+def gemm_tables(g):
+    """BASELINE configs 1, 3 and 5 plus an M sweep, on the automatic plans.
+    Warm: the same operands every launch (resident in L2/MALL); config 3
+    also cold, rotating through weight copies larger than the last-level
+    cache."""
+    Mmax = 4096
+    a = g.alloc(4 * Mmax * I)
+    g.fill_f32(a, Mmax * I, 21)
+    c = g.alloc(4 * Mmax * (Q + 2 * KV))
+    w = g.alloc(2 * 2 * I * H)
+    g.fill_bf16(w, 2 * I * H, 22)
+    out = {}
+    # config 1: one gate_proj GEMM at M = 16 (HBM-bound)
+    out["cfg1_m16_gate_proj"] = gemm_entry(g, 16, H, I, False, a, c, w)
+    # config 3: M = 512, warm and cold
+    ncopy = 48                                   # 48 x 12.6 MB = 604 MB of weights
+    wrot = [g.alloc(2 * 2 * I * H) for _ in range(ncopy)]
+    for p in wrot:
+        g.fill_bf16(p, 2 * I * H, 23)
+    cfg3 = {}
+    for name, (K, N, gated) in SHAPES.items():
+        cfg3[name] = gemm_entry(g, 512, K, N, gated, a, c, w)
+        cfg3[name]["cold_us"] = gemm_entry(g, 512, K, N, gated, a, c, w, wrot=wrot, reps=ncopy)["us"]
+    out["cfg3_m512"] = cfg3
+    # M sweep (warm)
+    sweep = {}
+    for M in (1024, 2048, 4096):
+        sweep[str(M)] = {name: gemm_entry(g, M, K, N, gated, a, c, w) for name, (K, N, gated) in SHAPES.items()}
+    out["m_sweep"] = sweep
+    # config 5: one GPU's share of batched decode, M = 64, incl. lm_head 64 x 1024 x 151936
+    emb = g.alloc(2 * V * H)
+    g.fill_bf16(emb, V * H, 24)
+    cfg5 = {name: gemm_entry(g, 64, K, N, gated, a, c, w) for name, (K, N, gated) in SHAPES.items()}
+    cl = g.alloc(4 * 64 * V)
+    cfg5["lm_head"] = gemm_entry(g, 64, H, V, False, a, cl, emb, reps=16)
+    layer_us = sum(cfg5[n]["us"] for n in ("qkv_fused", "o", "gate_up_silu", "down"))
+    cfg5["step_us"] = round(LAYERS * layer_us + cfg5["lm_head"]["us"], 1)
+    cfg5["tok_s_projections"] = round(64 / (cfg5["step_us"] * 1e-6), 1)
+    out["cfg5_m64"] = cfg5
+    return out
 
 
 def read_traffic(kernel):
@@ -468,7 +513,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extras", action="store_true", help="skip per-kernel and prefill tables")
+    ap.add_argument("--no-extras", action="store_true", help="skip per-kernel and GEMM tables")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the 113 kernels of a step one by one instead of replaying a graph")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -532,7 +577,7 @@ def main():
                     "traffic": read_traffic(dom),
                     "bytes_per_launch": d["bytes_per_launch"],
                     "us_per_launch": round(d["us_per_launch"], 3)}
-    prefill = None if args.no_extras else prefill_gemms(g)
+    gemms = None if args.no_extras else gemm_tables(g)
     if args.calibrate_copy:
         # a kernel of known traffic (64 MiB read + 64 MiB written per launch)
         # for scaling FETCH_SIZE / WRITE_SIZE counters in profiled runs
@@ -563,7 +608,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kclasses,
-        "prefill_m512": prefill,
+        "gemm": gemms,
         "model_cfg4": model,
         "host_pointer_path": hostp,
     }

@@ -179,4 +179,6 @@ PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4
          "pipe32x64k128s3": 18, "pipe32x64k128s4": 19, "pipe64x64k128s3": 20, "pipe64x64k64s4": 21,
          "pipe64x128k64s4": 22, "pipe128x128k64s3": 23, "pipe128x64k64s3": 24, "pipe32x64k64s4": 25,
          "pipe64x64k64s3": 26, "xl128x256": 27, "xl256x256": 28, "xl256x128": 29, "xl128x128": 30, "xl128x256k32": 31, "xl256x128k32": 32,
-         "xb256x256": 33, "xb256x256k32": 34, "xb128x256": 35, "xb256x128": 36, "xb128x128": 37}
+         "xb256x256": 33, "xb256x256k32": 34, "xb128x256": 35, "xb256x128": 36, "xb128x128": 37,
+         "xl64x256": 38, "xl64x128": 39,
+         "xl256x256s1": 40, "xb256x256s1": 41}

@@ -1152,7 +1152,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 // Requires K % BK == 0, 16-byte aligned a, b, b2, and fewer than 2^32 bytes
 // in A and in each weight matrix.  Rows >= M and columns >= N are clamped for
 // loading and never stored.
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false>
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 struct XlCfg {
     static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
     static constexpr int WTM = BM / 2, WTN = BN / 2;            // wave tile
@@ -1167,6 +1167,7 @@ struct XlCfg {
     static constexpr int MFMAS = TM * TN * (BK / 16);           // per wave per stage
     static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
     static_assert(BK == 32 || BK == 64, "k stage");
+    static_assert(SETS == 1 || SETS == 2, "register sets");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
     static_assert(A_LOADS >= 1 && B_LOADS >= 1, "loads per lane");
     static_assert(!GATED || BNO % B_ROWS_PER_LOAD == 0, "a load never mixes Wg and Wu rows");
@@ -1202,10 +1203,14 @@ template <int N, int SLOTS, int I>
 struct XlShare {   // how many of N items go after MFMA I of SLOTS (even spread)
     static constexpr int v = ((I + 1) * N) / SLOTS - (I * N) / SLOTS;
 };
-template <int I, int MFMAS, int KS, int FR, int LOADS>
+// STORE_FIRST (one register set): the stores of stage it+1 go in the first
+// half, the loads of stage it+2 (into the registers the stores freed) in the
+// second half.
+template <int I, int MFMAS, int KS, int FR, int LOADS, bool STORE_FIRST = false>
 struct XlSched {
     static constexpr int PER_K = MFMAS / KS;           // MFMAs per k-step
     static constexpr int H = MFMAS / 2;
+    static constexpr int FIRST = STORE_FIRST ? 0x200 : 0x020, SECOND = STORE_FIRST ? 0x020 : 0x200;
     static __device__ __forceinline__ void run() {
         if constexpr (I == 0) __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);   // first fragments
         if constexpr (I < MFMAS) {
@@ -1216,12 +1221,12 @@ struct XlSched {
             }
             if constexpr (I < H) {
                 constexpr int n = XlShare<LOADS, H, I>::v;
-                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x020, n, 0);   // global loads
+                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(FIRST, n, 0);
             } else {
                 constexpr int n = XlShare<LOADS, MFMAS - H, I - H>::v;
-                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x200, n, 0);   // LDS stores
+                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(SECOND, n, 0);
             }
-            XlSched<I + 1, MFMAS, KS, FR, LOADS>::run();
+            XlSched<I + 1, MFMAS, KS, FR, LOADS, STORE_FIRST>::run();
         }
     }
 };
@@ -1233,13 +1238,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t 
 
 // ABF16: A is already bf16 (a points to uint16_t bits): it is copied into LDS
 // like B, with no conversion.
-template <int BM, int BN, int BK, bool GATED, bool ABF16>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_xl(float *__restrict__ c,
+// 64-row tiles (batched decode) are bandwidth kernels: two blocks per CU
+// double the loads in flight
+// SETS = 1: one register set; each stage stores stage it+1 first and then
+// loads stage it+2 into the freed registers (one stage of latency cover, for
+// tiles whose two register sets would not fit).
+template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS>
+__global__ __launch_bounds__(NTHREADS, BM <= 64 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
                                                         int M, int K, int N, TileMap map) {
-    using X = XlCfg<BM, BN, BK, GATED, ABF16>;
+    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     constexpr int CPR = X::CPR;
     __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
     __shared__ __align__(16) unsigned char sa1[X::A_SLOT];
@@ -1307,11 +1317,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_xl(float *__restrict__ c,
         bsw[j] = xl_swz<CPR>(r);
     }
 
-    u32x4 areg[2][X::A_LOADS];
-    u32x4 breg[2][X::B_LOADS];
-    // SET: register set and LDS slot, both compile-time
+    u32x4 areg[SETS][X::A_LOADS];
+    u32x4 breg[SETS][X::B_LOADS];
+    // SET: register set (and, for store and compute, LDS slot), compile-time
     auto load = [&](int step, auto SET) {
-        constexpr int set = decltype(SET)::value;
+        constexpr int set = SETS == 1 ? 0 : decltype(SET)::value;
         const int ka = step * BK * (ABF16 ? 2 : 4), kb = step * BK * 2;   // scalar byte offsets
 #pragma unroll
         for (int i = 0; i < X::A_LOADS; i++)
@@ -1322,10 +1332,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_xl(float *__restrict__ c,
             breg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(up ? rb2 : rb, boffs[i], kb, 0);
         }
     };
-    auto store = [&](auto SET) {
-        constexpr int set = decltype(SET)::value;
-        unsigned char *as = set ? sa1 : sa0;
-        unsigned char *bs = set ? sb1 : sb0;
+    auto store = [&](auto SLOT) {
+        constexpr int slot = decltype(SLOT)::value;
+        constexpr int set = SETS == 1 ? 0 : slot;
+        unsigned char *as = slot ? sa1 : sa0;
+        unsigned char *bs = slot ? sb1 : sb0;
 #pragma unroll
         for (int i = 0; i < X::A_LOADS; i++) {
             if constexpr (ABF16) {
@@ -1381,28 +1392,47 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_xl(float *__restrict__ c,
         }
     };
 
-    // prologue: stages 0 and 1 in flight, stage 0 stored
-    load(0, IC<0>{});
-    if (nk > 1) load(1, IC<1>{});
-    store(IC<0>{});
+    // prologue: stage 0 stored, stage 1 (and with two sets stage 1 too)
+    // in flight
+    if constexpr (SETS == 2) {
+        load(0, IC<0>{});
+        if (nk > 1) load(1, IC<1>{});
+        store(IC<0>{});
+    } else {
+        load(0, IC<0>{});
+        store(IC<0>{});
+        if (nk > 1) load(1, IC<0>{});
+    }
     __syncthreads();
 
-    // steady state (it + 2 < nk): SET = it & 1.  The loads are unconditional
-    // here (conditional loads make the compiler's wait analysis wait for all
-    // of them).
+    // steady state (it + 2 < nk): SET = it & 1 is the LDS slot of stage it.
+    // The loads are unconditional here (conditional loads make the
+    // compiler's wait analysis wait for all of them).
     auto steady = [&](int it, auto SET) {
         constexpr int set = decltype(SET)::value;
-        load(it + 2, IC<set>{});
-        compute(IC<set>{});
-        store(IC<set ^ 1>{});
-        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS>::run();
+        if constexpr (SETS == 2) {
+            load(it + 2, IC<set>{});
+            compute(IC<set>{});
+            store(IC<set ^ 1>{});
+        } else {
+            store(IC<set ^ 1>{});
+            load(it + 2, IC<0>{});
+            compute(IC<set>{});
+        }
+        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS, SETS == 1>::run();
         __syncthreads();
     };
     auto tail = [&](int it, auto SET) {
         constexpr int set = decltype(SET)::value;
-        if (it + 2 < nk) load(it + 2, IC<set>{});
-        compute(IC<set>{});
-        if (it + 1 < nk) store(IC<set ^ 1>{});
+        if constexpr (SETS == 2) {
+            if (it + 2 < nk) load(it + 2, IC<set>{});
+            compute(IC<set>{});
+            if (it + 1 < nk) store(IC<set ^ 1>{});
+        } else {
+            if (it + 1 < nk) store(IC<set ^ 1>{});
+            if (it + 2 < nk) load(it + 2, IC<0>{});
+            compute(IC<set>{});
+        }
         __syncthreads();
     };
     int it = 0;
@@ -1752,7 +1782,13 @@ enum {
     PLAN_XB128x256 = 35,       // BK 64
     PLAN_XB256x128 = 36,       // BK 64
     PLAN_XB128x128 = 37,       // BK 64
-    PLAN_COUNT = 38
+    // 64-row tiles (batched decode, M <= 64), BK 64
+    PLAN_X64x256 = 38,
+    PLAN_X64x128 = 39,
+    // one register set, BK 64
+    PLAN_X256x256s1 = 40,
+    PLAN_XB256x256s1 = 41,
+    PLAN_COUNT = 42
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -1761,10 +1797,13 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "pipe32x64k128s3", "pipe32x64k128s4", "pipe64x64k128s3", "pipe64x64k64s4", "pipe64x128k64s4",
     "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
-    "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128"};
+    "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128", "xl64x256", "xl64x128",
+    "xl256x256s1", "xb256x256s1"};
 static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
-static inline bool is_xl_plan(int p) { return p >= PLAN_X128x256 && p <= PLAN_XB128x128; }
-static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256 && p <= PLAN_XB128x128; }
+static inline bool is_xl_plan(int p) { return p >= PLAN_X128x256 && p <= PLAN_XB256x256s1; }
+static inline bool is_xb_plan(int p) {
+    return (p >= PLAN_XB256x256 && p <= PLAN_XB128x128) || p == PLAN_XB256x256s1;
+}
 static inline int xl_bk(int p) {
     return (p == PLAN_X256x256 || p == PLAN_X128x256k32 || p == PLAN_X256x128k32 ||
             p == PLAN_XB256x256k32) ? 32 : 64;
@@ -1812,11 +1851,13 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
         if (M >= 1024) {
-            if (!gated && blocks(256, 256) >= 256) return PLAN_X256x256;
+            if (!gated && blocks(256, 256) >= 256)
+                return (size_t)M * K <= g_abf_elems ? PLAN_XB256x256s1 : PLAN_X256x256;
             if (gated && M >= 2048 && (size_t)M * K <= g_abf_elems) return PLAN_XB128x128;
             return PLAN_X128x128;
         }
-        if (M > 128 && blocks(128, 128) >= 128) return PLAN_X128x128;
+        if (M > 128 && blocks(128, 128) >= 128)
+            return (!gated && blocks(64, 128) >= 256) ? PLAN_X64x128 : PLAN_X128x128;
     }
     if (M <= 128 || (!gated && M <= 512)) {
         const long t = blocks(32, 64);
@@ -2024,14 +2065,14 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
 
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false>
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
                      int M, int K, int N) {
-    using X = XlCfg<BM, BN, BK, GATED, ABF16>;
+    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16>), dim3((unsigned)tiles), dim3(NTHREADS), 0,
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles), dim3(NTHREADS), 0,
                        g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
@@ -2058,6 +2099,7 @@ static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b,
         case PLAN_XB128x256:    return launch_xl<128, 256, 64, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_XB256x128:    return launch_xl<256, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_XB128x128:    return launch_xl<128, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
+        case PLAN_XB256x256s1:  return launch_xl<256, 256, 64, GATED, true, 1>(c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
     }
 }
@@ -2113,7 +2155,7 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_P32x64k64s4:   return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P64x64k64s3:   return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256: case PLAN_XB256x256k32: case PLAN_XB128x256: case PLAN_XB256x128:
-        case PLAN_XB128x128: {
+        case PLAN_XB128x128: case PLAN_XB256x256s1: {
             const int rc = launch_cvt_bf16(g_abf, a, (size_t)M * K);
             if (rc) return rc;
             return dispatch_bf16a<GATED>(plan, c, g_abf, b, b2, M, K, N);
@@ -2122,6 +2164,9 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x128: return launch_xl<256, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X256x256s1: return launch_xl<256, 256, 64, GATED, false, 1>(c, a, b, b2, M, K, N);
+        case PLAN_X64x256: return launch_xl<64, 256, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X64x128: return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x256k32: return launch_xl<128, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x128k32: return launch_xl<256, 128, 32, GATED>(c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
