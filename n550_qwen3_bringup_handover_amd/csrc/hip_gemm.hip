@@ -193,7 +193,10 @@ struct GemvPro {
 // activation row comes from the GemvPro prologue instead of a.
 // Dynamic LDS: (K + 8) floats.  Waves without rows still take part in the
 // barriers.
-template <int ROWS, int CPL, bool GATED, bool PRO = false>
+// MERGE: a holds split attention partials (qh_gemv_merge) and the activation
+// row is their softmax merge; their loads go out before the weight loads,
+// the merge arithmetic after them.
+template <int ROWS, int CPL, bool GATED, bool PRO = false, bool MERGE = false>
 __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                    const float *__restrict__ a,
                                                    const uint16_t *__restrict__ b,
@@ -210,7 +213,24 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
     // 1. this thread's share of the activation row (issued before the weights)
     f32x4 xa[QMAX];
     uint2 wn[QMAX];
-    if constexpr (!PRO) {
+    constexpr int MS = MERGE ? QH_ATT_SPLITS : 1;
+    f32x4 mo[MERGE ? QMAX : 1][MS];
+    float2 mml[MERGE ? QMAX : 1][MS];
+    if constexpr (MERGE) {
+        // chunk i = dims 4i .. 4i+3 of the 2048-vector: head i/32 (kv head
+        // i/64, query head (i/32)&1 of the group), d4 = i%32
+#pragma unroll
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            const int ii = i < nq ? i : 0;
+            const float *pb = a + ((size_t)(ii >> 6) * QH_ATT_SPLITS * 2 + ((ii >> 5) & 1)) * QH_ATT_PART;
+#pragma unroll
+            for (int s = 0; s < MS; s++) {
+                mml[q][s] = *reinterpret_cast<const float2 *>(pb + (size_t)s * 2 * QH_ATT_PART);
+                mo[q][s] = reinterpret_cast<const f32x4 *>(pb + (size_t)s * 2 * QH_ATT_PART + 4)[ii & 31];
+            }
+        }
+    } else if constexpr (!PRO) {
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
@@ -293,6 +313,27 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                round_bf16((xa[q].w * scale) * bf16_hi(wn[q].y))};
         }
     } else {
+        if constexpr (MERGE) {
+#pragma unroll
+            for (int q = 0; q < QMAX; q++) {
+                float mx = mml[q][0].x;
+#pragma unroll
+                for (int s = 1; s < MS; s++) mx = fmaxf(mx, mml[q][s].x);
+                float den = 0.0f;
+                f32x4 num = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int s = 0; s < MS; s++) {
+                    const float w = mml[q][s].x == -INFINITY ? 0.0f : expf(mml[q][s].x - mx);
+                    den = fmaf(w, mml[q][s].y, den);
+                    num.x = fmaf(w, mo[q][s].x, num.x);
+                    num.y = fmaf(w, mo[q][s].y, num.y);
+                    num.z = fmaf(w, mo[q][s].z, num.z);
+                    num.w = fmaf(w, mo[q][s].w, num.w);
+                }
+                const float inv = 1.0f / den;
+                xa[q] = num * inv;
+            }
+        }
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
@@ -1883,7 +1924,7 @@ extern "C" int qh_force_plan(int plan_id) {
     return QH_OK;
 }
 
-template <int ROWS, bool GATED, bool PRO>
+template <int ROWS, bool GATED, bool PRO, bool MERGE = false>
 static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                              int K, int N, int cpl, const GemvPro &pro) {
     const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
@@ -1892,7 +1933,7 @@ static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const 
 #define QH_GEMV1_CASE(P)                                                                     \
     case P:                                                                                  \
         if constexpr (ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16)                         \
-            hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED, PRO>), dim3(grid), dim3(NTHREADS),   \
+            hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED, PRO, MERGE>), dim3(grid), dim3(NTHREADS), \
                                lds, g_stream, c, a, b, b2, K, N, pro);                       \
         else                                                                                 \
             return QH_EINVAL;                                                                \
@@ -1938,6 +1979,16 @@ static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uin
 static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                         int K, int N, bool gated) {
     return launch_gemv1_t<false>(c, a, b, b2, K, N, gated, GemvPro{});
+}
+
+extern "C" int qh_gemv_merge(float *c, const float *part, const uint16_t *b, int K, int N) {
+    if (!g_inited) return QH_ESTATE;
+    if (!c || !part || !b || K != 2048 || N <= 0 || !aligned16(part) || !aligned16(b)) return QH_EINVAL;
+    // K = 2048: 256 chunks of 16 bytes per row, 4 per lane; one row per wave
+    // keeps >= 2048 waves for N = 1024 and 16 weight loads in flight per lane
+    const int cpl = K / 8 / WAVE;
+    const int rc = launch_gemv1_rows<1, false, false, true>(c, part, b, nullptr, K, N, cpl, GemvPro{});
+    return rc;
 }
 
 template <int MR>

@@ -275,63 +275,75 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention: one token at position pos = *pos_d.  Block b = g + 8*q
-// handles kv head g (its GRP query heads) and quarter q of the head
-// dimension: it computes the full scores of both query heads (K is read
-// once for the pair), the softmax, and out[h][32q .. 32q+32) from a quarter
-// of every V row, so no block needs another's result.  The 4 blocks of a kv
-// head share XCD g (block b runs on XCD b % 8) and so its L2 for the K rows.
-// Built for latency: every thread issues its K loads (32 x 16 B of one
-// position, a contiguous 1 KB run per wave in the d-chunk-major cache) and
-// its V loads at entry, before QK-norm and RoPE start.  Positions are taken
-// 256 at a time; scores live in LDS.  Block (g, 0) writes the new token's
-// cache entry.  grid = 4 * NKV blocks of 256 threads; dynamic LDS =
-// qm_attention_decode_lds_bytes(max_seq).
+// Decode attention split over positions: partials, merged by the o GEMV
 // ---------------------------------------------------------------------------
-#define DQ 4                      // head-dimension quarters
-#define DQW (HD / DQ)             // 32 dims per block
-
-__global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ qkv,
-                                                     float *__restrict__ out,
-                                                     float *__restrict__ kc, float *__restrict__ vc,
-                                                     const uint16_t *__restrict__ qn,
-                                                     const uint16_t *__restrict__ kn,
-                                                     const float *__restrict__ rcos,
-                                                     const float *__restrict__ rsin,
-                                                     const int *__restrict__ pos_d, int max_seq,
-                                                     float eps, float scale) {
-    const int g = blockIdx.x % NKV, q = blockIdx.x / NKV;
+// grid = NKV * QM_ATT_SPLITS blocks: block (g, s) takes positions
+// [s*chunk, min(ctx, (s+1)*chunk)) of kv head g, chunk = ceil(ctx / splits),
+// for both query heads of the group.  Every block normalises and ropes the
+// group's two q heads itself (and the new k); block s = 0 writes the new k/v
+// to the cache; the new position's k/v come from registers, never from the
+// cache, so no block reads an entry written in this launch.  Each block
+// writes, per head, the softmax partial of its range:
+//   part[((g*S + s)*GRP + h) * QM_ATT_PART + 0] = m   (max score, -inf if empty)
+//   part[... + 1] = l                                  (sum of exp(score - m))
+//   part[... + 4 .. + 4 + HD) = o                      (sum exp(score - m) * v)
+// The o-projection GEMV merges the splits (k_gemv1 with the merge prologue):
+// out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s with M = max_s m_s, the
+// reference softmax (ops_scalar.c:37-44) regrouped over position ranges.
+// A pass covers 64 positions (one pass up to ctx = 512): wave w owns head
+// dims 32w .. 32w+31.  Scores: lane l takes position l (8 K loads of 16 B,
+// each instruction 64 consecutive positions of the d-chunk-major cache).
+// Weighted V: lane l takes chunk 8w + l%8 of positions l/8 + 8j (each
+// instruction 8 positions x 128 contiguous bytes), then a 3-step shuffle
+// sums the 8 lanes of a chunk.  Every K and V load of the first pass goes
+// out at entry, before the q prologue: one memory round trip per launch.
+__global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv,
+                                                   float *__restrict__ part,
+                                                   float *__restrict__ kc, float *__restrict__ vc,
+                                                   const uint16_t *__restrict__ qn,
+                                                   const uint16_t *__restrict__ kn,
+                                                   const float *__restrict__ rcos,
+                                                   const float *__restrict__ rsin,
+                                                   const int *__restrict__ pos_d, int max_seq,
+                                                   float eps, float scale) {
+    constexpr int S = QM_ATT_SPLITS;
+    constexpr int P = 64;                        // positions per pass
+    const int g = blockIdx.x % NKV, sp = blockIdx.x / NKV;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int pos = *pos_d;
     if (pos < 0 || pos >= max_seq) return;      // uniform per launch
     const int ctx = pos + 1;
+    const int chunk = (ctx + S - 1) / S;
+    const int t0 = min(ctx, sp * chunk), t1 = min(ctx, t0 + chunk);
+    const int n = t1 - t0;                       // positions of this block (may be 0)
 
-    extern __shared__ float sm[];
-    float *sq = sm;                              // [GRP][HD]
-    float *sk = sq + GRP * HD;                   // [HD] k of the new token
-    float *red = sk + HD;                        // [32 groups][GRP][DQW]
-    float *sred = red + 32 * GRP * DQW;          // [16]
-    float *p = sred + 16;                        // [GRP][max_seq]
+    __shared__ float sq[GRP * HD];               // normalised, roped q of both heads
+    __shared__ float sk[HD];                     // the new k
+    __shared__ float sc[4][GRP][P];              // per-wave partial scores
+    __shared__ float pe[GRP][P];                 // softmax weights of the pass
 
     const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
-    // V: thread (tg = tid / 8, c = tid % 8) owns dims 32q + 4c .. +4 of positions tg, tg + 32, ...
-    const int tg = tid >> 3, c4 = tid & 7;
-    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD + q * DQW) + c4;
-    const f32x4 vnew = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD + q * DQW)[c4];
-    constexpr int VB = NTH / 32;                 // positions per thread and pass of 256
+    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD);
+    const f32x4 *vnew4 = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD);
+    const int vch = 8 * wave + (lane & 7);       // V chunk (16 bytes) of this lane
+    const int vp = lane >> 3;                    // V positions vp + 8j of the pass
 
-    // loads of the first pass go out before anything else
-    f32x4 kv[HD / 4];
-    if (tid < pos) {
+    f32x4 kk[8], vv[8];
+    auto load_pass = [&](int base) {
+        const int tk = t0 + base + lane;
+        if (base + lane < n && tk < pos) {
 #pragma unroll
-        for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + tid];
-    }
-    f32x4 vv[VB];
+            for (int j = 0; j < 8; j++) kk[j] = kbase[(size_t)(8 * wave + j) * max_seq + tk];
+        }
 #pragma unroll
-    for (int u = 0; u < VB; u++) {
-        const int t = tg + 32 * u;
-        vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
-    }
+        for (int j = 0; j < 8; j++) {
+            const int i = base + vp + 8 * j;
+            const int tv = t0 + i;
+            vv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (i < n) vv[j] = tv < pos ? vbase[(size_t)tv * (HD / 4) + vch] : vnew4[vch];
+        }
+    };
+    load_pass(0);
 
     // QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
     if (wave < GRP + 1) {
@@ -342,110 +354,95 @@ __global__ __launch_bounds__(NTH) void k_attn_decode(const float *__restrict__ q
         const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
         const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
         const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
-        const float y0 = (x0 * sc) * w0, y1 = (x1 * sc) * w1;
+        const float sc_ = 1.0f / sqrtf(ss / (float)HD + eps);
+        const float y0 = (x0 * sc_) * w0, y1 = (x1 * sc_) * w1;
         dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
         dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
     }
     __syncthreads();
-    if (q == 0 && tid < HD) {                    // one block per kv head writes the new entry
+    if (sp == 0 && tid < HD) {                   // one block per kv head writes the new entry
         kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = sk[tid];
         vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[VOFF + (size_t)g * HD + tid];
     }
 
-    // scores of both query heads: the first 256 positions from the registers
-    // loaded at entry, later ones (ctx > 256) in further passes
-    auto dot2 = [&](const f32x4 *k, float &s0, float &s1) {
-#pragma unroll
-        for (int d4 = 0; d4 < HD / 4; d4++) {
-            const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
-            const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
-            s0 = fmaf(q0.x, k[d4].x, s0); s0 = fmaf(q0.y, k[d4].y, s0);
-            s0 = fmaf(q0.z, k[d4].z, s0); s0 = fmaf(q0.w, k[d4].w, s0);
-            s1 = fmaf(q1.x, k[d4].x, s1); s1 = fmaf(q1.y, k[d4].y, s1);
-            s1 = fmaf(q1.z, k[d4].z, s1); s1 = fmaf(q1.w, k[d4].w, s1);
-        }
-    };
-    if (tid < ctx) {
-        float s0 = 0.0f, s1 = 0.0f;
-        if (tid < pos) dot2(kv, s0, s1);
-        else dot2(reinterpret_cast<const f32x4 *>(sk), s0, s1);   // the new token
-        p[tid] = s0 * scale;
-        p[max_seq + tid] = s1 * scale;
-    }
-    for (int t = NTH + tid; t < ctx; t += NTH) {
-        float s0 = 0.0f, s1 = 0.0f;
-        if (t < pos) {
-            f32x4 k2[HD / 4];
-#pragma unroll
-            for (int d4 = 0; d4 < HD / 4; d4++) k2[d4] = kbase[(size_t)d4 * max_seq + t];
-            dot2(k2, s0, s1);
-        } else {
-            dot2(reinterpret_cast<const f32x4 *>(sk), s0, s1);
-        }
-        p[t] = s0 * scale;
-        p[max_seq + t] = s1 * scale;
-    }
-    __syncthreads();
-
-    // softmax of both heads (ops_scalar.c:37-44)
-    float m0 = -INFINITY, m1 = -INFINITY;
-    for (int t = tid; t < ctx; t += NTH) {
-        m0 = fmaxf(m0, p[t]);
-        m1 = fmaxf(m1, p[max_seq + t]);
-    }
-    m0 = wave_max(m0);
-    m1 = wave_max(m1);
-    if (lane == 0) { sred[wave] = m0; sred[4 + wave] = m1; }
-    __syncthreads();
-    m0 = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-    m1 = fmaxf(fmaxf(sred[4], sred[5]), fmaxf(sred[6], sred[7]));
-    float e0 = 0.0f, e1 = 0.0f;
-    for (int t = tid; t < ctx; t += NTH) {
-        const float a0 = expf(p[t] - m0), a1 = expf(p[max_seq + t] - m1);
-        p[t] = a0;
-        p[max_seq + t] = a1;
-        e0 += a0;
-        e1 += a1;
-    }
-    e0 = wave_sum(e0);
-    e1 = wave_sum(e1);
-    if (lane == 0) { sred[8 + wave] = e0; sred[12 + wave] = e1; }
-    __syncthreads();
-    const float inv0 = 1.0f / ((sred[8] + sred[9]) + (sred[10] + sred[11]));
-    const float inv1 = 1.0f / ((sred[12] + sred[13]) + (sred[14] + sred[15]));
-
-    // out[h][32q + d] = sum_t p[h][t] v_t[32q + d] / e_h
+    float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-    for (int base = 0; base < ctx; base += NTH) {
-        if (base > 0) {
+    for (int base = 0; base < n; base += P) {
+        if (base > 0) load_pass(base);
+        // partial scores over this wave's 32 dims
+        {
+            const int tk = t0 + base + lane;
+            const f32x4 *kp = kk;
+            f32x4 knew[8];
+            if (tk == pos) {
 #pragma unroll
-            for (int u = 0; u < VB; u++) {
-                const int t = base + tg + 32 * u;
-                vv[u] = t < pos ? vbase[(size_t)t * (HD / 4)] : vnew;
+                for (int j = 0; j < 8; j++) knew[j] = reinterpret_cast<const f32x4 *>(sk)[8 * wave + j];
+                kp = knew;
             }
-        }
+            float a0 = 0.0f, a1 = 0.0f;
+            if (base + lane < n) {
 #pragma unroll
-        for (int u = 0; u < VB; u++) {
-            const int t = base + tg + 32 * u;
-            if (t < ctx) {
-                const float w0 = p[t], w1 = p[max_seq + t];
-                o0.x = fmaf(w0, vv[u].x, o0.x); o0.y = fmaf(w0, vv[u].y, o0.y);
-                o0.z = fmaf(w0, vv[u].z, o0.z); o0.w = fmaf(w0, vv[u].w, o0.w);
-                o1.x = fmaf(w1, vv[u].x, o1.x); o1.y = fmaf(w1, vv[u].y, o1.y);
-                o1.z = fmaf(w1, vv[u].z, o1.z); o1.w = fmaf(w1, vv[u].w, o1.w);
+                for (int j = 0; j < 8; j++) {
+                    const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[8 * wave + j];
+                    const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[8 * wave + j];
+                    a0 = fmaf(q0.x, kp[j].x, a0); a0 = fmaf(q0.y, kp[j].y, a0);
+                    a0 = fmaf(q0.z, kp[j].z, a0); a0 = fmaf(q0.w, kp[j].w, a0);
+                    a1 = fmaf(q1.x, kp[j].x, a1); a1 = fmaf(q1.y, kp[j].y, a1);
+                    a1 = fmaf(q1.z, kp[j].z, a1); a1 = fmaf(q1.w, kp[j].w, a1);
+                }
             }
+            sc[wave][0][lane] = a0;
+            sc[wave][1][lane] = a1;
         }
+        __syncthreads();
+        // every wave sums the four partials of position `lane` and keeps the
+        // pass's softmax statistics (identical in all waves)
+        const bool valid = base + lane < n;
+        const float s0 = valid ? ((sc[0][0][lane] + sc[1][0][lane]) + (sc[2][0][lane] + sc[3][0][lane])) * scale
+                               : -INFINITY;
+        const float s1 = valid ? ((sc[0][1][lane] + sc[1][1][lane]) + (sc[2][1][lane] + sc[3][1][lane])) * scale
+                               : -INFINITY;
+        const float nm0 = fmaxf(m0, wave_max(s0)), nm1 = fmaxf(m1, wave_max(s1));
+        const float e0 = valid ? expf(s0 - nm0) : 0.0f, e1 = valid ? expf(s1 - nm1) : 0.0f;
+        const float r0 = m0 == -INFINITY ? 0.0f : expf(m0 - nm0);
+        const float r1 = m1 == -INFINITY ? 0.0f : expf(m1 - nm1);
+        l0 = l0 * r0 + wave_sum(e0);
+        l1 = l1 * r1 + wave_sum(e1);
+        m0 = nm0;
+        m1 = nm1;
+        if (wave == 0) { pe[0][lane] = e0; pe[1][lane] = e1; }
+        __syncthreads();
+        o0 *= r0;
+        o1 *= r1;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float w0 = pe[0][vp + 8 * j], w1 = pe[1][vp + 8 * j];   // 0 beyond n
+            o0.x = fmaf(w0, vv[j].x, o0.x); o0.y = fmaf(w0, vv[j].y, o0.y);
+            o0.z = fmaf(w0, vv[j].z, o0.z); o0.w = fmaf(w0, vv[j].w, o0.w);
+            o1.x = fmaf(w1, vv[j].x, o1.x); o1.y = fmaf(w1, vv[j].y, o1.y);
+            o1.z = fmaf(w1, vv[j].z, o1.z); o1.w = fmaf(w1, vv[j].w, o1.w);
+        }
+        __syncthreads();                          // sc / pe reused by the next pass
     }
-    reinterpret_cast<f32x4 *>(red + (tg * GRP + 0) * DQW)[c4] = o0;
-    reinterpret_cast<f32x4 *>(red + (tg * GRP + 1) * DQW)[c4] = o1;
-    __syncthreads();
-    if (tid < GRP * DQW) {
-        const int h = tid / DQW, d = tid % DQW;
-        float sacc = 0.0f;
-#pragma unroll 8
-        for (int k = 0; k < 32; k++) sacc += red[(k * GRP + h) * DQW + d];
-        out[(size_t)(g * GRP + h) * HD + q * DQW + d] = sacc * (h ? inv1 : inv0);
+
+    // sum the 8 lanes of each chunk (lanes c, c+8, ..., c+56) and write
+#pragma unroll
+    for (int msk = 8; msk <= 32; msk <<= 1) {
+        o0.x += __shfl_xor(o0.x, msk); o0.y += __shfl_xor(o0.y, msk);
+        o0.z += __shfl_xor(o0.z, msk); o0.w += __shfl_xor(o0.w, msk);
+        o1.x += __shfl_xor(o1.x, msk); o1.y += __shfl_xor(o1.y, msk);
+        o1.z += __shfl_xor(o1.z, msk); o1.w += __shfl_xor(o1.w, msk);
+    }
+    float *pp = part + (size_t)(g * S + sp) * GRP * QM_ATT_PART;
+    if (lane < 8) {
+        reinterpret_cast<f32x4 *>(pp + 4)[vch] = o0;
+        reinterpret_cast<f32x4 *>(pp + QM_ATT_PART + 4)[vch] = o1;
+    }
+    if (tid == 0) {
+        pp[0] = m0;
+        pp[1] = l0;
+        pp[QM_ATT_PART] = m1;
+        pp[QM_ATT_PART + 1] = l1;
     }
 }
 
@@ -500,27 +497,15 @@ extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const 
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 
-extern "C" size_t qm_attention_decode_lds_bytes(int max_seq) {
-    return sizeof(float) * ((size_t)GRP * HD + HD + 32 * GRP * DQW + 16 + (size_t)GRP * max_seq);
-}
-
-extern "C" int qm_attention_decode(const float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
-                                   const uint16_t *kn, const float *rcos, const float *rsin,
-                                   const int *pos_d, int max_seq, float eps) {
+extern "C" int qm_attention_decode_part(const float *qkv, float *part, float *kc, float *vc, const uint16_t *qn,
+                                        const uint16_t *kn, const float *rcos, const float *rsin,
+                                        const int *pos_d, int max_seq, float eps) {
     if (!stream()) return QH_ESTATE;
-    if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
+    if (!qkv || !part || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
-    const size_t lds = qm_attention_decode_lds_bytes(max_seq);
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_attn_decode, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)qm_attention_decode_lds_bytes(QM_MAX_SEQ)) != hipSuccess)
-            return QH_ELAUNCH;
-        attr_set = true;
-    }
     const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
-    hipLaunchKernelGGL(k_attn_decode, dim3(DQ * NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, qn, kn,
-                       rcos, rsin, pos_d, max_seq, eps, scale);
+    hipLaunchKernelGGL(k_attn_part, dim3(NKV * QM_ATT_SPLITS), dim3(NTH), 0, stream(), qkv, part, kc, vc,
+                       qn, kn, rcos, rsin, pos_d, max_seq, eps, scale);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

@@ -86,6 +86,16 @@ typedef struct {
 int qh_gemv_pro(float *c_d, const qh_gemv_pro_t *pro, const uint16_t *b_d, const uint16_t *b2_d,
                 int K, int N, int gated);
 
+/* M = 1 GEMV whose activation row is decode attention merged from split
+ * softmax partials (the o projection): part holds, for 8 kv heads x
+ * QH_ATT_SPLITS position ranges x 2 query heads, QH_ATT_PART floats
+ * {m, l, -, -, o[128]} (max score, sum of exp(score - m), sum of
+ * exp(score - m) * v); the activation is sum_s e^(m_s-M) o_s / sum_s
+ * e^(m_s-M) l_s per head, M = max_s m_s.  K = 2048 (16 heads x 128). */
+#define QH_ATT_SPLITS 8
+#define QH_ATT_PART (4 + 128)
+int qh_gemv_merge(float *c_d, const float *part_d, const uint16_t *b_d, int K, int N);
+
 /* device copy by a plain 16-byte-vector kernel (bytes % 16 == 0, 16-byte
  * aligned pointers): the known-traffic reference for HBM counter calibration */
 int qh_copy(void *dst_d, const void *src_d, size_t bytes);

@@ -50,6 +50,7 @@ struct qwen3_hip_model {
     float *kc, *vc;                    /* [NL][KVH][..] see hip_model.hip */
     float *rcos, *rsin;                /* [max_seq][64] */
     float *x, *x0, *x1, *xb, *qkv, *att, *ob, *hb, *dn, *logits;
+    float *apart;                      /* decode attention partials [QM_ATT_PART_FLOATS] */
     int *tok_in;                       /* [QM_MAX_CHUNK] */
     int *state;                        /* [0] token, [1] position, [2] step */
     int *out_tok;                      /* [max_seq + 1] */
@@ -128,7 +129,7 @@ void qwen3_hip_model_close(qwen3_hip_model *m) {
     (void)qh_sync();
     if (m->graph_id >= 0) (void)qh_graph_destroy(m->graph_id);
     void *bufs[] = {m->wbuf, m->kc, m->vc, m->rcos, m->rsin, m->x, m->x0, m->x1, m->xb, m->qkv,
-                    m->att, m->ob, m->hb, m->dn, m->logits, m->tok_in, m->state, m->out_tok};
+                    m->att, m->ob, m->hb, m->dn, m->logits, m->apart, m->tok_in, m->state, m->out_tok};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) (void)qh_free(bufs[i]);
     free(m->dump_host);
     free(m);
@@ -173,6 +174,7 @@ int qwen3_hip_model_open(qwen3_hip_model **out, const void *blob, size_t size, i
     DEV(m->hb, B * QW3M_INTER * 4);
     DEV(m->dn, B * H * 4);
     DEV(m->logits, (size_t)V * 4);
+    DEV(m->apart, (size_t)QM_ATT_PART_FLOATS * 4);
     DEV(m->tok_in, B * sizeof(int));
     DEV(m->state, 4 * sizeof(int));
     DEV(m->out_tok, ((size_t)max_seq + 1) * sizeof(int));
@@ -351,10 +353,11 @@ static int decode_step(qwen3_hip_model *m) {
         qh_gemv_pro_t pro = {m->x0, NULL, NULL, 0, m->dn, L->in_norm, m->x1, eps};
         if (l == 0) { pro.x = NULL; pro.r = NULL; pro.emb = m->embed; pro.tok = m->state; pro.emb_rows = V; }
         rc = qh_gemv_pro(m->qkv, &pro, L->wqkv, NULL, H, QKV_N, 0);
-        if (!rc) rc = qm_attention_decode(m->qkv, m->att, m->kc + l * kv_layer_floats(m),
-                                          m->vc + l * kv_layer_floats(m), L->qn, L->kn, m->rcos, m->rsin,
-                                          m->state + 1, m->max_seq, eps);
-        if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, 1, QW3M_Q_DIM, H);
+        /* attention as split-softmax partials, merged in the o GEMV's prologue */
+        if (!rc) rc = qm_attention_decode_part(m->qkv, m->apart, m->kc + l * kv_layer_floats(m),
+                                               m->vc + l * kv_layer_floats(m), L->qn, L->kn, m->rcos,
+                                               m->rsin, m->state + 1, m->max_seq, eps);
+        if (!rc) rc = qh_gemv_merge(m->ob, m->apart, L->wo, QW3M_Q_DIM, H);
         const qh_gemv_pro_t pro2 = {m->x1, NULL, NULL, 0, m->ob, L->post_norm, m->x0, eps};
         if (!rc) rc = qh_gemv_pro(m->hb, &pro2, L->wg, L->wu, H, QW3M_INTER, 1);
         if (!rc) rc = qh_gemm(m->dn, m->hb, L->wd, 1, QW3M_INTER, H);

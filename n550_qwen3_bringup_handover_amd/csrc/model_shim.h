@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "hip_shim.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -26,12 +28,16 @@ int qm_attention(float *qkv_d, float *out_d, float *kc_d, float *vc_d, const uin
                  int nt, int max_seq, float eps);
 size_t qm_attention_lds_bytes(int max_seq);
 
-/* the same computation for one token (decode), one block per query head,
- * scheduled for latency */
-int qm_attention_decode(const float *qkv_d, float *out_d, float *kc_d, float *vc_d, const uint16_t *qn_d,
-                        const uint16_t *kn_d, const float *rcos_d, const float *rsin_d, const int *pos_d,
-                        int max_seq, float eps);
-size_t qm_attention_decode_lds_bytes(int max_seq);
+/* decode attention split into QM_ATT_SPLITS position ranges per kv head:
+ * writes softmax partials (m, l, o[128] per head and range, QM_ATT_PART
+ * floats each, [kv head][split][2 heads]) for the o-projection GEMV to merge
+ * (qh_gemv_merge); also writes the new k/v to the cache */
+#define QM_ATT_SPLITS QH_ATT_SPLITS
+#define QM_ATT_PART QH_ATT_PART
+#define QM_ATT_PART_FLOATS (8 * QM_ATT_SPLITS * 2 * QM_ATT_PART)
+int qm_attention_decode_part(const float *qkv_d, float *part_d, float *kc_d, float *vc_d,
+                             const uint16_t *qn_d, const uint16_t *kn_d, const float *rcos_d,
+                             const float *rsin_d, const int *pos_d, int max_seq, float eps);
 
 /* *p = v, as a kernel (safe inside stream capture) */
 int qm_set_i32(int *p_d, int v);
