@@ -519,6 +519,9 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 64 MiB copy kernel (traffic-counter calibration)")
     ap.add_argument("--no-model", action="store_true", help="skip the full-forward (cfg 4) measurement")
+    ap.add_argument("--gemm-shape", default=None, metavar="M,K,N,GATED",
+                    help="only time one GEMM shape on its automatic plan (--steps launches, "
+                         "graph-replayed) and print one JSON line; for profiling runs")
     ap.add_argument("--cpu-baseline-child", type=float, default=None, help=argparse.SUPPRESS)
     ap.add_argument("--cpu-model-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
@@ -528,6 +531,17 @@ def main():
         return 0
     if args.cpu_model_child:
         cpu_model_child()
+        return 0
+    if args.gemm_shape:
+        M, K, N, gated = (int(v) for v in args.gemm_shape.split(","))
+        g = Gpu()
+        a = g.alloc(4 * M * K)
+        g.fill_f32(a, M * K, 31)
+        w = g.alloc(2 * N * K * (2 if gated else 1))
+        g.fill_bf16(w, N * K * (2 if gated else 1), 32)
+        c = g.alloc(4 * M * N)
+        e = gemm_entry(g, M, K, N, bool(gated), a, c, w, reps=max(1, args.steps))
+        print(json.dumps({"gemm_shape": e}))
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
