@@ -1285,7 +1285,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t 
 // loads stage it+2 into the freed registers (one stage of latency cover, for
 // tiles whose two register sets would not fit).
 template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS>
-__global__ __launch_bounds__(NTHREADS, BM <= 64 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
+__global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
