@@ -181,4 +181,5 @@ PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4
          "pipe64x64k64s3": 26, "xl128x256": 27, "xl256x256": 28, "xl256x128": 29, "xl128x128": 30, "xl128x256k32": 31, "xl256x128k32": 32,
          "xb256x256": 33, "xb256x256k32": 34, "xb128x256": 35, "xb256x128": 36, "xb128x128": 37,
          "xl64x256": 38, "xl64x128": 39,
-         "xl256x256s1": 40, "xb256x256s1": 41}
+         "xl256x256s1": 40, "xb256x256s1": 41,
+         "stream": 42, "stream-ks1": 43, "stream-ks2": 44, "stream-ks4": 45, "stream-ks8": 46}

@@ -47,6 +47,41 @@ __device__ __forceinline__ float round_bf16(float x) {
     return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
 }
 
+// raw buffer resource over [p, p + bytes): stride 0, num_records = bytes.  A
+// load at an offset past num_records returns zeros and reads no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+#define BUF_OOB 0x80000000u      // an offset past every buffer below 2 GiB
+
+// w.lo * x.lo + w.hi * x.hi + acc for two packed bf16 pairs (v_dot2_f32_bf16)
+__device__ __forceinline__ float bf16_dot2(uint32_t w, uint32_t x, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), acc,
+                                           false);
+}
+
+// Sum over the 64 lanes of a wave, the same bits in every lane.  Each step
+// adds a lane's value and its partner's, so both partners hold the same sum:
+// DPP within rows of 16 lanes (quad permutes for xor 1 and xor 2, then the
+// half-row mirror and the row mirror, which pair groups that already hold
+// equal sums), then the gfx950 permlane swaps across rows (xor 16, xor 32).
+// All VALU: no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_partner<0xB1>(x);      // quad_perm [1,0,3,2]
+    x += dpp_partner<0x4E>(x);      // quad_perm [2,3,0,1]
+    x += dpp_partner<0x141>(x);     // row_half_mirror
+    x += dpp_partner<0x140>(x);     // row_mirror
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    x = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
     // reference: (g / (1 + expf(-g))) * u  (ops_scalar.c:46-51)
     return (g / (1.0f + expf(-g))) * u;
@@ -163,6 +198,8 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
     }
 }
 
+__device__ const int k_zero_token = 0;     // token read by prologues without an embedding
+
 // Activation prologue of the M = 1 GEMV (decode): the GEMV input is
 //   a = rmsnorm(x + r) * nw       (fpga_bringup/src/src/ops_scalar.c:11-16,
 //                                  residual add ops_scalar.c:53-55)
@@ -203,96 +240,108 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                    const uint16_t *__restrict__ b2,
                                                    int K, int N, GemvPro pro) {
     constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
-    constexpr int QMAX = (CPL * 8 * WAVE + 4 * NTHREADS - 1) / (4 * NTHREADS);   // f32x4 per thread
-    extern __shared__ float sact[];                  // [K] activation, then [4] partial sums
+    constexpr int NQ = CPL * 2 * WAVE;               // 4-element groups of the padded row (512*CPL)
+    constexpr int QMAX = (NQ + NTHREADS - 1) / NTHREADS;
+    extern __shared__ __align__(16) uint32_t sx[];   // [2*NQ] bf16 pairs of the padded row, then [4] floats
+    float *sred = reinterpret_cast<float *>(sx + 2 * NQ);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
-    const bool active = row0 < N;
+    // MERGE is launched for K = 2048 only (the 16 x 128 attention output),
+    // whose 512 groups the 256 threads cover exactly: its merge has no tail
+    static_assert(!MERGE || (CPL == 4 && QMAX == 2), "MERGE expects K = 2048");
     const int nch = K >> 3, nq = K >> 2;
 
-    // 1. this thread's share of the activation row (issued before the weights)
+    // 1. this thread's share of the activation row (issued before the
+    //    weights; groups past K read zeros)
     f32x4 xa[QMAX];
     uint2 wn[QMAX];
+    f32x4 xv[PRO ? QMAX : 1], rv[PRO ? QMAX : 1];    // prologue sources (x, r, embedding row)
+    uint2 e[PRO ? QMAX : 1];
     constexpr int MS = MERGE ? QH_ATT_SPLITS : 1;
     f32x4 mo[MERGE ? QMAX : 1][MS];
     float2 mml[MERGE ? QMAX : 1][MS];
+    // Scheduling barriers keep the activation-side loads ahead of the weight
+    // loads and their arithmetic behind them, so a wave waits for the
+    // activation alone before its LDS store.
     if constexpr (MERGE) {
-        // chunk i = dims 4i .. 4i+3 of the 2048-vector: head i/32 (kv head
+        // group i = dims 4i .. 4i+3 of the 2048-vector: head i/32 (kv head
         // i/64, query head (i/32)&1 of the group), d4 = i%32
+        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a, (size_t)8 * QH_ATT_SPLITS * 2 * QH_ATT_PART * 4);
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            const int ii = i < nq ? i : 0;
-            const float *pb = a + ((size_t)(ii >> 6) * QH_ATT_SPLITS * 2 + ((ii >> 5) & 1)) * QH_ATT_PART;
+            const int ii = tid + NTHREADS * q;       // < 512 = nq: no tail for K = 2048
+            const uint32_t pb = (uint32_t)(((ii >> 6) * QH_ATT_SPLITS * 2 + ((ii >> 5) & 1)) * QH_ATT_PART) * 4u;
 #pragma unroll
             for (int s = 0; s < MS; s++) {
-                mml[q][s] = *reinterpret_cast<const float2 *>(pb + (size_t)s * 2 * QH_ATT_PART);
-                mo[q][s] = reinterpret_cast<const f32x4 *>(pb + (size_t)s * 2 * QH_ATT_PART + 4)[ii & 31];
+                const uint32_t ps = pb + (uint32_t)(s * 2 * QH_ATT_PART) * 4u;
+                mml[q][s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rp, ps, 0, 0));
+                mo[q][s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         rp, ps + 16u + (uint32_t)(ii & 31) * 16u, 0, 0));
             }
         }
     } else if constexpr (!PRO) {
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)K * 4);
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
-            xa[q] = i < nq ? reinterpret_cast<const f32x4 *>(a)[i] : f32x4{0.f, 0.f, 0.f, 0.f};
+            xa[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  ra, i < nq ? (uint32_t)i * 16 : BUF_OOB, 0, 0));
         }
     } else {
-        const uint2 *e2 = nullptr;
-        if (pro.emb) {
-            int t = *pro.tok;
-            t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
-            e2 = reinterpret_cast<const uint2 *>(pro.emb + (size_t)t * K);
-        }
+        // x + r, or the embedding row of the device-held token: every source
+        // is loaded, absent ones from empty buffers, which read as zeros, so
+        // the prologue has no branch
+        const bool emb = pro.emb != nullptr;
+        int t = *(emb ? pro.tok : &k_zero_token);
+        t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
+        const __amdgpu_buffer_rsrc_t re = buf_rsrc(emb ? pro.emb + (size_t)t * K : nullptr, emb ? (size_t)K * 2 : 0);
+        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(pro.x, (pro.x && !emb) ? (size_t)K * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(pro.r, (pro.r && !emb) ? (size_t)K * 4 : 0);
+        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(pro.nw, (size_t)K * 2);
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
-            xa[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-            wn[q] = uint2{0u, 0u};
-            if (i < nq) {
-                wn[q] = reinterpret_cast<const uint2 *>(pro.nw)[i];
-                if (e2) {
-                    const uint2 e = e2[i];
-                    xa[q] = f32x4{bf16_lo(e.x), bf16_hi(e.x), bf16_lo(e.y), bf16_hi(e.y)};
-                } else {
-                    xa[q] = reinterpret_cast<const f32x4 *>(pro.x)[i];
-                    if (pro.r) xa[q] += reinterpret_cast<const f32x4 *>(pro.r)[i];
-                }
-            }
+            const uint32_t o16 = i < nq ? (uint32_t)i * 16 : BUF_OOB, o8 = i < nq ? (uint32_t)i * 8 : BUF_OOB;
+            xv[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o16, 0, 0));
+            rv[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, o16, 0, 0));
+            e[q] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(re, o8, 0, 0));
+            wn[q] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, o8, 0, 0));
         }
     }
+    __builtin_amdgcn_sched_barrier(0);               // the activation loads go out first
 
-    // 2. all weight loads of this wave
-    const u32x4 *b4 = reinterpret_cast<const u32x4 *>(b);
-    const u32x4 *u4 = reinterpret_cast<const u32x4 *>(b2);
+    // 2. all weight loads of this wave; rows past N and chunks past K read
+    //    zeros (the caller keeps N*K*2 below 2 GiB)
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
     u32x4 bv[NB][CPL];
-    if (active) {
 #pragma unroll
-        for (int r = 0; r < ROWS; r++) {
-            const size_t rb = (size_t)min(row0 + r, N - 1) * nch;
+    for (int r = 0; r < ROWS; r++) {
+        const int row = row0 + r;
 #pragma unroll
-            for (int j = 0; j < CPL; j++) {
-                const int ch = lane + WAVE * j;
-                if (ch < nch) {
-                    bv[r][j] = __builtin_nontemporal_load(b4 + rb + ch);
-                    if constexpr (GATED) bv[ROWS + r][j] = __builtin_nontemporal_load(u4 + rb + ch);
-                } else {
-                    bv[r][j] = u32x4{0u, 0u, 0u, 0u};
-                    if constexpr (GATED) bv[ROWS + r][j] = u32x4{0u, 0u, 0u, 0u};
-                }
-            }
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            const uint32_t off = (row < N && ch < nch) ? (uint32_t)row * (uint32_t)K * 2u + (uint32_t)ch * 16u
+                                                       : BUF_OOB;
+            bv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);      // nt: read once
+            if constexpr (GATED) bv[ROWS + r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);               // ... then every weight load
 
-    // 3. activation through LDS, rounded to bf16 (normalised first for PRO)
-    f32x4 *sa4 = reinterpret_cast<f32x4 *>(sact);
+    // 3. activation through LDS as bf16 (RNE), normalised first for PRO;
+    //    zeros past K
+    uint2 *sx2 = reinterpret_cast<uint2 *>(sx);
     if constexpr (PRO) {
+#pragma unroll
+        for (int q = 0; q < QMAX; q++)
+            xa[q] = f32x4{bf16_lo(e[q].x), bf16_hi(e[q].x), bf16_lo(e[q].y), bf16_hi(e[q].y)} + (xv[q] + rv[q]);
         float ss = 0.0f;
 #pragma unroll
         for (int q = 0; q < QMAX; q++)
             ss += xa[q].x * xa[q].x + xa[q].y * xa[q].y + xa[q].z * xa[q].z + xa[q].w * xa[q].w;
-#pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
-        if (lane == 0) sact[K + wave] = ss;
+        ss = wave_sum(ss);
+        if (lane == 0) sred[wave] = ss;
         if (pro.x_out && blockIdx.x == 0) {
 #pragma unroll
             for (int q = 0; q < QMAX; q++) {
@@ -301,16 +350,14 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
             }
         }
         __syncthreads();
-        ss = (sact[K] + sact[K + 1]) + (sact[K + 2] + sact[K + 3]);
+        ss = (sred[0] + sred[1]) + (sred[2] + sred[3]);
         const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
-            if (i < nq)
-                sa4[i] = f32x4{round_bf16((xa[q].x * scale) * bf16_lo(wn[q].x)),
-                               round_bf16((xa[q].y * scale) * bf16_hi(wn[q].x)),
-                               round_bf16((xa[q].z * scale) * bf16_lo(wn[q].y)),
-                               round_bf16((xa[q].w * scale) * bf16_hi(wn[q].y))};
+            if (NQ % NTHREADS == 0 || i < NQ)
+                sx2[i] = uint2{pack_bf16x2((xa[q].x * scale) * bf16_lo(wn[q].x), (xa[q].y * scale) * bf16_hi(wn[q].x)),
+                               pack_bf16x2((xa[q].z * scale) * bf16_lo(wn[q].y), (xa[q].w * scale) * bf16_hi(wn[q].y))};
         }
     } else {
         if constexpr (MERGE) {
@@ -337,55 +384,39 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
 #pragma unroll
         for (int q = 0; q < QMAX; q++) {
             const int i = tid + NTHREADS * q;
-            if (i < nq)
-                sa4[i] = f32x4{round_bf16(xa[q].x), round_bf16(xa[q].y), round_bf16(xa[q].z),
-                               round_bf16(xa[q].w)};
+            if (NQ % NTHREADS == 0 || i < NQ)
+                sx2[i] = uint2{pack_bf16x2(xa[q].x, xa[q].y), pack_bf16x2(xa[q].z, xa[q].w)};
         }
     }
     __syncthreads();
-    if (!active) return;                             // no barrier below this point
 
-    float av[CPL][8];
+    // 4. this lane's activation chunks, then packed bf16 dot products
+    u32x4 xc[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        const int ch = lane + WAVE * j;
-        if (ch < nch) {
-            const f32x4 x0 = sa4[2 * ch], x1 = sa4[2 * ch + 1];
-            av[j][0] = x0.x; av[j][1] = x0.y; av[j][2] = x0.z; av[j][3] = x0.w;
-            av[j][4] = x1.x; av[j][5] = x1.y; av[j][6] = x1.z; av[j][7] = x1.w;
-        } else {
+    for (int j = 0; j < CPL; j++) xc[j] = reinterpret_cast<const u32x4 *>(sx)[lane + WAVE * j];
+    float acc[NB];
 #pragma unroll
-            for (int e = 0; e < 8; e++) av[j][e] = 0.0f;
-        }
+    for (int r = 0; r < NB; r++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) s = bf16_dot2(bv[r][j][e], xc[j][e], s);
+        acc[r] = s;
     }
 
-    constexpr int V = pow2_ceil<NB>::v;
-    float acc[V];
+    // 5. wave sums (every lane holds every row's total); lane r stores row r
+    float tot = 0.0f, up = 0.0f;
 #pragma unroll
-    for (int i = 0; i < V; i++) acc[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++)
-#pragma unroll
-        for (int r = 0; r < NB; r++) {
-            float s = acc[r];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                s = fmaf(av[j][2 * e], bf16_lo(bv[r][j][e]), s);
-                s = fmaf(av[j][2 * e + 1], bf16_hi(bv[r][j][e]), s);
-            }
-            acc[r] = s;
+    for (int r = 0; r < ROWS; r++) {
+        const float t = wave_sum(acc[r]);
+        tot = lane == r ? t : tot;
+        if constexpr (GATED) {
+            const float u = wave_sum(acc[ROWS + r]);
+            up = lane == r ? u : up;
         }
-
-    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
-    const float tot = wave_transpose_reduce<V>(acc, lane);
-    const int idx = lane >> (6 - LV);
-    const int step = 64 >> LV;                       // lanes holding each value
-    if constexpr (!GATED) {
-        if ((lane & (step - 1)) == 0 && idx < ROWS && row0 + idx < N) c[row0 + idx] = tot;
-    } else {
-        const float up = __shfl(tot, (lane + ROWS * step) & 63);
-        if ((lane & (step - 1)) == 0 && idx < ROWS && row0 + idx < N) c[row0 + idx] = silu_mul(tot, up);
     }
+    if (lane < ROWS && row0 + lane < N) c[row0 + lane] = GATED ? silu_mul(tot, up) : tot;
 }
 
 // Fused gate/up GEMV: rows of Wg and Wu with the same index share a wave, and
@@ -1617,6 +1648,168 @@ __global__ __launch_bounds__(NTHREADS) void k_fill_zero(float *__restrict__ c, s
 }
 
 // ---------------------------------------------------------------------------
+// Weight-streaming MFMA GEMM for 5 <= M <= 64 (small decode batches)
+// ---------------------------------------------------------------------------
+// For M <= 64 the weights are almost all of the traffic, and the tile kernels
+// above keep too few of their bytes in flight per CU to stream them at HBM
+// rate.  Here a block of 8 waves owns 16-row tiles of B (the weights) and a
+// K slice of 256*KS (blockIdx.y picks the slice).  Wave w owns k range
+// [slice + 32*KS*w, +32*KS): it holds its A fragments (MT m-tiles of 16 rows,
+// rounded to bf16 RNE) in registers for the whole kernel and loads its B
+// fragments straight from memory into registers, ST tiles ahead, with
+// v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand = weights).
+// Lane (r, g) = (lane % 16, lane / 16) holds k = 32s + 8g .. 32s + 8g + 7 of
+// step s for row r of both operands.  The 8 partial tiles are summed through
+// LDS in wave order (one barrier per tile, two LDS buffers).  Blocks walk
+// tiles blockIdx.x, +gridDim.x, ... so one launch of <= 256 blocks streams any
+// N.  Every load is an unconditional buffer load: rows past N and tiles past
+// a block's last one read at an offset beyond the buffer, which returns zeros
+// and touches no memory, so the loop has no branches around its loads.
+// part == nullptr: C (or silu(gate)*up) is written; otherwise the fp32 sums
+// of slice ks go to part[ks][j][M][N] (j = 0, or gate/up for GATED) and
+// k_stream_reduce adds the slices in order.
+#define STREAM_THREADS 512
+
+template <int MT, int KS, int ST, bool GATED>
+__global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__restrict__ c,
+                                                                float *__restrict__ part,
+                                                                const float *__restrict__ a,
+                                                                const uint16_t *__restrict__ b,
+                                                                const uint16_t *__restrict__ b2,
+                                                                int M, int K, int N, int ntiles) {
+    constexpr int NJ = GATED ? 2 : 1;
+    constexpr int SLOTS = MT * NJ;                       // f32x4 accumulators per lane
+    __shared__ f32x4 red[2][STREAM_THREADS / WAVE][SLOTS][WAVE];
+
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int kw0 = blockIdx.y * (256 * KS) + w * (32 * KS) + 8 * g;     // this lane's first k
+    const int first = blockIdx.x, stride = gridDim.x;
+    const int nmine = first < ntiles ? (ntiles - 1 - first) / stride + 1 : 0;
+    if (nmine == 0) return;                              // uniform over the block
+
+    // ---- A fragments, rounded once
+    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
+    bf16x8 af[MT][KS];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const int m = 16 * mt + r16;
+        const uint32_t off = m < M ? (uint32_t)(((size_t)m * K + kw0) * 4) : BUF_OOB;
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 128 * s, 0, 0);
+            const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 128 * s + 16, 0, 0);
+            u32x4 p;
+            p.x = pack_bf16x2(__uint_as_float(lo.x), __uint_as_float(lo.y));
+            p.y = pack_bf16x2(__uint_as_float(lo.z), __uint_as_float(lo.w));
+            p.z = pack_bf16x2(__uint_as_float(hi.x), __uint_as_float(hi.y));
+            p.w = pack_bf16x2(__uint_as_float(hi.z), __uint_as_float(hi.w));
+            af[mt][s] = __builtin_bit_cast(bf16x8, p);
+        }
+    }
+
+    // ---- B fragments: ST tiles in flight
+    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
+    u32x4 bq[ST][NJ][KS];
+    auto boff = [&](int i) -> uint32_t {                  // byte offset of this lane's row of tile i
+        const int n = 16 * (first + stride * i) + r16;
+        return (i < nmine && n < N) ? (uint32_t)(((size_t)n * K + kw0) * 2) : BUF_OOB;
+    };
+    auto load = [&](u32x4 (&q)[NJ][KS], int i) {
+        const uint32_t off = boff(i);
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            q[0][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 64 * s, 0, 0);
+            if constexpr (GATED) q[1][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off + 64 * s, 0, 0);
+        }
+    };
+
+    const size_t MN = (size_t)M * N;
+    auto tile = [&](const u32x4 (&q)[NJ][KS], int i) {
+        f32x4 acc[NJ][MT];
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const bf16x8 bf = __builtin_bit_cast(bf16x8, q[j][s]);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][s], bf, acc[j][mt], 0, 0, 0);
+            }
+        const int buf = i & 1;
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) red[buf][w][j * MT + mt][lane] = acc[j][mt];
+        __syncthreads();
+        // thread q < 64*MT sums slot (mt, lane p) over the 8 waves in order:
+        // rows 16*mt + 4*(p/16) + 0..3, column 16*tile + p%16
+        const int t = threadIdx.x;
+        if (t < WAVE * MT) {
+            const int mt = t / WAVE, p = t % WAVE;
+            f32x4 sum[NJ];
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                sum[j] = red[buf][0][j * MT + mt][p];
+#pragma unroll
+                for (int v = 1; v < STREAM_THREADS / WAVE; v++) sum[j] += red[buf][v][j * MT + mt][p];
+            }
+            const int n = 16 * (first + stride * i) + (p & 15);
+            const int m0 = 16 * mt + 4 * (p >> 4);
+            if (n < N) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + r;
+                    if (m < M) {
+                        const size_t o = (size_t)m * N + n;
+                        if (part) {
+                            float *pp = part + (size_t)blockIdx.y * NJ * MN + o;
+                            pp[0] = sum[0][r];
+                            if constexpr (GATED) pp[MN] = sum[1][r];
+                        } else if constexpr (GATED) {
+                            c[o] = silu_mul(sum[0][r], sum[1][r]);
+                        } else {
+                            c[o] = sum[0][r];
+                        }
+                    }
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int d = 0; d < ST; d++) load(bq[d], d);
+    for (int base = 0; base < nmine; base += ST) {
+#pragma unroll
+        for (int d = 0; d < ST; d++) {
+            if (base + d < nmine) tile(bq[d], base + d);     // uniform over the block
+            load(bq[d], base + d + ST);
+        }
+    }
+}
+
+// C = sum over the KSPLIT slices of part, in slice order (gated: silu(gate)*up)
+template <bool GATED>
+__global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ c,
+                                                            const float *__restrict__ part,
+                                                            size_t MN, int ksplit) {
+    constexpr int NJ = GATED ? 2 : 1;
+    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < MN; i += (size_t)gridDim.x * NTHREADS) {
+        float s0 = part[i], s1 = GATED ? part[MN + i] : 0.f;
+        for (int ks = 1; ks < ksplit; ks++) {
+            s0 += part[(size_t)ks * NJ * MN + i];
+            if constexpr (GATED) s1 += part[(size_t)ks * NJ * MN + MN + i];
+        }
+        c[i] = GATED ? silu_mul(s0, s1) : s0;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side of the shim
 // ---------------------------------------------------------------------------
 static int g_inited = 0;
@@ -1637,6 +1830,7 @@ static const int AM_BLOCKS = 1024;
 // bf16 copy of an fp32 A for the large-tile GEMMs (grown outside graph capture)
 static uint16_t *g_abf = nullptr;
 static size_t g_abf_elems = 0;
+static int g_cus = 256;            // compute units of the device (set at init)
 static const size_t ABF_INIT_ELEMS = (size_t)8192 * 3072;   // 48 MiB: M x K up to 8192 x 3072
 
 static int fail(hipError_t e, int code) {
@@ -1671,6 +1865,7 @@ extern "C" int qh_init(int device) {
         return QH_ENODEV;             // the code objects are built for gfx950 only
     }
     strncpy(g_devname, prop.gcnArchName, sizeof g_devname - 1);
+    if (prop.multiProcessorCount > 0) g_cus = prop.multiProcessorCount;
     {
         const char *e = getenv("QWEN3_HIP_NO_XCD_MAP");   // A/B switch for tile order
         g_no_xcd_map = (e && e[0] == '1') ? 1 : 0;
@@ -1829,7 +2024,14 @@ enum {
     // one register set, BK 64
     PLAN_X256x256s1 = 40,
     PLAN_XB256x256s1 = 41,
-    PLAN_COUNT = 42
+    // weight-streaming MFMA GEMM for M <= 64 (K % 256 == 0): KS chosen per
+    // shape, or forced (wave k range 32*KS; K / (256*KS) block slices)
+    PLAN_STREAM = 42,
+    PLAN_STREAM_KS1 = 43,
+    PLAN_STREAM_KS2 = 44,
+    PLAN_STREAM_KS4 = 45,
+    PLAN_STREAM_KS8 = 46,
+    PLAN_COUNT = 47
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -1839,11 +2041,33 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
     "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128", "xl64x256", "xl64x128",
-    "xl256x256s1", "xb256x256s1"};
+    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8"};
 static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return p >= PLAN_X128x256 && p <= PLAN_XB256x256s1; }
 static inline bool is_xb_plan(int p) {
     return (p >= PLAN_XB256x256 && p <= PLAN_XB128x128) || p == PLAN_XB256x256s1;
+}
+static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
+static inline int stream_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
+// the stream kernel's limits: M <= 64, whole 256-deep block slices, byte
+// offsets below 2 GiB (its out-of-range marker), 16-byte aligned rows
+static inline bool stream_fits(int M, int K, int N) {
+    return M >= 1 && M <= 64 && K > 0 && K % 256 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
+           (size_t)N * K * 2 < (1ull << 31);
+}
+// k steps of 32 per wave: the largest KS (fewest slices; none is best, it
+// needs no reduction pass) whose grid still gives every CU a block, else
+// the smallest; A fragments take 4*MT*KS registers (<= 64)
+static int stream_ks(int M, int K, int N, int cus) {
+    const int mt = stream_mt(M), kb = K / 256;
+    const long ntiles = (N + 15) / 16;
+    int smallest = 0;
+    for (int ks = 8; ks >= 1; ks /= 2) {
+        if (mt * ks > 16 || kb % ks) continue;
+        if (ntiles * (kb / ks) >= cus) return ks;
+        smallest = ks;
+    }
+    return smallest;
 }
 static inline int xl_bk(int p) {
     return (p == PLAN_X256x256 || p == PLAN_X128x256k32 || p == PLAN_X256x128k32 ||
@@ -1928,11 +2152,11 @@ template <int ROWS, bool GATED, bool PRO, bool MERGE = false>
 static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                              int K, int N, int cpl, const GemvPro &pro) {
     const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
-    const size_t lds = (size_t)(K + 8) * sizeof(float);
+    const size_t lds = (size_t)(4 * WAVE * cpl + 8) * sizeof(uint32_t);   // bf16 row padded to 512*cpl, partials
     // only the (ROWS, CPL) pairs launch_gemv1 can pick: <= 16 loads per lane
 #define QH_GEMV1_CASE(P)                                                                     \
     case P:                                                                                  \
-        if constexpr (ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16)                         \
+        if constexpr ((ROWS == 1 || ROWS * P * (GATED ? 2 : 1) <= 16) && (!MERGE || P == 4)) \
             hipLaunchKernelGGL((k_gemv1<ROWS, P, GATED, PRO, MERGE>), dim3(grid), dim3(NTHREADS), \
                                lds, g_stream, c, a, b, b2, K, N, pro);                       \
         else                                                                                 \
@@ -1984,6 +2208,7 @@ static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint1
 extern "C" int qh_gemv_merge(float *c, const float *part, const uint16_t *b, int K, int N) {
     if (!g_inited) return QH_ESTATE;
     if (!c || !part || !b || K != 2048 || N <= 0 || !aligned16(part) || !aligned16(b)) return QH_EINVAL;
+    if ((size_t)N * K * 2 >= (1ull << 31)) return QH_ETOOBIG;
     // K = 2048: 256 chunks of 16 bytes per row, 4 per lane; one row per wave
     // keeps >= 2048 waves for N = 1024 and 16 weight loads in flight per lane
     const int cpl = K / 8 / WAVE;
@@ -1994,7 +2219,8 @@ extern "C" int qh_gemv_merge(float *c, const float *part, const uint16_t *b, int
 template <int MR>
 static int launch_gemv_mr(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                           int K, int N, bool gated) {
-    if (MR == 1 && K <= 8 * WAVE * 8) return launch_gemv1(c, a, b, b2, K, N, gated);
+    if (MR == 1 && K <= 8 * WAVE * 8 && (size_t)N * K * 2 < (1ull << 31))   // k_gemv1's 32-bit offsets
+        return launch_gemv1(c, a, b, b2, K, N, gated);
     const size_t lds = (size_t)MR * K * sizeof(float);
     // rows per wave: enough waves to cover the GPU for small N, and up to 8
     // rows (16 loads of 16 B in flight per lane at K = 1024) for large N
@@ -2140,6 +2366,55 @@ static int launch_cvt_bf16(uint16_t *dst, const float *src, size_t n) {
     return QH_OK;
 }
 
+// weight-streaming GEMM: K % (256*KS) == 0, M <= 64, 16-byte aligned a, b,
+// b2 and sizes within stream_fits (checked by the caller).  K / (256*KS) > 1
+// slices sum through the workspace and one k_stream_reduce pass.
+template <int MT, int KS, bool GATED>
+static int launch_stream_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                           int M, int K, int N) {
+    constexpr int ST = KS >= 8 ? 2 : KS >= 4 ? 3 : KS >= 2 ? 4 : 8;   // tiles in flight per wave
+    const int ksplit = K / (256 * KS);
+    const int ntiles = (N + 15) / 16;
+    const int gx = ntiles < g_cus ? ntiles : g_cus;
+    float *part = nullptr;
+    const size_t MN = (size_t)M * N;
+    if (ksplit > 1) {
+        const size_t need = (size_t)ksplit * (GATED ? 2 : 1) * MN * sizeof(float);
+        if (need > g_abf_elems * sizeof(uint16_t)) return QH_ETOOBIG;
+        part = reinterpret_cast<float *>(g_abf);
+    }
+    hipLaunchKernelGGL((k_gemm_stream<MT, KS, ST, GATED>), dim3(gx, ksplit), dim3(STREAM_THREADS), 0,
+                       g_stream, c, part, a, b, b2, M, K, N, ntiles);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    if (ksplit > 1) {
+        size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
+        if (blocks > 1024) blocks = 1024;
+        hipLaunchKernelGGL((k_stream_reduce<GATED>), dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream,
+                           c, part, MN, ksplit);
+        HCHECK(hipGetLastError(), QH_ELAUNCH);
+    }
+    return QH_OK;
+}
+
+template <bool GATED>
+static int launch_stream(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                         int M, int K, int N, int ks) {
+    switch (stream_mt(M) * 100 + ks) {
+        case 101: return launch_stream_t<1, 1, GATED>(c, a, b, b2, M, K, N);
+        case 102: return launch_stream_t<1, 2, GATED>(c, a, b, b2, M, K, N);
+        case 104: return launch_stream_t<1, 4, GATED>(c, a, b, b2, M, K, N);
+        case 108: return launch_stream_t<1, 8, GATED>(c, a, b, b2, M, K, N);
+        case 201: return launch_stream_t<2, 1, GATED>(c, a, b, b2, M, K, N);
+        case 202: return launch_stream_t<2, 2, GATED>(c, a, b, b2, M, K, N);
+        case 204: return launch_stream_t<2, 4, GATED>(c, a, b, b2, M, K, N);
+        case 208: return launch_stream_t<2, 8, GATED>(c, a, b, b2, M, K, N);
+        case 401: return launch_stream_t<4, 1, GATED>(c, a, b, b2, M, K, N);
+        case 402: return launch_stream_t<4, 2, GATED>(c, a, b, b2, M, K, N);
+        case 404: return launch_stream_t<4, 4, GATED>(c, a, b, b2, M, K, N);
+        default: return QH_EINVAL;
+    }
+}
+
 // bf16-A large-tile GEMM for plan p (an xb plan); a is bf16 bits
 template <bool GATED>
 static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b, const uint16_t *b2,
@@ -2220,6 +2495,10 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_X64x128: return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x256k32: return launch_xl<128, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x128k32: return launch_xl<256, 128, 32, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_STREAM_KS1: return launch_stream<GATED>(c, a, b, b2, M, K, N, 1);
+        case PLAN_STREAM_KS2: return launch_stream<GATED>(c, a, b, b2, M, K, N, 2);
+        case PLAN_STREAM_KS4: return launch_stream<GATED>(c, a, b, b2, M, K, N, 4);
+        case PLAN_STREAM_KS8: return launch_stream<GATED>(c, a, b, b2, M, K, N, 8);
         default: return QH_EINVAL;
     }
 }
@@ -2251,6 +2530,19 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
         plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
     if (is_xb_plan(plan) && !abf_ensure((size_t)M * K))            // no room for the bf16 copy of A
         plan = PLAN_X128x256;
+    if (is_stream_plan(plan)) {
+        // KS must divide the slices and fit the A registers; more than one
+        // slice needs workspace for the fp32 partial sums
+        const bool fits = stream_fits(M, K, N);
+        const int ks = plan != PLAN_STREAM ? 1 << (plan - PLAN_STREAM_KS1) : fits ? stream_ks(M, K, N, g_cus) : 0;
+        bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16;
+        if (ok && K / (256 * ks) > 1) {
+            const size_t part = (size_t)(K / (256 * ks)) * (gated ? 2 : 1) * M * N * sizeof(float);
+            ok = abf_ensure((part + 1) / sizeof(uint16_t));
+        }
+        if (!ok) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
+        else plan = ks == 1 ? PLAN_STREAM_KS1 : ks == 2 ? PLAN_STREAM_KS2 : ks == 4 ? PLAN_STREAM_KS4 : PLAN_STREAM_KS8;
+    }
     return gated ? dispatch<true>(plan, c, a, b, b2, M, K, N)
                  : dispatch<false>(plan, c, a, b, nullptr, M, K, N);
 }
@@ -2423,6 +2715,7 @@ extern "C" int qh_gemv_pro(float *c, const qh_gemv_pro_t *p, const uint16_t *b, 
     if (!g_inited) return QH_ESTATE;
     if (!c || !p || !b || (gated && !b2) || !p->nw || (!p->x && !(p->emb && p->tok))) return QH_EINVAL;
     if (K <= 0 || N <= 0 || K % 8 || K > 8 * WAVE * 8) return QH_EINVAL;
+    if ((size_t)N * K * 2 >= (1ull << 31)) return QH_ETOOBIG;      // 32-bit weight offsets
     if (p->emb && p->emb_rows <= 0) return QH_EINVAL;
     if (!aligned16(c) || !aligned16(b) || (gated && !aligned16(b2)) || !aligned16(p->nw) ||
         (p->x && !aligned16(p->x)) || (p->r && !aligned16(p->r)) ||

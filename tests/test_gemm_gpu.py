@@ -164,8 +164,29 @@ def test_every_kernel_variant(plan, M, K, N):
     numerics.compare(c, a, b, M, K, N, rows=numerics.pick_rows(M, 40))
 
 
-@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe", "xl")) or p == "gemv"])
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400)])
+STREAM_PLANS = [p for p in ALL_PLANS if p.startswith("stream")]
+
+
+@pytest.mark.parametrize("plan", STREAM_PLANS)
+@pytest.mark.parametrize("M,K,N", [(5, 256, 100), (16, 1024, 3072), (33, 512, 77), (64, 2048, 1000),
+                                   (64, 3072, 1024), (7, 1024, 9000), (48, 768, 4113), (64, 1024, 16)])
+def test_stream_variants(plan, M, K, N):
+    """The weight-streaming kernel for M <= 64: every forced KS (one block
+    slice, or several summed by the reduction pass), rows of M and N that
+    leave partial tiles, and N large enough that blocks walk several tiles."""
+    a, b = inputs(M, K, N, 4200 + M + K + N)
+    abi.force_plan(abi.PLANS[plan])
+    try:
+        c = run_gemm(a, b, M, K, N)
+    finally:
+        abi.force_plan(0)
+    numerics.compare(c, a, b, M, K, N, rows=numerics.pick_rows(M, 40),
+                     cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+
+
+@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe", "xl", "stream")) or p == "gemv"])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
+                                   (40, 2048, 300), (16, 1024, 3072)])
 def test_every_kernel_variant_gated(plan, M, K, N):
     x = oracle.f32_bf16_normal(M * K, 4100 + M)
     wg = oracle.bf16_normal(N * K, 4101 + M, 0.02)
