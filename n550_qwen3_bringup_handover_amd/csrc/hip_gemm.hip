@@ -2055,16 +2055,20 @@ static inline bool stream_fits(int M, int K, int N) {
     return M >= 1 && M <= 64 && K > 0 && K % 256 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
            (size_t)N * K * 2 < (1ull << 31);
 }
-// k steps of 32 per wave: the largest KS (fewest slices; none is best, it
-// needs no reduction pass) whose grid still gives every CU a block, else
-// the smallest; A fragments take 4*MT*KS registers (<= 64)
+// k steps of 32 per wave (KS must divide K/256, and the A fragments, 4*MT*KS
+// registers, must fit in 64): no K split while there are >= 128 tiles of 16
+// rows; else the largest KS whose slices still give >= 192 blocks (measured
+// on MI355X: a split costs a reduction pass, ~2 us, but 64 blocks leave
+// three quarters of the chip idle)
 static int stream_ks(int M, int K, int N, int cus) {
+    (void)cus;
     const int mt = stream_mt(M), kb = K / 256;
     const long ntiles = (N + 15) / 16;
     int smallest = 0;
     for (int ks = 8; ks >= 1; ks /= 2) {
         if (mt * ks > 16 || kb % ks) continue;
-        if (ntiles * (kb / ks) >= cus) return ks;
+        const long blocks = ntiles * (kb / ks);
+        if ((kb / ks == 1 && ntiles >= 128) || blocks >= 192) return ks;
         smallest = ks;
     }
     return smallest;
@@ -2099,6 +2103,11 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
+    // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
+    // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
+    // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
+    // stay on the tiles, which hold both weight rows of a block in one pass
+    if (!gated && stream_fits(M, K, N) && (M <= 16 || (M <= 32 && N <= 2048))) return PLAN_STREAM;
     const int bno = gated ? 2 : 1;   // gated tiles produce half as many output columns
     auto blocks = [&](int bm, int bn) {
         return (long)((M + bm - 1) / bm) * (long)((N + bn / bno - 1) / (bn / bno));
