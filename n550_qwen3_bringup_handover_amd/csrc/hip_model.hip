@@ -37,16 +37,59 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
+// Cross-lane reductions without LDS round trips: DPP within rows of 16 lanes
+// (quad permutes for xor 1 / xor 2, the half-row and row mirrors, or a
+// rotation by 8), then the gfx950 permlane swaps across rows (xor 16, xor
+// 32).  Each step combines a lane with its partner, so partners end with the
+// same bits: the results are identical in every lane of the group.
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ f32x2 swap16(float x) {     // {lanes l and l ^ 16}, in lane order
+    const auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return f32x2{__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1])};
+}
+__device__ __forceinline__ f32x2 swap32(float x) {     // {lanes l and l ^ 32}, in lane order
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return f32x2{__builtin_bit_cast(float, (int)p[0]), __builtin_bit_cast(float, (int)p[1])};
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-    return v;
+    v += dpp_partner<0xB1>(v);      // quad_perm [1,0,3,2]
+    v += dpp_partner<0x4E>(v);      // quad_perm [2,3,0,1]
+    v += dpp_partner<0x141>(v);     // row_half_mirror
+    v += dpp_partner<0x140>(v);     // row_mirror
+    f32x2 p = swap16(v);
+    v = p.x + p.y;
+    p = swap32(v);
+    return p.x + p.y;
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
-    return v;
+    v = fmaxf(v, dpp_partner<0xB1>(v));
+    v = fmaxf(v, dpp_partner<0x4E>(v));
+    v = fmaxf(v, dpp_partner<0x141>(v));
+    v = fmaxf(v, dpp_partner<0x140>(v));
+    f32x2 p = swap16(v);
+    v = fmaxf(p.x, p.y);
+    p = swap32(v);
+    return fmaxf(p.x, p.y);
 }
+// sum over lanes l, l ^ 8, l ^ 16, ..., l ^ 56 (the 8 lanes holding one value
+// column): rotation by 8 within each row of 16, then the two permlane swaps
+__device__ __forceinline__ float sum_stride8(float v) {
+    v += dpp_partner<0x128>(v);     // row_ror:8
+    f32x2 p = swap16(v);
+    v = p.x + p.y;
+    p = swap32(v);
+    return p.x + p.y;
+}
+
+// raw buffer resource over [p, p + bytes); loads past num_records return
+// zeros and read no memory
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+#define BUF_OOB 0x80000000u            // an offset past every buffer below 2 GiB
 
 // ---------------------------------------------------------------------------
 // rows: x[row] = emb[tok[row]] (bf16 -> fp32)   when emb is set, else
@@ -322,37 +365,50 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     __shared__ float sc[4][GRP][P];              // per-wave partial scores
     __shared__ float pe[GRP][P];                 // softmax weights of the pass
 
-    const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
-    const f32x4 *vbase = reinterpret_cast<const f32x4 *>(vc + (size_t)g * max_seq * HD);
     const f32x4 *vnew4 = reinterpret_cast<const f32x4 *>(qkv + VOFF + (size_t)g * HD);
     const int vch = 8 * wave + (lane & 7);       // V chunk (16 bytes) of this lane
     const int vp = lane >> 3;                    // V positions vp + 8j of the pass
 
+    // 1. prologue sources first: waves 0/1 the rows of the two query heads,
+    //    wave 2 the new k (wave 3 repeats wave 2's loads), norm weights, the
+    //    rope angles of this position and the new v chunk -- all
+    //    unconditional, so a wave later waits for these alone
+    const int hw = wave < GRP + 1 ? wave : GRP;
+    const float *src = hw < GRP ? qkv + (size_t)(g * GRP + hw) * HD : qkv + KOFF + (size_t)g * HD;
+    const uint16_t *nwp = hw < GRP ? qn : kn;
+    const float x0 = src[lane], x1 = src[lane + 64];
+    const float w0 = bf16f(nwp[lane]), w1 = bf16f(nwp[lane + 64]);
+    const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
+    const f32x4 vnew = vnew4[vch];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. the K and V cache reads of a pass: buffer loads whose offset is out
+    //    of range (returns zeros, reads nothing) past this block's positions
+    //    and at the new position, which comes from sk / vnew instead
+    const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kc + (size_t)g * HD * max_seq, (size_t)HD * max_seq * 4);
+    const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc + (size_t)g * max_seq * HD, (size_t)max_seq * HD * 4);
     f32x4 kk[8], vv[8];
     auto load_pass = [&](int base) {
         const int tk = t0 + base + lane;
-        if (base + lane < n && tk < pos) {
+        const bool kin = base + lane < n && tk < pos;
 #pragma unroll
-            for (int j = 0; j < 8; j++) kk[j] = kbase[(size_t)(8 * wave + j) * max_seq + tk];
-        }
+        for (int j = 0; j < 8; j++)
+            kk[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                        rk, kin ? (uint32_t)(((8 * wave + j) * max_seq + tk) * 16) : BUF_OOB, 0, 0));
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = base + vp + 8 * j;
             const int tv = t0 + i;
-            vv[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (i < n) vv[j] = tv < pos ? vbase[(size_t)tv * (HD / 4) + vch] : vnew4[vch];
+            vv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                        rv, (i < n && tv < pos) ? (uint32_t)((tv * (HD / 4) + vch) * 16) : BUF_OOB, 0, 0));
         }
     };
     load_pass(0);
+    __builtin_amdgcn_sched_barrier(0);
 
-    // QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
+    // 3. QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
     if (wave < GRP + 1) {
-        const float *src = wave < GRP ? qkv + (size_t)(g * GRP + wave) * HD : qkv + KOFF + (size_t)g * HD;
-        const uint16_t *w = wave < GRP ? qn : kn;
         float *dst = wave < GRP ? sq + wave * HD : sk;
-        const float x0 = src[lane], x1 = src[lane + 64];
-        const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
-        const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float sc_ = 1.0f / sqrtf(ss / (float)HD + eps);
         const float y0 = (x0 * sc_) * w0, y1 = (x1 * sc_) * w1;
@@ -360,9 +416,9 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
         dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
     }
     __syncthreads();
-    if (sp == 0 && tid < HD) {                   // one block per kv head writes the new entry
-        kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = sk[tid];
-        vc[((size_t)g * max_seq + pos) * HD + tid] = qkv[VOFF + (size_t)g * HD + tid];
+    if (sp == 0) {                               // one block per kv head writes the new entry
+        if (tid < HD) kc[(((size_t)g * (HD / 4) + (tid >> 2)) * max_seq + pos) * 4 + (tid & 3)] = sk[tid];
+        if (vp == 0) reinterpret_cast<f32x4 *>(vc + ((size_t)g * max_seq + pos) * HD)[vch] = vnew;
     }
 
     float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
@@ -371,25 +427,19 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
         if (base > 0) load_pass(base);
         // partial scores over this wave's 32 dims
         {
-            const int tk = t0 + base + lane;
-            const f32x4 *kp = kk;
-            f32x4 knew[8];
-            if (tk == pos) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) knew[j] = reinterpret_cast<const f32x4 *>(sk)[8 * wave + j];
-                kp = knew;
-            }
+            // the new position's k comes from sk (a per-element select keeps
+            // kk in registers; positions past n read zeros and are masked below)
+            const bool isnew = t0 + base + lane == pos;
             float a0 = 0.0f, a1 = 0.0f;
-            if (base + lane < n) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[8 * wave + j];
-                    const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[8 * wave + j];
-                    a0 = fmaf(q0.x, kp[j].x, a0); a0 = fmaf(q0.y, kp[j].y, a0);
-                    a0 = fmaf(q0.z, kp[j].z, a0); a0 = fmaf(q0.w, kp[j].w, a0);
-                    a1 = fmaf(q1.x, kp[j].x, a1); a1 = fmaf(q1.y, kp[j].y, a1);
-                    a1 = fmaf(q1.z, kp[j].z, a1); a1 = fmaf(q1.w, kp[j].w, a1);
-                }
+            for (int j = 0; j < 8; j++) {
+                const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[8 * wave + j];
+                const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[8 * wave + j];
+                const f32x4 kj = isnew ? reinterpret_cast<const f32x4 *>(sk)[8 * wave + j] : kk[j];
+                a0 = fmaf(q0.x, kj.x, a0); a0 = fmaf(q0.y, kj.y, a0);
+                a0 = fmaf(q0.z, kj.z, a0); a0 = fmaf(q0.w, kj.w, a0);
+                a1 = fmaf(q1.x, kj.x, a1); a1 = fmaf(q1.y, kj.y, a1);
+                a1 = fmaf(q1.z, kj.z, a1); a1 = fmaf(q1.w, kj.w, a1);
             }
             sc[wave][0][lane] = a0;
             sc[wave][1][lane] = a1;
@@ -416,23 +466,19 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
         o1 *= r1;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float w0 = pe[0][vp + 8 * j], w1 = pe[1][vp + 8 * j];   // 0 beyond n
-            o0.x = fmaf(w0, vv[j].x, o0.x); o0.y = fmaf(w0, vv[j].y, o0.y);
-            o0.z = fmaf(w0, vv[j].z, o0.z); o0.w = fmaf(w0, vv[j].w, o0.w);
-            o1.x = fmaf(w1, vv[j].x, o1.x); o1.y = fmaf(w1, vv[j].y, o1.y);
-            o1.z = fmaf(w1, vv[j].z, o1.z); o1.w = fmaf(w1, vv[j].w, o1.w);
+            const float pw0 = pe[0][vp + 8 * j], pw1 = pe[1][vp + 8 * j];   // 0 beyond n
+            const f32x4 v = t0 + base + vp + 8 * j == pos ? vnew : vv[j];
+            o0.x = fmaf(pw0, v.x, o0.x); o0.y = fmaf(pw0, v.y, o0.y);
+            o0.z = fmaf(pw0, v.z, o0.z); o0.w = fmaf(pw0, v.w, o0.w);
+            o1.x = fmaf(pw1, v.x, o1.x); o1.y = fmaf(pw1, v.y, o1.y);
+            o1.z = fmaf(pw1, v.z, o1.z); o1.w = fmaf(pw1, v.w, o1.w);
         }
         __syncthreads();                          // sc / pe reused by the next pass
     }
 
     // sum the 8 lanes of each chunk (lanes c, c+8, ..., c+56) and write
-#pragma unroll
-    for (int msk = 8; msk <= 32; msk <<= 1) {
-        o0.x += __shfl_xor(o0.x, msk); o0.y += __shfl_xor(o0.y, msk);
-        o0.z += __shfl_xor(o0.z, msk); o0.w += __shfl_xor(o0.w, msk);
-        o1.x += __shfl_xor(o1.x, msk); o1.y += __shfl_xor(o1.y, msk);
-        o1.z += __shfl_xor(o1.z, msk); o1.w += __shfl_xor(o1.w, msk);
-    }
+    o0 = f32x4{sum_stride8(o0.x), sum_stride8(o0.y), sum_stride8(o0.z), sum_stride8(o0.w)};
+    o1 = f32x4{sum_stride8(o1.x), sum_stride8(o1.y), sum_stride8(o1.z), sum_stride8(o1.w)};
     float *pp = part + (size_t)(g * S + sp) * GRP * QM_ATT_PART;
     if (lane < 8) {
         reinterpret_cast<f32x4 *>(pp + 4)[vch] = o0;
