@@ -1320,7 +1320,8 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
-                                                        int M, int K, int N, TileMap map) {
+                                                        int M, int K, int N, TileMap map,
+                                                        float *__restrict__ part, int kslice) {
     using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     constexpr int CPR = X::CPR;
     __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
@@ -1336,7 +1337,10 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * X::BNO;
-    const int nk = K / BK;
+    // split K: blockIdx.y owns k range [kslice*y, kslice*(y+1)); with part set
+    // the raw fp32 sums go to part[y][j][M][N] (j: gate, up for GATED)
+    const int nk = kslice / BK;
+    const int kofs = blockIdx.y * kslice;
 
     const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * (ABF16 ? 2 : 4));
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
@@ -1394,7 +1398,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     // SET: register set (and, for store and compute, LDS slot), compile-time
     auto load = [&](int step, auto SET) {
         constexpr int set = SETS == 1 ? 0 : decltype(SET)::value;
-        const int ka = step * BK * (ABF16 ? 2 : 4), kb = step * BK * 2;   // scalar byte offsets
+        const int ka = (kofs + step * BK) * (ABF16 ? 2 : 4), kb = (kofs + step * BK) * 2;   // scalar byte offsets
 #pragma unroll
         for (int i = 0; i < X::A_LOADS; i++)
             areg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoffs[i], ka, 0);
@@ -1519,6 +1523,32 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
 
     // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
     // column lane%32
+    if (part) {                                  // uniform: one K slice's raw sums
+        constexpr int NJ = GATED ? 2 : 1;
+        constexpr int TNO = X::TN / NJ;
+        const size_t MN = (size_t)M * N;
+        float *pp = part + (size_t)blockIdx.y * NJ * MN;
+#pragma unroll
+        for (int i = 0; i < X::TM; i++) {
+            const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
+#pragma unroll
+            for (int j = 0; j < TNO; j++) {
+                // the columns of the direct epilogue below
+                const int col = n0 + (GATED ? wn * (X::BNO / 2) : wn * X::WTN) + 32 * j + lrow;
+                if (col < N) {
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const int row = rbase + 8 * (v >> 2) + (v & 3);
+                        if (row < M) {
+                            pp[(size_t)row * N + col] = acc[i][j][v];
+                            if constexpr (GATED) pp[MN + (size_t)row * N + col] = acc[i][j + TNO][v];
+                        }
+                    }
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < X::TM; i++) {
         const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
@@ -1831,6 +1861,9 @@ static const int AM_BLOCKS = 1024;
 static uint16_t *g_abf = nullptr;
 static size_t g_abf_elems = 0;
 static int g_cus = 256;            // compute units of the device (set at init)
+#define PART_INIT_BYTES ((size_t)32 << 20)
+static float *g_part = nullptr;    // split-K partial sums of the large-tile GEMM (grown on demand)
+static size_t g_part_bytes = 0;
 static const size_t ABF_INIT_ELEMS = (size_t)8192 * 3072;   // 48 MiB: M x K up to 8192 x 3072
 
 static int fail(hipError_t e, int code) {
@@ -1875,6 +1908,10 @@ extern "C" int qh_init(int device) {
     HCHECK(hipMalloc((void **)&g_am_i, AM_BLOCKS * sizeof(int)), QH_ENOMEM);
     HCHECK(hipMalloc((void **)&g_abf, ABF_INIT_ELEMS * sizeof(uint16_t)), QH_ENOMEM);
     g_abf_elems = ABF_INIT_ELEMS;
+    // split-K partials: 32 MiB covers the Qwen3-0.6B projection shapes up to M = 2048
+    // (e.g. 4 slices x 1024 x 1024 fp32); grown outside graph capture if needed
+    HCHECK(hipMalloc((void **)&g_part, PART_INIT_BYTES), QH_ENOMEM);
+    g_part_bytes = PART_INIT_BYTES;
     g_device = device;
     g_inited = 1;
     return QH_OK;
@@ -1890,6 +1927,9 @@ extern "C" void qh_shutdown(void) {
     (void)hipFree(g_abf);
     g_abf = nullptr;
     g_abf_elems = 0;
+    (void)hipFree(g_part);
+    g_part = nullptr;
+    g_part_bytes = 0;
     (void)hipFree(g_am_v);
     (void)hipFree(g_am_i);
     g_am_v = nullptr;
@@ -2031,7 +2071,9 @@ enum {
     PLAN_STREAM_KS2 = 44,
     PLAN_STREAM_KS4 = 45,
     PLAN_STREAM_KS8 = 46,
-    PLAN_COUNT = 47
+    // 128x128 large tiles with K split over blocks when the tiles leave CUs idle
+    PLAN_X128x128SK = 47,
+    PLAN_COUNT = 48
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2041,9 +2083,9 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
     "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128", "xl64x256", "xl64x128",
-    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8"};
+    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "xl128x128sk"};
 static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
-static inline bool is_xl_plan(int p) { return p >= PLAN_X128x256 && p <= PLAN_XB256x256s1; }
+static inline bool is_xl_plan(int p) { return (p >= PLAN_X128x256 && p <= PLAN_XB256x256s1) || p == PLAN_X128x128SK; }
 static inline bool is_xb_plan(int p) {
     return (p >= PLAN_XB256x256 && p <= PLAN_XB128x128) || p == PLAN_XB256x256s1;
 }
@@ -2125,6 +2167,11 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
         if (M >= 1024) {
+            // K-heavy shapes with <= 128 tiles of 128x128 (o, down up to M =
+            // 2048): split K over the idle CUs (measured: 1024x3072x1024
+            // 36.0 -> 21.5 us, 1024x2048x1024 23.3 -> 18.0 us); at K = 1024
+            // the partials' round trip costs more than it saves
+            if (!gated && K >= 2048 && blocks(128, 128) <= 128) return PLAN_X128x128SK;
             if (!gated && blocks(256, 256) >= 256)
                 return (size_t)M * K <= g_abf_elems ? PLAN_XB256x256s1 : PLAN_X256x256;
             if (gated && M >= 2048 && (size_t)M * K <= g_abf_elems) return PLAN_XB128x128;
@@ -2349,18 +2396,47 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     return QH_OK;
 }
 
+// the split-K workspace holds at least `bytes` (grows only outside capture)
+static bool part_ensure(size_t bytes) {
+    if (bytes <= g_part_bytes) return true;
+    if (g_capturing) return false;
+    float *p = nullptr;
+    if (hipMalloc((void **)&p, bytes) != hipSuccess) { (void)hipGetLastError(); return false; }
+    (void)hipStreamSynchronize(g_stream);      // the old buffer may still be read
+    (void)hipFree(g_part);
+    g_part = p;
+    g_part_bytes = bytes;
+    return true;
+}
+
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
 template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
-                     int M, int K, int N) {
+                     int M, int K, int N, bool allow_split = false) {
     using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles), dim3(NTHREADS), 0,
-                       g_stream, c, a, b, b2, M, K, N, map);
+    // split K when the tiles leave most CUs idle: slices of >= 4 stages,
+    // doubled until every CU has a block; the fp32 partials need workspace
+    int ks = 1;
+    if (allow_split)
+        while (tiles * ks < g_cus && (K / (2 * ks)) % BK == 0 && K / (2 * ks) >= 4 * BK) ks *= 2;
+    float *part = nullptr;
+    const size_t MN = (size_t)M * N;
+    if (ks > 1 && !part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) ks = 1;
+    if (ks > 1) part = g_part;
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, ks), dim3(NTHREADS), 0,
+                       g_stream, c, a, b, b2, M, K, N, map, part, K / ks);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
+    if (ks > 1) {
+        size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL((k_stream_reduce<GATED>), dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream,
+                           c, part, MN, ks);
+        HCHECK(hipGetLastError(), QH_ELAUNCH);
+    }
     return QH_OK;
 }
 
@@ -2499,6 +2575,7 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x128: return launch_xl<256, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X128x128SK: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N, true);
         case PLAN_X256x256s1: return launch_xl<256, 256, 64, GATED, false, 1>(c, a, b, b2, M, K, N);
         case PLAN_X64x256: return launch_xl<64, 256, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128: return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);

@@ -343,14 +343,18 @@ def test_bf16a_gated_and_rejects_bad_k():
 
 
 @pytest.mark.parametrize("M,K,N,gated", [(1024, 1024, 4096, False), (2048, 1024, 3072, True),
-                                         (1536, 3072, 1024, False)])
+                                         (1536, 3072, 1024, False), (1024, 2048, 1024, False)])
 def test_large_m_automatic_plans(M, K, N, gated):
     """The plans chosen from M = 1024 on (256 x 256 tiles, bf16 rounding pass
-    + 128 x 128 tiles for gate|up, 128 x 128) on a row subset."""
+    + 128 x 128 tiles for gate|up, 128 x 128, and 128 x 128 with K split over
+    blocks for the K-heavy shapes) on a row subset; the split-K sum is added
+    in slice order, so a second run gives the same bits."""
     a = oracle.f32_bf16_normal(M * K, 970 + M)
     if not gated:
         b = oracle.bf16_normal(N * K, 971, 0.02)
-        numerics.compare(run_gemm(a, b, M, K, N), a, b, M, K, N, rows=numerics.pick_rows(M, 24))
+        c = run_gemm(a, b, M, K, N)
+        numerics.compare(c, a, b, M, K, N, rows=numerics.pick_rows(M, 24))
+        assert np.array_equal(c.view(np.uint32), run_gemm(a, b, M, K, N).view(np.uint32))
     else:
         wg = oracle.bf16_normal(N * K, 972, 0.02)
         wu = oracle.bf16_normal(N * K, 973, 0.02)
