@@ -183,4 +183,4 @@ PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4
          "xl64x256": 38, "xl64x128": 39,
          "xl256x256s1": 40, "xb256x256s1": 41,
          "stream": 42, "stream-ks1": 43, "stream-ks2": 44, "stream-ks4": 45, "stream-ks8": 46,
-         "xl128x128sk": 47}
+         "xl128x128sk": 47, "skinny": 48}

@@ -1823,19 +1823,177 @@ __global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__rest
     }
 }
 
-// C = sum over the KSPLIT slices of part, in slice order (gated: silu(gate)*up)
+// ---------------------------------------------------------------------------
+// Skinny GEMM for M <= 64 with small N (batched-decode projections)
+// ---------------------------------------------------------------------------
+// C[M,N] = A[M,K]·B[N,K]^T with A short: blockIdx.x owns 64 rows of B (four
+// waves, 16 rows each) and blockIdx.y a K slice of KSL (a multiple of 64, at
+// most 256).  The block stages its slice of A once in LDS as bf16 (RNE), rows
+// of 16-byte chunks XOR-swizzled by row, so that the four waves read their
+// v_mfma_f32_16x16x32_bf16 A fragments from one copy instead of each block
+// re-reading A per 16-row tile; each wave issues all of its B loads (one 16-B
+// chunk per lane per 32-deep step) before the staging wait, so the weight
+// stream is in flight while A is converted.  No cross-wave reduction: a wave
+// owns its 16 output columns.  With more than one slice the fp32 sums go to
+// part[slice][j][M][N] (j = gate/up when GATED) and k_stream_reduce adds the
+// slices in order; otherwise C (or silu(gate)*up) is written directly.
+// Loads past M and past N are buffer loads at out-of-range offsets (zeros).
+template <int MT, bool GATED>
+__global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c, float *__restrict__ part,
+                                                          const float *__restrict__ a,
+                                                          const uint16_t *__restrict__ b,
+                                                          const uint16_t *__restrict__ b2,
+                                                          int M, int K, int N, int ksl) {
+    constexpr int NJ = GATED ? 2 : 1;
+    constexpr int KSMAX = 256 / 32;                      // 32-deep steps per slice, at most
+    __shared__ __align__(16) u32x4 sa[MT * 16 * (256 / 8)];   // [row][chunk ^ swz(row)], bf16
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int k0 = blockIdx.y * ksl;
+    const int ncs = ksl >> 3;                           // 16-byte chunks per row of the slice
+    const int nst = ksl >> 5;                           // 32-deep steps
+
+    // 1. the block's A slice first (8 floats per chunk, CPT chunks per
+    //    thread; chunks past the slice or rows past M read zeros) ...
+    constexpr int CPT = MT * 16 * (256 / 8) / NTHREADS;
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * K * 4);
+    const int total = MT * 16 * ncs;                     // chunks of the staged slice
+    u32x4 alo[CPT], ahi[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int q = tid + NTHREADS * i;
+        const int m = q / ncs, ch = q % ncs;
+        const uint32_t off = (q < total && m < M) ? (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4) : BUF_OOB;
+        alo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
+        ahi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. ... then this wave's B chunks: row n of its 16, k = k0 + 32 s + 8 g
+    //    (in flight while A is converted; loads complete in order, so a wait
+    //    for A does not wait for these)
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
+    const int n = blockIdx.x * 64 + w * 16 + r16;
+    const uint32_t boff = n < N ? (uint32_t)(((size_t)n * K + k0 + 8 * g) * 2) : BUF_OOB;
+    u32x4 bq[NJ][KSMAX];
+#pragma unroll
+    for (int s = 0; s < KSMAX; s++) {
+        const uint32_t off = (s < nst && n < N) ? boff + 64u * s : BUF_OOB;
+        bq[0][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
+        if constexpr (GATED) bq[1][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // the A slice -> LDS as bf16 (RNE), 16-byte chunks XOR-swizzled by row
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+        const int q = tid + NTHREADS * i;
+        const int m = q / ncs, ch = q % ncs;
+        u32x4 v;
+        v.x = pack_bf16x2(__uint_as_float(alo[i].x), __uint_as_float(alo[i].y));
+        v.y = pack_bf16x2(__uint_as_float(alo[i].z), __uint_as_float(alo[i].w));
+        v.z = pack_bf16x2(__uint_as_float(ahi[i].x), __uint_as_float(ahi[i].y));
+        v.w = pack_bf16x2(__uint_as_float(ahi[i].z), __uint_as_float(ahi[i].w));
+        if (q < total) sa[m * ncs + (ch ^ (m & 7))] = v;
+    }
+    __syncthreads();
+
+    // 3. MFMA over the slice: A fragment rows 16 mt + r16, chunk 4 s + g
+    f32x4 acc[NJ][MT];
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KSMAX; s++) {
+        if (s < nst) {                                   // uniform
+            bf16x8 af[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const int m = 16 * mt + r16;
+                af[mt] = __builtin_bit_cast(bf16x8, sa[m * ncs + ((4 * s + g) ^ (m & 7))]);
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const bf16x8 bf = __builtin_bit_cast(bf16x8, bq[j][s]);
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[j][mt], 0, 0, 0);
+            }
+        }
+    }
+
+    // 4. lane holds rows 16 mt + 4 g + r, column n
+    if (n < N) {
+        const size_t MN = (size_t)M * N;
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = 16 * mt + 4 * g + r;
+                if (m < M) {
+                    const size_t o = (size_t)m * N + n;
+                    if (part) {
+                        float *pp = part + (size_t)blockIdx.y * NJ * MN + o;
+                        pp[0] = acc[0][mt][r];
+                        if constexpr (GATED) pp[MN] = acc[1][mt][r];
+                    } else if constexpr (GATED) {
+                        c[o] = silu_mul(acc[0][mt][r], acc[1][mt][r]);
+                    } else {
+                        c[o] = acc[0][mt][r];
+                    }
+                }
+            }
+    }
+}
+
+// C = sum over the KSPLIT slices of part, in slice order (gated: silu(gate)*up).
+// Four outputs per thread; the loads of every slice (at most RMAX) go out
+// before the first add, so the pass costs one memory round trip, not one per
+// slice.  Requires MN % 4 == 0 and 16-byte aligned c and part (else the
+// scalar tail below handles the last MN % 4).
+#define RMAX 16
 template <bool GATED>
 __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ c,
                                                             const float *__restrict__ part,
                                                             size_t MN, int ksplit) {
     constexpr int NJ = GATED ? 2 : 1;
-    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < MN; i += (size_t)gridDim.x * NTHREADS) {
-        float s0 = part[i], s1 = GATED ? part[MN + i] : 0.f;
-        for (int ks = 1; ks < ksplit; ks++) {
-            s0 += part[(size_t)ks * NJ * MN + i];
-            if constexpr (GATED) s1 += part[(size_t)ks * NJ * MN + MN + i];
+    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(part, (size_t)ksplit * NJ * MN * 4);
+    const size_t n4 = MN / 4;
+    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n4; i += (size_t)gridDim.x * NTHREADS) {
+        f32x4 v[NJ][RMAX];
+#pragma unroll
+        for (int ks = 0; ks < RMAX; ks++)
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                const size_t e = ((size_t)ks * NJ + j) * MN + 4 * i;     // element offset
+                v[j][ks] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               rp, ks < ksplit && e * 4 < 0x80000000ull ? (uint32_t)(e * 4) : BUF_OOB, 0, 0));
+            }
+        f32x4 s0 = v[0][0], s1 = GATED ? v[NJ - 1][0] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 1; ks < RMAX; ks++)
+            if (ks < ksplit) {
+                s0 += v[0][ks];
+                if constexpr (GATED) s1 += v[1][ks];
+            }
+        f32x4 o = s0;
+        if constexpr (GATED) o = f32x4{silu_mul(s0.x, s1.x), silu_mul(s0.y, s1.y), silu_mul(s0.z, s1.z), silu_mul(s0.w, s1.w)};
+        if (((uintptr_t)c & 15) == 0) {
+            reinterpret_cast<f32x4 *>(c)[i] = o;
+        } else {                                     // C only 4-byte aligned
+            c[4 * i] = o.x; c[4 * i + 1] = o.y; c[4 * i + 2] = o.z; c[4 * i + 3] = o.w;
         }
-        c[i] = GATED ? silu_mul(s0, s1) : s0;
+    }
+    if (blockIdx.x == 0 && threadIdx.x < MN % 4) {       // tail
+        const size_t i = n4 * 4 + threadIdx.x;
+        float t0 = part[i], t1 = GATED ? part[MN + i] : 0.f;
+        for (int ks = 1; ks < ksplit; ks++) {
+            t0 += part[(size_t)ks * NJ * MN + i];
+            if constexpr (GATED) t1 += part[(size_t)ks * NJ * MN + MN + i];
+        }
+        c[i] = GATED ? silu_mul(t0, t1) : t0;
     }
 }
 
@@ -2073,7 +2231,9 @@ enum {
     PLAN_STREAM_KS8 = 46,
     // 128x128 large tiles with K split over blocks when the tiles leave CUs idle
     PLAN_X128x128SK = 47,
-    PLAN_COUNT = 48
+    // skinny M <= 64: A slice staged in LDS, K split over blocks (K % 64 == 0)
+    PLAN_SKINNY = 48,
+    PLAN_COUNT = 49
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2083,7 +2243,7 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
     "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128", "xl64x256", "xl64x128",
-    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "xl128x128sk"};
+    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "xl128x128sk", "skinny"};
 static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return (p >= PLAN_X128x256 && p <= PLAN_XB256x256s1) || p == PLAN_X128x128SK; }
 static inline bool is_xb_plan(int p) {
@@ -2145,6 +2305,14 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
+    // K-heavy, narrow shapes at M <= 64 (o and down of batched decode): the
+    // skinny kernel, A slices staged once per block and K split over blocks
+    // (measured on MI355X: 64x3072x1024 13.6 -> 10.1 us, 48x2048x1024
+    // 10.0 -> 8.9 us, 16x3072x1024 8.1 -> 6.4 us); at K = 1024 the slices'
+    // partial sums cost more than they save
+    if (!gated && M <= 64 && K >= 2048 && K <= 4096 && K % 64 == 0 && N <= 2048 &&
+        (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31))
+        return PLAN_SKINNY;
     // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
     // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
     // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
@@ -2398,6 +2566,7 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
 
 // the split-K workspace holds at least `bytes` (grows only outside capture)
 static bool part_ensure(size_t bytes) {
+    if (bytes >= (1ull << 31)) return false;           // the reduction's 32-bit offsets
     if (bytes <= g_part_bytes) return true;
     if (g_capturing) return false;
     float *p = nullptr;
@@ -2422,7 +2591,7 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
     // doubled until every CU has a block; the fp32 partials need workspace
     int ks = 1;
     if (allow_split)
-        while (tiles * ks < g_cus && (K / (2 * ks)) % BK == 0 && K / (2 * ks) >= 4 * BK) ks *= 2;
+        while (tiles * ks < g_cus && 2 * ks <= RMAX && (K / (2 * ks)) % BK == 0 && K / (2 * ks) >= 4 * BK) ks *= 2;
     float *part = nullptr;
     const size_t MN = (size_t)M * N;
     if (ks > 1 && !part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) ks = 1;
@@ -2479,6 +2648,54 @@ static int launch_stream_t(float *c, const float *a, const uint16_t *b, const ui
         HCHECK(hipGetLastError(), QH_ELAUNCH);
     }
     return QH_OK;
+}
+
+// K slices of the skinny kernel: multiples of 64, at most 256 deep; the
+// fewest that give every CU a 64-row block (else the most)
+static int skinny_slices(int K, int N) {
+    const long nblk = (N + 63) / 64;
+    int best = 0;
+    for (int ks = 1; ks <= K / 64 && ks <= RMAX; ks++) {
+        if (K % ks || (K / ks) % 64 || K / ks > 256) continue;
+        best = ks;
+        if (nblk * ks >= g_cus) return ks;
+    }
+    return best;
+}
+
+// skinny GEMM: M <= 64, K % 64 == 0, 16-byte aligned a, b, b2 and sizes below
+// 2 GiB (checked by the caller); more than one slice needs the split-K workspace
+template <int MT, bool GATED>
+static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                           int M, int K, int N) {
+    const int ks = skinny_slices(K, N);
+    if (ks <= 0) return QH_EINVAL;
+    const int nblk = (N + 63) / 64;
+    const size_t MN = (size_t)M * N;
+    float *part = nullptr;
+    if (ks > 1) {
+        if (!part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) return QH_ETOOBIG;
+        part = g_part;
+    }
+    hipLaunchKernelGGL((k_gemm_skinny<MT, GATED>), dim3(nblk, ks), dim3(NTHREADS), 0, g_stream, c, part, a, b, b2,
+                       M, K, N, K / ks);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    if (ks > 1) {
+        size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
+        if (blocks > 2048) blocks = 2048;
+        hipLaunchKernelGGL((k_stream_reduce<GATED>), dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream,
+                           c, part, MN, ks);
+        HCHECK(hipGetLastError(), QH_ELAUNCH);
+    }
+    return QH_OK;
+}
+template <bool GATED>
+static int launch_skinny(float *c, const float *a, const uint16_t *b, const uint16_t *b2, int M, int K, int N) {
+    switch (stream_mt(M)) {
+        case 1: return launch_skinny_t<1, GATED>(c, a, b, b2, M, K, N);
+        case 2: return launch_skinny_t<2, GATED>(c, a, b, b2, M, K, N);
+        default: return launch_skinny_t<4, GATED>(c, a, b, b2, M, K, N);
+    }
 }
 
 template <bool GATED>
@@ -2576,6 +2793,7 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_X256x128: return launch_xl<256, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x128SK: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N, true);
+        case PLAN_SKINNY: return launch_skinny<GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x256s1: return launch_xl<256, 256, 64, GATED, false, 1>(c, a, b, b2, M, K, N);
         case PLAN_X64x256: return launch_xl<64, 256, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128: return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
@@ -2616,12 +2834,18 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
         plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
     if (is_xb_plan(plan) && !abf_ensure((size_t)M * K))            // no room for the bf16 copy of A
         plan = PLAN_X128x256;
+    if (plan == PLAN_SKINNY) {
+        const int ks = (M <= 64 && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
+                        (size_t)N * K * 2 < (1ull << 31)) ? skinny_slices(K, N) : 0;
+        const size_t part = (size_t)ks * (gated ? 2 : 1) * M * N * sizeof(float);
+        if (ks <= 0 || (ks > 1 && !part_ensure(part))) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
+    }
     if (is_stream_plan(plan)) {
         // KS must divide the slices and fit the A registers; more than one
         // slice needs workspace for the fp32 partial sums
         const bool fits = stream_fits(M, K, N);
         const int ks = plan != PLAN_STREAM ? 1 << (plan - PLAN_STREAM_KS1) : fits ? stream_ks(M, K, N, g_cus) : 0;
-        bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16;
+        bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16 && K / (256 * ks) <= RMAX;
         if (ok && K / (256 * ks) > 1) {
             const size_t part = (size_t)(K / (256 * ks)) * (gated ? 2 : 1) * M * N * sizeof(float);
             ok = abf_ensure((part + 1) / sizeof(uint16_t));
