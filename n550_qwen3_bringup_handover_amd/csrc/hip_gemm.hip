@@ -2848,7 +2848,7 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
         bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16 && K / (256 * ks) <= RMAX;
         if (ok && K / (256 * ks) > 1) {
             const size_t part = (size_t)(K / (256 * ks)) * (gated ? 2 : 1) * M * N * sizeof(float);
-            ok = abf_ensure((part + 1) / sizeof(uint16_t));
+            ok = part < (1ull << 31) && abf_ensure((part + 1) / sizeof(uint16_t));   // 32-bit offsets
         }
         if (!ok) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
         else plan = ks == 1 ? PLAN_STREAM_KS1 : ks == 2 ? PLAN_STREAM_KS2 : ks == 4 ? PLAN_STREAM_KS4 : PLAN_STREAM_KS8;
