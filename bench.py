@@ -514,6 +514,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="skip per-kernel and GEMM tables")
+    ap.add_argument("--no-gemm-tables", action="store_true",
+                    help="skip the GEMM tables (keeps the per-kernel decode timing); the profiled run "
+                         "of the decode set uses it, the GEMM shapes are profiled one by one")
     ap.add_argument("--no-graph", action="store_true",
                     help="launch the 113 kernels of a step one by one instead of replaying a graph")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -591,7 +594,7 @@ def main():
                     "traffic": read_traffic(dom),
                     "bytes_per_launch": d["bytes_per_launch"],
                     "us_per_launch": round(d["us_per_launch"], 3)}
-    gemms = None if args.no_extras else gemm_tables(g)
+    gemms = None if (args.no_extras or args.no_gemm_tables) else gemm_tables(g)
     if args.calibrate_copy:
         # a kernel of known traffic (64 MiB read + 64 MiB written per launch)
         # for scaling FETCH_SIZE / WRITE_SIZE counters in profiled runs
