@@ -2335,11 +2335,18 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
         if (M >= 1024) {
-            // K-heavy shapes with <= 128 tiles of 128x128 (o, down up to M =
-            // 2048): split K over the idle CUs (measured: 1024x3072x1024
-            // 36.0 -> 21.5 us, 1024x2048x1024 23.3 -> 18.0 us); at K = 1024
-            // the partials' round trip costs more than it saves
-            if (!gated && K >= 2048 && blocks(128, 128) <= 128) return PLAN_X128x128SK;
+            // Fewer than 256 tiles of 128x128 (measured on MI355X, every plan at
+            // M = 1024 and 2048 on the Qwen3-0.6B shapes): the 32x64 tiles while
+            // they fit two rounds (1024 x {1024,2048,3072} -> 1024: 9.1, 15.1,
+            // 21.3 us against 13.9, 19.6, 21.7 on 128x128 / split K), 64x128
+            // tiles at K = 1024 (1024x1024x2048 12.7 vs 15.4 us, 2048x1024x1024
+            // 12.7 vs 15.0), 64x64 tiles while they fit two rounds (2048x2048
+            // x1024 21.9 vs 27.2 us), else K split over the idle CUs
+            if (!gated && blocks(128, 128) < 256) {
+                if (blocks(32, 64) <= 512) return PLAN_P32x64k64s4;
+                if (K <= 1024 && blocks(64, 128) >= 256) return PLAN_X64x128;
+                if (blocks(64, 64) <= 512) return PLAN_P64x64k64s3;
+            }
             if (!gated && blocks(256, 256) >= 256)
                 return (size_t)M * K <= g_abf_elems ? PLAN_XB256x256s1 : PLAN_X256x256;
             if (gated && M >= 2048 && (size_t)M * K <= g_abf_elems) return PLAN_XB128x128;

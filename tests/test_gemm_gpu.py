@@ -364,9 +364,9 @@ def test_bf16a_gated_and_rejects_bad_k():
                                          (1536, 3072, 1024, False), (1024, 2048, 1024, False)])
 def test_large_m_automatic_plans(M, K, N, gated):
     """The plans chosen from M = 1024 on (256 x 256 tiles, bf16 rounding pass
-    + 128 x 128 tiles for gate|up, 128 x 128, and 128 x 128 with K split over
-    blocks for the K-heavy shapes) on a row subset; the split-K sum is added
-    in slice order, so a second run gives the same bits."""
+    + 128 x 128 tiles for gate|up, 128 x 128, 64 x 128, and the 32 x 64 /
+    64 x 64 tiles for the K-heavy shapes with few 128 x 128 tiles) on a row
+    subset; a second run gives the same bits."""
     a = oracle.f32_bf16_normal(M * K, 970 + M)
     if not gated:
         b = oracle.bf16_normal(N * K, 971, 0.02)
