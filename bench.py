@@ -241,6 +241,47 @@ def model_cfg4(n_prompt=128, n_decode=128):
             "ms_per_decode_token": round(dec / n_decode, 4), "first_tokens": [int(t) for t in toks[:8]]}
 
 
+def model_batch_decode(n_seq=64, ctx=2048, n_decode=32, warm=2):
+    """Batched greedy decode (qwen3_hip_batch_*): n_seq sequences, each
+    prefilled with its own random prompt of ctx - n_decode - warm tokens;
+    `warm` untimed steps (the first eager, then the captured graph), then
+    n_decode timed steps of all sequences at once, the last at position
+    ctx - 1.  Each step reads every weight once (M = n_seq GEMMs) and every
+    sequence's K/V cache up to its position (fp32, 229,376 B per position)."""
+    import numpy as np
+    from n550_qwen3_bringup_handover_amd import model as M
+    n_prompt = ctx - n_decode - warm
+    rng = np.random.default_rng(5)
+    blob = M.qw3m_random(MODEL_SEED, M.LAYOUT_ROW, threads=16)
+    with M.Model(blob, max_seq=ctx) as m:
+        del blob
+        with M.Batch(m, n_seq, ctx) as b:
+            t0 = time.time()
+            for s in range(n_seq):
+                b.prefill(s, rng.integers(0, V, n_prompt).astype(np.int32))
+                if s % 16 == 15:
+                    print(f"batched decode: {s + 1} of {n_seq} sequences prefilled, {time.time() - t0:.1f} s",
+                          file=sys.stderr, flush=True)
+            prefill_s = time.time() - t0
+            b.decode(warm)
+            out = b.decode(n_decode)
+            dec = b.timing()
+    kv_pos_bytes = LAYERS * 8 * 128 * 4 * 2
+    # positions read by the timed steps: step i of each sequence attends over n_prompt + warm + i + 1
+    kv_bytes = n_seq * kv_pos_bytes * sum(n_prompt + warm + i + 1 for i in range(n_decode))
+    w_bytes = n_decode * STEP_BYTES
+    return {"workload": f"Qwen3-0.6B batched greedy decode, random-init bf16 weights: {n_seq} sequences, "
+                        f"each prefilled with its own {n_prompt}-token random prompt, then {n_decode} timed "
+                        f"steps of all sequences at once (graph replay each) at positions "
+                        f"{n_prompt + warm}..{ctx - 1}; fp32 KV cache",
+            "n_seq": n_seq, "ctx": ctx, "prefill_s": round(prefill_s, 2),
+            "decode_ms": round(dec, 3), "ms_per_step": round(dec / n_decode, 4),
+            "decode_tok_s": round(n_seq * n_decode / dec * 1e3, 1),
+            "hbm_bytes_per_step": int((kv_bytes + w_bytes) / n_decode),
+            "hbm_GBps": round((kv_bytes + w_bytes) / (dec * 1e-3) / 1e9, 1),
+            "first_tokens_seq0": [int(t) for t in out[0, :8]]}
+
+
 # ---------------------------------------------------------------------------
 # GPU side
 # ---------------------------------------------------------------------------
@@ -604,10 +645,11 @@ def main():
             g.rt.check(g.L.qwen3_hip_copy_dev(ctypes.c_void_p(dst), ctypes.c_void_p(src), nb), "copy")
         g.sync()
 
-    model = None
+    model = batch = None
     if not args.no_model:
         model = model_cfg4()
         model["cpu_baseline"] = cpu_model
+        batch = model_batch_decode()
     hostp = None if args.no_extras else host_path()
 
     line = {
@@ -627,6 +669,7 @@ def main():
         "kernels": kclasses,
         "gemm": gemms,
         "model_cfg4": model,
+        "model_batch_decode": batch,
         "host_pointer_path": hostp,
     }
     print(json.dumps(line))

@@ -117,6 +117,56 @@ typedef void (*qwen3_hip_dump_fn)(void *ctx, int layer, const char *name, const 
                                   size_t n);
 int qwen3_hip_model_set_dump(qwen3_hip_model *model, qwen3_hip_dump_fn fn, void *ctx);
 
+/* ---- multi-sequence batched decode ----------------------------------------
+ *
+ * No counterpart in the reference, whose forward holds one sequence
+ * (SRC/qwen3.h:234-241).  n_seq independent sequences share the model's
+ * weights; each has its own KV cache of max_ctx positions (229,376 bytes per
+ * position: 28 layers x 8 kv heads x 128 dims x fp32 K and V).  A sequence
+ * is prefilled on its own through the forward of qwen3_hip_model_forward; a
+ * decode step then feeds one token of every sequence, each at its own
+ * position, so each projection is one GEMM with M = n_seq rows (the same
+ * qwen3_gemm kernels) instead of n_seq GEMVs, and attention runs over every
+ * sequence's cache in one launch.  Greedy selection as
+ * qwen3_hip_model_generate (first index of the maximum).
+ *
+ * The batch borrows the model's weights, rope tables and activation
+ * buffers: close it before the model.  Its calls, like the model's, are
+ * synchronous; a batch call discards the model's last logits. */
+typedef struct qwen3_hip_batch qwen3_hip_batch;
+
+/* n_seq in 1 .. 128 (QWEN3_MAX_BATCH rows per GEMM); max_ctx in 2 ..
+ * qwen3_hip_model_max_seq(model). */
+int qwen3_hip_batch_open(qwen3_hip_batch **batch, qwen3_hip_model *model, int n_seq, int max_ctx);
+
+void qwen3_hip_batch_close(qwen3_hip_batch *batch);
+
+/* Prefill sequence seq (0 .. n_seq-1) with n_prompt tokens (1 .. max_ctx-1)
+ * at positions 0 .. n_prompt-1, in chunks of 128, replacing whatever the
+ * sequence held; its next token is the argmax of the last prompt row's
+ * logits.  Sequences may have prompts of different lengths. */
+int qwen3_hip_batch_prefill(qwen3_hip_batch *batch, int seq, const int *prompt, int n_prompt);
+
+/* n_decode greedy steps of every sequence at once (every sequence must be
+ * prefilled).  out[s * (n_decode + 1) + 0] receives the token sequence s is
+ * fed first (after a prefill: the prefill's argmax), out[s * (n_decode + 1)
+ * + i] the token generated by step i.  A later call continues where the
+ * previous one ended.  Each sequence's positions must stay below max_ctx:
+ * n_prompt + tokens decoded since its prefill + n_decode <= max_ctx.  EOS
+ * does not stop a sequence (callers cut at it). */
+int qwen3_hip_batch_decode(qwen3_hip_batch *batch, int n_decode, int *out);
+
+/* Logits of the last decode step, n_seq x vocab floats (synchronous copy). */
+int qwen3_hip_batch_logits(qwen3_hip_batch *batch, float *out);
+
+/* Decode steps as one graph replay each (1, the default; the first step of
+ * the first call runs eagerly, then the step is captured) or as eager
+ * launches (0); both compute the same thing. */
+int qwen3_hip_batch_set_graph(qwen3_hip_batch *batch, int on);
+
+/* Wall-clock ms of the last qwen3_hip_batch_decode call. */
+int qwen3_hip_batch_timing(const qwen3_hip_batch *batch, double *decode_ms);
+
 #ifdef __cplusplus
 }
 #endif

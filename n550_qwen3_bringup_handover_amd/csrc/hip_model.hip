@@ -320,7 +320,7 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 // ---------------------------------------------------------------------------
 // Decode attention split over positions: partials, merged by the o GEMV
 // ---------------------------------------------------------------------------
-// grid = NKV * QM_ATT_SPLITS blocks: block (g, s) takes positions
+// grid = (NKV * QM_ATT_SPLITS, n_seq): block (g, s) takes positions
 // [s*chunk, min(ctx, (s+1)*chunk)) of kv head g, chunk = ceil(ctx / splits),
 // for both query heads of the group.  Every block normalises and ropes the
 // group's two q heads itself (and the new k); block s = 0 writes the new k/v
@@ -340,6 +340,9 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 // instruction 8 positions x 128 contiguous bytes), then a 3-step shuffle
 // sums the 8 lanes of a chunk.  Every K and V load of the first pass goes
 // out at entry, before the q prologue: one memory round trip per launch.
+// Batched decode: blockIdx.y is the sequence, with its own qkv row, position
+// pos_d[seq], cache (kv_seq floats after the previous sequence's) and
+// partials (QM_ATT_PART_FLOATS after the previous sequence's).
 __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv,
                                                    float *__restrict__ part,
                                                    float *__restrict__ kc, float *__restrict__ vc,
@@ -348,12 +351,18 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
                                                    const float *__restrict__ rcos,
                                                    const float *__restrict__ rsin,
                                                    const int *__restrict__ pos_d, int max_seq,
-                                                   float eps, float scale) {
+                                                   size_t kv_seq, float eps, float scale) {
     constexpr int S = QM_ATT_SPLITS;
     constexpr int P = 64;                        // positions per pass
     const int g = blockIdx.x % NKV, sp = blockIdx.x / NKV;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int pos = *pos_d;
+    // sequence blockIdx.y of a batch: its qkv row, position, cache and partials
+    const int seq = blockIdx.y;
+    qkv += (size_t)seq * QKV_LD;
+    kc += (size_t)seq * kv_seq;
+    vc += (size_t)seq * kv_seq;
+    part += (size_t)seq * QM_ATT_PART_FLOATS;
+    const int pos = pos_d[seq];
     if (pos < 0 || pos >= max_seq) return;      // uniform per launch
     const int ctx = pos + 1;
     const int chunk = (ctx + S - 1) / S;
@@ -492,6 +501,105 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     }
 }
 
+// ---------------------------------------------------------------------------
+// Batched decode: the split partials of k_attn_part merged into the attention
+// output att[seq][16 heads x 128], the same softmax merge as the o GEMV's
+// prologue: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s.
+// grid = (NKV, n_seq), 256 threads = 2 query heads x 128 dims.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(NTH) void k_attn_merge(float *__restrict__ att, const float *__restrict__ part) {
+    constexpr int S = QM_ATT_SPLITS;
+    const int g = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
+    const int h = tid >> 7, d = tid & (HD - 1);
+    const float *pp = part + (size_t)seq * QM_ATT_PART_FLOATS + (size_t)(g * S * GRP + h) * QM_ATT_PART;
+    float m[S], l[S], o[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const float *ps = pp + (size_t)s * GRP * QM_ATT_PART;
+        m[s] = ps[0];
+        l[s] = ps[1];
+        o[s] = ps[4 + d];
+    }
+    float mx = m[0];
+#pragma unroll
+    for (int s = 1; s < S; s++) mx = fmaxf(mx, m[s]);
+    float den = 0.0f, num = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const float w = m[s] == -INFINITY ? 0.0f : expf(m[s] - mx);
+        den = fmaf(w, l[s], den);
+        num = fmaf(w, o[s], num);
+    }
+    att[(size_t)seq * (NKV * GRP * HD) + (size_t)(g * GRP + h) * HD + d] = num * (1.0f / den);
+}
+
+// (value, index) argmax step: larger value wins, ties -> lower index, an
+// ordered value beats NaN (the strict ">" scan of ops_scalar.c:57-62, whose
+// only other case, a NaN at index 0, the caller resolves)
+__device__ __forceinline__ void am_take(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i) || (v != v && v2 == v2)) { v = v2; i = i2; }
+}
+
+// ---------------------------------------------------------------------------
+// Batched greedy step bookkeeping: block r scans logits row r (n floats),
+// tok[r] = first index of its maximum (ops_scalar.c:57-62), then
+// out[r * out_ld + pos[r] - plen[r] + 1] = tok[r] when that index lies in
+// [0, out_ld), and pos[r] += 1.  grid = n_rows blocks of AM_ROW_THREADS.
+// ---------------------------------------------------------------------------
+#define AM_ROW_THREADS 1024
+__global__ __launch_bounds__(AM_ROW_THREADS) void k_argmax_rows(const float *__restrict__ logits, int n,
+                                                               int *__restrict__ tok, int *__restrict__ pos,
+                                                               const int *__restrict__ plen,
+                                                               int *__restrict__ out, int out_ld) {
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float *v = logits + (size_t)r * n;
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(v, (size_t)n * 4);
+    const int n4 = n >> 2;
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+    // four 16-byte loads in flight per thread; groups past n4 read nothing
+    for (int i0 = tid; i0 < n4; i0 += 4 * AM_ROW_THREADS) {
+        f32x4 x[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * AM_ROW_THREADS;
+            x[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rs, i < n4 ? (uint32_t)i * 16u : BUF_OOB, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * AM_ROW_THREADS;
+            if (i < n4) {
+                am_take(bv, bi, x[u].x, 4 * i);
+                am_take(bv, bi, x[u].y, 4 * i + 1);
+                am_take(bv, bi, x[u].z, 4 * i + 2);
+                am_take(bv, bi, x[u].w, 4 * i + 3);
+            }
+        }
+    }
+    for (int i = 4 * n4 + tid; i < n; i += AM_ROW_THREADS) am_take(bv, bi, v[i], i);
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+        const float ov = __shfl_xor(bv, msk);
+        const int oi = __shfl_xor(bi, msk);
+        am_take(bv, bi, ov, oi);
+    }
+    __shared__ float sv[AM_ROW_THREADS / WAVE];
+    __shared__ int si[AM_ROW_THREADS / WAVE];
+    if ((tid & 63) == 0) { sv[tid >> 6] = bv; si[tid >> 6] = bi; }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < AM_ROW_THREADS / WAVE; w++) am_take(bv, bi, sv[w], si[w]);
+        // the reference's scan starts from v[0]: a NaN there is never beaten
+        const int t = (bi == 0x7FFFFFFF || v[0] != v[0]) ? 0 : bi;
+        tok[r] = t;
+        const int p = pos[r];
+        const int idx = p - plen[r] + 1;
+        if (idx >= 0 && idx < out_ld) out[(size_t)r * out_ld + idx] = t;
+        pos[r] = p + 1;
+    }
+}
+
 __global__ void k_set_i32(int *p, int v) {
     if (threadIdx.x == 0 && blockIdx.x == 0) p[0] = v;
 }
@@ -551,7 +659,33 @@ extern "C" int qm_attention_decode_part(const float *qkv, float *part, float *kc
     if (max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
     const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
     hipLaunchKernelGGL(k_attn_part, dim3(NKV * QM_ATT_SPLITS), dim3(NTH), 0, stream(), qkv, part, kc, vc,
-                       qn, kn, rcos, rsin, pos_d, max_seq, eps, scale);
+                       qn, kn, rcos, rsin, pos_d, max_seq, (size_t)0, eps, scale);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" int qm_attention_decode_batch(const float *qkv, float *att, float *part, float *kc, float *vc,
+                                         size_t kv_seq, const uint16_t *qn, const uint16_t *kn,
+                                         const float *rcos, const float *rsin, const int *pos_d, int n_seq,
+                                         int max_seq, float eps) {
+    if (!stream()) return QH_ESTATE;
+    if (!qkv || !att || !part || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
+    if (n_seq <= 0 || n_seq > QM_MAX_CHUNK || max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
+    if (kv_seq < (size_t)NKV * HD * max_seq) return QH_EINVAL;     // sequences' caches must not overlap
+    const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
+    hipLaunchKernelGGL(k_attn_part, dim3(NKV * QM_ATT_SPLITS, n_seq), dim3(NTH), 0, stream(), qkv, part, kc,
+                       vc, qn, kn, rcos, rsin, pos_d, max_seq, kv_seq, eps, scale);
+    if (hipGetLastError() != hipSuccess) return QH_ELAUNCH;
+    hipLaunchKernelGGL(k_attn_merge, dim3(NKV, n_seq), dim3(NTH), 0, stream(), att, part);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+extern "C" int qm_argmax_rows(const float *logits, int n, int n_rows, int *tok, int *pos, const int *plen,
+                              int *out, int out_ld) {
+    if (!stream()) return QH_ESTATE;
+    if (!logits || !tok || !pos || !plen || !out || n <= 0 || n_rows <= 0 || out_ld < 0) return QH_EINVAL;
+    if ((size_t)n * 4 >= ((size_t)1 << 31)) return QH_EINVAL;      // one buffer resource per row
+    hipLaunchKernelGGL(k_argmax_rows, dim3(n_rows), dim3(AM_ROW_THREADS), 0, stream(), logits, n, tok, pos,
+                       plen, out, out_ld);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

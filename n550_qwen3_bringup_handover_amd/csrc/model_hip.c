@@ -287,9 +287,23 @@ static size_t kv_layer_floats(const qwen3_hip_model *m) {
     return (size_t)QW3M_N_KV_HEADS * m->max_seq * QW3M_HEAD_DIM;
 }
 
+/* where a chunk's K/V go: layer l's cache of one sequence starts at
+ * kc + l * layer_stride (layout in hip_model.hip, max_seq positions) */
+typedef struct {
+    float *kc, *vc;
+    size_t layer_stride;
+    int max_seq;
+} kv_t;
+
+static kv_t model_kv(qwen3_hip_model *m) {
+    const kv_t kv = {m->kc, m->vc, kv_layer_floats(m), m->max_seq};
+    return kv;
+}
+
 /* nt tokens already in tok_in at positions pos0.. (pos0 set by the caller in
- * state[1]); logits of the last row when want_logits */
-static int run_chunk(qwen3_hip_model *m, int nt, int want_logits) {
+ * state[1]) of the sequence whose cache is kv; logits of the last row when
+ * want_logits */
+static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int want_logits) {
     int rc;
     const float eps = QW3M_RMS_EPS;
     /* with a dump callback the residual add of down_proj is done at the end
@@ -310,9 +324,9 @@ static int run_chunk(qwen3_hip_model *m, int nt, int want_logits) {
         DUMP(l, "q_proj_out", m->qkv, QKV_N, 0, QW3M_Q_DIM);
         DUMP(l, "k_proj_out", m->qkv, QKV_N, QW3M_Q_DIM, QW3M_KV_DIM);
         DUMP(l, "v_proj_out", m->qkv, QKV_N, QW3M_Q_DIM + QW3M_KV_DIM, QW3M_KV_DIM);
-        if (!rc) rc = qm_attention(m->qkv, m->att, m->kc + l * kv_layer_floats(m),
-                                   m->vc + l * kv_layer_floats(m), L->qn, L->kn, m->rcos, m->rsin,
-                                   m->state + 1, nt, m->max_seq, eps);
+        if (!rc) rc = qm_attention(m->qkv, m->att, kv->kc + l * kv->layer_stride,
+                                   kv->vc + l * kv->layer_stride, L->qn, L->kn, m->rcos, m->rsin,
+                                   m->state + 1, nt, kv->max_seq, eps);
         DUMP(l, "attn_out", m->att, QW3M_Q_DIM, 0, QW3M_Q_DIM);
         if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, nt, QW3M_Q_DIM, H);
         DUMP(l, "o_proj_out", m->ob, H, 0, H);
@@ -388,8 +402,9 @@ int qwen3_hip_model_forward(qwen3_hip_model *m, const int *tokens, int n_token, 
     if (n_token < 1 || n_token > QM_MAX_CHUNK || pos0 < 0 || pos0 + n_token > m->max_seq)
         return QWEN3_HIP_EINVAL;
     int rc = check_tokens(tokens, n_token);
+    const kv_t kv = model_kv(m);
     if (!rc) rc = load_chunk(m, tokens, n_token, pos0);
-    if (!rc) rc = run_chunk(m, n_token, 1);
+    if (!rc) rc = run_chunk(m, &kv, n_token, 1);
     m->have_logits = rc == 0;
     return rc;
 }
@@ -417,12 +432,13 @@ int qwen3_hip_model_generate(qwen3_hip_model *m, const int *prompt, int n_prompt
     int rc = check_tokens(prompt, n_prompt);
     if (rc) return rc;
 
+    const kv_t kv = model_kv(m);
     const double t0 = now_ms();
     int nt = 0;
     for (int p0 = 0; p0 < n_prompt && !rc; p0 += QM_MAX_CHUNK) {
         nt = n_prompt - p0 < QM_MAX_CHUNK ? n_prompt - p0 : QM_MAX_CHUNK;
         rc = load_chunk(m, prompt + p0, nt, p0);
-        if (!rc) rc = run_chunk(m, nt, p0 + nt == n_prompt);
+        if (!rc) rc = run_chunk(m, &kv, nt, p0 + nt == n_prompt);
     }
     /* first token; state[1] = pos0 of the last chunk + nt = n_prompt */
     if (!rc) rc = qm_set_i32(m->state + 2, 0);
@@ -468,5 +484,200 @@ int qwen3_hip_model_timing(const qwen3_hip_model *m, double *prefill_ms, double 
     if (!m) return QWEN3_HIP_EINVAL;
     if (prefill_ms) *prefill_ms = m->t_prefill_ms;
     if (decode_ms) *decode_ms = m->t_decode_ms;
+    return QWEN3_HIP_OK;
+}
+
+/* ---- multi-sequence batched decode ------------------------------------------ */
+
+struct qwen3_hip_batch {
+    qwen3_hip_model *m;
+    int n_seq, max_ctx, out_ld;
+    size_t kv_seq;                     /* floats of one sequence's cache in one layer */
+    float *kc, *vc;                    /* [NL][n_seq][kv_seq] */
+    float *logits;                     /* [n_seq][V] of the last decode step */
+    float *part;                       /* [n_seq][QM_ATT_PART_FLOATS] */
+    int *tok, *pos, *plen;             /* [n_seq]: next token fed, its position, prompt length */
+    int *out;                          /* [n_seq][out_ld]: token i of a sequence at i = pos - plen + 1 */
+    int *h_next;                       /* host: position of each sequence's next fed token (-1: empty) */
+    int *h_plen;                       /* host: prompt length of each sequence */
+    int *h_out;                        /* host staging of out */
+    int use_graph;
+    int graph_id;
+    int have_logits;
+    double t_decode_ms;
+};
+
+void qwen3_hip_batch_close(qwen3_hip_batch *b) {
+    if (!b) return;
+    (void)qh_sync();
+    if (b->graph_id >= 0) (void)qh_graph_destroy(b->graph_id);
+    void *bufs[] = {b->kc, b->vc, b->logits, b->part, b->tok, b->pos, b->plen, b->out};
+    for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) (void)qh_free(bufs[i]);
+    free(b->h_next);
+    free(b->h_plen);
+    free(b->h_out);
+    free(b);
+}
+
+int qwen3_hip_batch_open(qwen3_hip_batch **out, qwen3_hip_model *m, int n_seq, int max_ctx) {
+    if (!out) return QWEN3_HIP_EINVAL;
+    *out = NULL;
+    if (!m || n_seq < 1 || n_seq > QM_MAX_CHUNK || max_ctx < 2 || max_ctx > m->max_seq) return QWEN3_HIP_EINVAL;
+    qwen3_hip_batch *b = (qwen3_hip_batch *)calloc(1, sizeof *b);
+    if (!b) return QWEN3_HIP_ENOMEM;
+    b->m = m;
+    b->n_seq = n_seq;
+    b->max_ctx = max_ctx;
+    b->out_ld = max_ctx + 1;
+    b->kv_seq = (size_t)QW3M_N_KV_HEADS * max_ctx * QW3M_HEAD_DIM;
+    b->use_graph = 1;
+    b->graph_id = -1;
+    int rc = QWEN3_HIP_ENOMEM;
+    b->h_next = (int *)malloc((size_t)n_seq * sizeof(int));
+    b->h_plen = (int *)calloc((size_t)n_seq, sizeof(int));
+    b->h_out = (int *)malloc((size_t)n_seq * b->out_ld * sizeof(int));
+    if (!b->h_next || !b->h_plen || !b->h_out) goto fail;
+    for (int s = 0; s < n_seq; s++) b->h_next[s] = -1;
+#define DEV(ptr, bytes)                                                   \
+    do {                                                                  \
+        if ((rc = qh_malloc((void **)&(ptr), (bytes))) != 0) goto fail;   \
+    } while (0)
+    const size_t kv_bytes = (size_t)NL * n_seq * b->kv_seq * sizeof(float);
+    DEV(b->kc, kv_bytes);
+    DEV(b->vc, kv_bytes);
+    DEV(b->logits, (size_t)n_seq * V * sizeof(float));
+    DEV(b->part, (size_t)n_seq * QM_ATT_PART_FLOATS * sizeof(float));
+    DEV(b->tok, (size_t)n_seq * sizeof(int));
+    DEV(b->pos, (size_t)n_seq * sizeof(int));
+    DEV(b->plen, (size_t)n_seq * sizeof(int));
+    DEV(b->out, (size_t)n_seq * b->out_ld * sizeof(int));
+#undef DEV
+    rc = qm_zero_i32(b->tok, n_seq);
+    if (!rc) rc = qm_zero_i32(b->pos, n_seq);
+    if (!rc) rc = qm_zero_i32(b->plen, n_seq);
+    if (!rc) rc = qh_sync();
+    if (rc) goto fail;
+    *out = b;
+    return QWEN3_HIP_OK;
+fail:
+    qwen3_hip_batch_close(b);
+    return rc;
+}
+
+int qwen3_hip_batch_set_graph(qwen3_hip_batch *b, int on) {
+    if (!b) return QWEN3_HIP_EINVAL;
+    b->use_graph = on ? 1 : 0;
+    return QWEN3_HIP_OK;
+}
+
+int qwen3_hip_batch_prefill(qwen3_hip_batch *b, int seq, const int *prompt, int n_prompt) {
+    if (!b || !prompt || seq < 0 || seq >= b->n_seq || n_prompt < 1 || n_prompt >= b->max_ctx)
+        return QWEN3_HIP_EINVAL;
+    int rc = check_tokens(prompt, n_prompt);
+    if (rc) return rc;
+    qwen3_hip_model *m = b->m;
+    const kv_t kv = {b->kc + (size_t)seq * b->kv_seq, b->vc + (size_t)seq * b->kv_seq,
+                     (size_t)b->n_seq * b->kv_seq, b->max_ctx};
+    b->h_next[seq] = -1;
+    m->have_logits = 0;             /* the model's logits buffer is reused below */
+    for (int p0 = 0; p0 < n_prompt && !rc; p0 += QM_MAX_CHUNK) {
+        const int nt = n_prompt - p0 < QM_MAX_CHUNK ? n_prompt - p0 : QM_MAX_CHUNK;
+        rc = load_chunk(m, prompt + p0, nt, p0);
+        if (!rc) rc = run_chunk(m, &kv, nt, p0 + nt == n_prompt);
+    }
+    /* first token: out[seq][0] at pos - plen + 1 = 0, then pos = n_prompt */
+    if (!rc) rc = qm_set_i32(b->pos + seq, n_prompt - 1);
+    if (!rc) rc = qm_set_i32(b->plen + seq, n_prompt);
+    if (!rc) rc = qm_argmax_rows(m->logits, V, 1, b->tok + seq, b->pos + seq, b->plen + seq,
+                                 b->out + (size_t)seq * b->out_ld, b->out_ld);
+    if (!rc) rc = qh_sync();
+    if (!rc) {
+        b->h_next[seq] = n_prompt;
+        b->h_plen[seq] = n_prompt;
+    }
+    return rc;
+}
+
+/* one decode step of every sequence: token tok[s] at position pos[s] */
+static int batch_step(qwen3_hip_batch *b) {
+    qwen3_hip_model *m = b->m;
+    const int n = b->n_seq;
+    const float eps = QW3M_RMS_EPS;
+    const size_t lstride = (size_t)n * b->kv_seq;
+    int rc = QWEN3_HIP_OK;
+    for (int l = 0; l < NL && !rc; l++) {
+        const layer_t *L = &m->L[l];
+        if (l == 0) rc = qm_rows_norm(m->x, NULL, m->embed, b->tok, V, L->in_norm, m->xb, n, H, eps);
+        else rc = qm_rows_norm(m->x, m->dn, NULL, NULL, 0, L->in_norm, m->xb, n, H, eps);
+        if (!rc) rc = qh_gemm(m->qkv, m->xb, L->wqkv, n, H, QKV_N);
+        if (!rc) rc = qm_attention_decode_batch(m->qkv, m->att, b->part, b->kc + l * lstride, b->vc + l * lstride,
+                                                b->kv_seq, L->qn, L->kn, m->rcos, m->rsin, b->pos, n,
+                                                b->max_ctx, eps);
+        if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, n, QW3M_Q_DIM, H);
+        if (!rc) rc = qm_rows_norm(m->x, m->ob, NULL, NULL, 0, L->post_norm, m->xb, n, H, eps);
+        if (!rc) rc = qh_gemm_gate_up_silu(m->hb, m->xb, L->wg, L->wu, n, H, QW3M_INTER);
+        if (!rc) rc = qh_gemm(m->dn, m->hb, L->wd, n, QW3M_INTER, H);
+    }
+    if (!rc) rc = qm_rows_norm(m->x, m->dn, NULL, NULL, 0, m->final_norm, m->xb, n, H, eps);
+    if (!rc) rc = qh_gemm(b->logits, m->xb, m->embed, n, H, V);
+    if (!rc) rc = qm_argmax_rows(b->logits, V, n, b->tok, b->pos, b->plen, b->out, b->out_ld);
+    return rc;
+}
+
+int qwen3_hip_batch_decode(qwen3_hip_batch *b, int n_decode, int *out) {
+    if (!b || !out || n_decode < 0) return QWEN3_HIP_EINVAL;
+    for (int s = 0; s < b->n_seq; s++)
+        if (b->h_next[s] < 0 || (long)b->h_next[s] + n_decode > b->max_ctx) return QWEN3_HIP_EINVAL;
+    int rc = QWEN3_HIP_OK;
+    const double t0 = now_ms();
+    for (int i = 0; i < n_decode && !rc; i++) {
+        /* with graphs on, a first step runs eagerly (any workspace its GEMM
+           plans need is allocated then, outside capture); later steps replay
+           the one captured step */
+        if (!b->use_graph || (b->graph_id < 0 && i == 0)) {
+            rc = batch_step(b);
+            continue;
+        }
+        if (b->graph_id < 0) {
+            rc = qh_capture_begin();
+            if (rc) break;
+            const int rc2 = batch_step(b);
+            int gid = -1;
+            rc = qh_capture_end(&gid);
+            if (!rc) rc = rc2;
+            if (rc) {
+                if (gid >= 0) (void)qh_graph_destroy(gid);
+                break;
+            }
+            b->graph_id = gid;
+        }
+        rc = qh_graph_launch(b->graph_id);
+    }
+    if (!rc) rc = qh_sync();
+    b->t_decode_ms = now_ms() - t0;
+    if (rc) return rc;
+    if (n_decode > 0) b->have_logits = 1;
+    rc = qh_d2h(b->h_out, b->out, (size_t)b->n_seq * b->out_ld * sizeof(int));
+    if (!rc) rc = qh_sync();
+    if (rc) return rc;
+    for (int s = 0; s < b->n_seq; s++) {
+        /* the token fed at position h_next sits at out index h_next - plen */
+        const int *row = b->h_out + (size_t)s * b->out_ld + (b->h_next[s] - b->h_plen[s]);
+        memcpy(out + (size_t)s * (n_decode + 1), row, ((size_t)n_decode + 1) * sizeof(int));
+        b->h_next[s] += n_decode;
+    }
+    return QWEN3_HIP_OK;
+}
+
+int qwen3_hip_batch_logits(qwen3_hip_batch *b, float *out) {
+    if (!b || !out || !b->have_logits) return QWEN3_HIP_EINVAL;
+    int rc = qh_d2h(out, b->logits, (size_t)b->n_seq * V * sizeof(float));
+    if (!rc) rc = qh_sync();
+    return rc;
+}
+
+int qwen3_hip_batch_timing(const qwen3_hip_batch *b, double *decode_ms) {
+    if (!b) return QWEN3_HIP_EINVAL;
+    if (decode_ms) *decode_ms = b->t_decode_ms;
     return QWEN3_HIP_OK;
 }

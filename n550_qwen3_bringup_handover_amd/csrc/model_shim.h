@@ -39,6 +39,22 @@ int qm_attention_decode_part(const float *qkv_d, float *part_d, float *kc_d, flo
                              const uint16_t *qn_d, const uint16_t *kn_d, const float *rcos_d,
                              const float *rsin_d, const int *pos_d, int max_seq, float eps);
 
+/* batched decode attention for n_seq sequences, one token each: row s of
+ * qkv is sequence s's token at position pos[s]; its cache starts kv_seq
+ * floats after sequence s-1's (same layout as above); part holds
+ * QM_ATT_PART_FLOATS per sequence.  The split partials are merged into
+ * att[n_seq][2048] (two launches) */
+int qm_attention_decode_batch(const float *qkv_d, float *att_d, float *part_d, float *kc_d, float *vc_d,
+                              size_t kv_seq, const uint16_t *qn_d, const uint16_t *kn_d,
+                              const float *rcos_d, const float *rsin_d, const int *pos_d, int n_seq,
+                              int max_seq, float eps);
+
+/* greedy step of n_rows sequences: tok[r] = argmax of logits row r (n
+ * floats, first index on ties); out[r*out_ld + pos[r] - plen[r] + 1] =
+ * tok[r] when that index is in [0, out_ld); pos[r] += 1 */
+int qm_argmax_rows(const float *logits_d, int n, int n_rows, int *tok_d, int *pos_d, const int *plen_d,
+                   int *out_d, int out_ld);
+
 /* *p = v, as a kernel (safe inside stream capture) */
 int qm_set_i32(int *p_d, int v);
 /* p[0..n) = 0, as a kernel */

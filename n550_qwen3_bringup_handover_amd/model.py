@@ -150,6 +150,57 @@ class Model:
         return a.value, b.value
 
 
+class Batch:
+    """n_seq sequences decoded together on one Model (qwen3_hip_batch_*):
+    prefill each sequence, then decode steps feed one token of every
+    sequence at once (M = n_seq projections)."""
+
+    def __init__(self, model, n_seq, max_ctx):
+        L = runtime.lib()
+        h = VP()
+        _rc(L.qwen3_hip_batch_open(ctypes.byref(h), model._h, n_seq, max_ctx), "qwen3_hip_batch_open")
+        self._h = h
+        self.n_seq = n_seq
+        self.max_ctx = max_ctx
+
+    def close(self):
+        if self._h:
+            runtime.lib().qwen3_hip_batch_close(self._h)
+            self._h = VP()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def prefill(self, seq, prompt):
+        p = _i32(prompt)
+        _rc(runtime.lib().qwen3_hip_batch_prefill(self._h, seq, p.ctypes.data_as(I32P), p.size),
+            "qwen3_hip_batch_prefill")
+
+    def decode(self, n_decode):
+        """[n_seq, n_decode + 1] int32: the token each sequence is fed first,
+        then the n_decode generated ones."""
+        out = np.zeros((self.n_seq, n_decode + 1), dtype=np.int32)
+        _rc(runtime.lib().qwen3_hip_batch_decode(self._h, n_decode, out.ctypes.data_as(I32P)),
+            "qwen3_hip_batch_decode")
+        return out
+
+    def logits(self):
+        out = np.empty((self.n_seq, VOCAB), dtype=np.float32)
+        _rc(runtime.lib().qwen3_hip_batch_logits(self._h, out.ctypes.data_as(F32P)), "qwen3_hip_batch_logits")
+        return out
+
+    def set_graph(self, on):
+        _rc(runtime.lib().qwen3_hip_batch_set_graph(self._h, 1 if on else 0), "qwen3_hip_batch_set_graph")
+
+    def timing(self):
+        a = ctypes.c_double()
+        _rc(runtime.lib().qwen3_hip_batch_timing(self._h, ctypes.byref(a)), "qwen3_hip_batch_timing")
+        return a.value
+
+
 def main(argv=None):
     """Greedy generation on a seeded random-init blob:
     python -m n550_qwen3_bringup_handover_amd.model [--seed S] [--prompt N] [--decode N]

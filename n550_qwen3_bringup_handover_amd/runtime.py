@@ -89,6 +89,13 @@ _PROTOS = {
     "qwen3_hip_model_timing": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "qwen3_hip_model_set_graph": (ctypes.c_int, [VP, ctypes.c_int]),
     "qwen3_hip_model_set_dump": (ctypes.c_int, [VP, VP, VP]),
+    "qwen3_hip_batch_open": (ctypes.c_int, [ctypes.POINTER(VP), VP, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_batch_close": (None, [VP]),
+    "qwen3_hip_batch_prefill": (ctypes.c_int, [VP, ctypes.c_int, I32P, ctypes.c_int]),
+    "qwen3_hip_batch_decode": (ctypes.c_int, [VP, ctypes.c_int, I32P]),
+    "qwen3_hip_batch_logits": (ctypes.c_int, [VP, F32P]),
+    "qwen3_hip_batch_set_graph": (ctypes.c_int, [VP, ctypes.c_int]),
+    "qwen3_hip_batch_timing": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_double)]),
 }
 
 # qwen3_hip_dump_fn

@@ -10,6 +10,8 @@ oracle/ref_driver.c, runs on a random-init QW3M blob:
   model_<name>.npz: seed, layout, blob checksum, prompt, tokens (out[0] from
   the prefill, then one per decode step), top-2 logit margins per step, and
   for the short case the prefill's last logits row.
+  model_batch.npz: three more prompts (lengths 1, 19, 40) with their greedy
+  tokens and margins, the per-sequence answers for batched decoding.
   model_short_dump.npz: intermediate tensors of the short prompt's prefill
   (the reference's qwen3_set_dump names): every layer-0 tensor the GPU
   forward also materialises, and "layer_out" at several depths.
@@ -18,7 +20,7 @@ The blob itself (1.19 GB) is not stored: tests rebuild it from the seed with
 the library's QW3M writer and compare the checksum first.  The prompt comes
 from the oracle's SplitMix64 stream.  Usage:
 
-    python tests/golden/make_model_fixtures.py [short|cfg4|all]
+    python tests/golden/make_model_fixtures.py [short|cfg4|batch|dump|all]
 """
 import ctypes
 import os
@@ -51,8 +53,8 @@ def blob_checksum(blob):
     return int(np.add.reduce(w, dtype=np.uint64))
 
 
-def prompt_tokens(n):
-    st = ctypes.c_uint64(PROMPT_SEED)
+def prompt_tokens(n, seed=PROMPT_SEED):
+    st = ctypes.c_uint64(seed)
     L = oracle.lib()
     return np.array([L.orc_splitmix64(ctypes.byref(st)) % VOCAB for _ in range(n)], dtype=np.int32)
 
@@ -88,6 +90,48 @@ def run(name):
     path = os.path.join(HERE, f"model_{name}.npz")
     np.savez_compressed(path, **arrays)
     print(f"{path}: {n} tokens in {time.time() - t0:.0f} s; min margin {margins.min():.4g}")
+
+
+# batched decode: more prompts of other lengths (prompt i from the stream
+# PROMPT_SEED + 1 + i), each decoded greedily on its own by the reference
+BATCH_PROMPTS = (1, 19, 40)
+BATCH_DECODE = 8
+
+
+def run_batch():
+    L = oracle.ref("ref_model_hwsim")
+    if L is None:
+        sys.exit("oracle/_ref/libref_model_hwsim.so missing: run `make -C oracle ref`")
+    L.refdrv_generate.restype = ctypes.c_int
+    L.refdrv_generate.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
+                                  ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                  ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float),
+                                  ctypes.POINTER(ctypes.c_float)]
+    blob = M.qw3m_random(SEED, M.LAYOUT_ROW, threads=8)
+    t0 = time.time()
+    prompts, tokens, margins = [], [], []
+    for i, n_prompt in enumerate(BATCH_PROMPTS):
+        prompt = prompt_tokens(n_prompt, PROMPT_SEED + 1 + i)
+        out = np.zeros(BATCH_DECODE + 1, np.int32)
+        mg = np.zeros(BATCH_DECODE + 1, np.float32)
+        logits = np.zeros(VOCAB, np.float32)
+        n = L.refdrv_generate(blob.ctypes.data_as(ctypes.c_void_p), blob.nbytes,
+                              prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), n_prompt, BATCH_DECODE, 0,
+                              out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                              mg.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                              logits.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+        if n != BATCH_DECODE + 1:
+            sys.exit(f"refdrv_generate returned {n}")
+        prompts.append(prompt)
+        tokens.append(out)
+        margins.append(mg)
+        print(f"batch prompt {i} ({n_prompt} tokens): {out.tolist()}", flush=True)
+    path = os.path.join(HERE, "model_batch.npz")
+    np.savez_compressed(path, seed=np.uint64(SEED), checksum=np.uint64(blob_checksum(blob)),
+                        prompt_lens=np.array(BATCH_PROMPTS, np.int32), prompts=np.concatenate(prompts),
+                        tokens=np.stack(tokens), margins=np.stack(margins), kernel=np.array("hwsim"),
+                        seconds=np.float64(time.time() - t0))
+    print(f"{path}: {len(BATCH_PROMPTS)} prompts in {time.time() - t0:.0f} s")
 
 
 # tensors compared op by op (layer 0) and along depth (layer_out)
@@ -135,5 +179,7 @@ if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "all"
     if which in ("dump", "all"):
         dumps()
-    for name in (CASES if which == "all" else ([] if which == "dump" else [which])):
+    if which in ("batch", "all"):
+        run_batch()
+    for name in (CASES if which == "all" else ([] if which in ("dump", "batch") else [which])):
         run(name)

@@ -240,3 +240,164 @@ def test_reference_forward_with_gpu_plugin(blob, case):
         err = np.abs(logits.astype(np.float64) - fx["prefill_logits"]).max()
         print(f"reference forward + plug-in: prefill logits max abs err {err:.3e}", flush=True)
         assert err <= LOGIT_TOL
+
+
+# ---- multi-sequence batched decode (qwen3_hip_batch_*) ----------------------
+
+def _batch_cases():
+    """(prompt, tokens, margins) per sequence: the three batch prompts and
+    the short and cfg4 prompts, interleaved so prompt lengths are ragged."""
+    fb = fixture("batch")
+    lens = fb["prompt_lens"]
+    starts = np.concatenate([[0], np.cumsum(lens)])
+    extra = [(fb["prompts"][starts[i]:starts[i + 1]], fb["tokens"][i], fb["margins"][i]) for i in range(len(lens))]
+    fs, fc = fixture("short"), fixture("cfg4")
+    return [extra[0], (fs["prompt"], fs["tokens"], fs["margins"]), extra[1],
+            (fc["prompt"], fc["tokens"], fc["margins"]), extra[2]]
+
+
+def _check_row(got, want, margins, what):
+    n = min(len(got), len(want))
+    diff = np.nonzero(got[:n] != want[:n])[0]
+    if len(diff) == 0:
+        return n
+    j = int(diff[0])
+    assert margins[j] < TIE_TOL, (f"{what}: token {j} is {got[j]}, reference {want[j]} "
+                                  f"(reference margin {margins[j]:.3g} >= {TIE_TOL})")
+    print(f"{what}: near-tie divergence at step {j} (margin {margins[j]:.3g})", flush=True)
+    return j
+
+
+def test_batch_decode_matches_reference(model):
+    """Five sequences with prompts of 1, 5, 19, 128 and 40 tokens decoded
+    together: every sequence's greedy tokens equal the reference forward's
+    for that prompt alone."""
+    cases = _batch_cases()
+    n_dec = 8
+    with M.Batch(model, len(cases), 160) as b:
+        for s, (p, _, _) in enumerate(cases):
+            b.prefill(s, p)
+        out = b.decode(n_dec)
+        ms = b.timing()
+    print(f"batch of {len(cases)}: {n_dec} steps {ms:.2f} ms", flush=True)
+    for s, (p, want, mg) in enumerate(cases):
+        _check_row(out[s], want[:n_dec + 1], mg, f"batch seq {s} (prompt {len(p)})")
+
+
+def _forward_all(model, seq):
+    """Single-sequence forward of seq from position 0, in calls of <= 128."""
+    for p0 in range(0, len(seq), 128):
+        model.forward(seq[p0:p0 + 128], p0)
+
+
+def test_batch_logits_match_single_sequence_forward(model):
+    """Batch logits after k steps equal the single-sequence forward of the
+    prompt plus the k fed tokens (its last row), within LOGIT_TOL."""
+    cases = _batch_cases()
+    n_dec = 6
+    with M.Batch(model, len(cases), 160) as b:
+        for s, (p, _, _) in enumerate(cases):
+            b.prefill(s, p)
+        out = b.decode(n_dec)
+        lb = b.logits()
+    worst = 0.0
+    for s, (p, _, _) in enumerate(cases):
+        _forward_all(model, np.concatenate([p, out[s, :n_dec]]))
+        ls = model.logits()
+        err = float(np.abs(ls.astype(np.float64) - lb[s]).max())
+        worst = max(worst, err)
+        assert err <= LOGIT_TOL, f"seq {s}: max abs logit diff {err:.3e}"
+    print(f"batch vs single-sequence forward: worst max abs logit diff {worst:.3e}", flush=True)
+
+
+def test_batch_split_calls_graph_and_eager_agree(model):
+    """Two decode calls of 4 steps continue exactly like one call of 8, and
+    graph replay equals eager launches bit for bit (same kernels, same order)."""
+    cases = _batch_cases()
+    res = {}
+    for mode in ("graph", "eager"):
+        with M.Batch(model, len(cases), 160) as b:
+            b.set_graph(mode == "graph")
+            for s, (p, _, _) in enumerate(cases):
+                b.prefill(s, p)
+            a = b.decode(4)
+            c = b.decode(4)
+            res[mode] = (np.concatenate([a, c[:, 1:]], axis=1), b.logits())
+            assert np.array_equal(a[:, -1], c[:, 0])
+    with M.Batch(model, len(cases), 160) as b:
+        for s, (p, _, _) in enumerate(cases):
+            b.prefill(s, p)
+        one = b.decode(8)
+        l_one = b.logits()
+    assert np.array_equal(res["graph"][0], one)
+    assert np.array_equal(res["graph"][1], l_one)
+    assert np.array_equal(res["eager"][0], one)
+    assert np.array_equal(res["eager"][1], l_one)
+
+
+def test_batch_reprefill_one_sequence(model):
+    """Re-prefilling one sequence restarts it while the others continue."""
+    cases = _batch_cases()
+    fc = fixture("cfg4")
+    with M.Batch(model, len(cases), 160) as b:
+        for s, (p, _, _) in enumerate(cases):
+            b.prefill(s, p)
+        first = b.decode(3)
+        b.prefill(1, cases[0][0])                 # sequence 1 now holds prompt 0
+        second = b.decode(5)
+    # cfg4 (sequence 3) continues: its 9 tokens over both calls
+    cont = np.concatenate([first[3], second[3, 1:]])
+    _check_row(cont, fc["tokens"][:9], fc["margins"], "cfg4 continued")
+    _check_row(second[1], cases[0][1][:6], cases[0][2], "re-prefilled seq 1")
+    _check_row(np.concatenate([first[0], second[0, 1:]]), cases[0][1][:9], cases[0][2], "seq 0 continued")
+
+
+def test_batch_64_duplicate_sequences_identical(model):
+    """64 sequences of ragged random prompts (1 .. 300 tokens), each prompt
+    used twice (sequences i and i + 32): the two copies of a prompt produce
+    bit-identical tokens and logits (each output row of every kernel depends
+    on its own row only), and a sample matches the single-sequence forward."""
+    rng = np.random.default_rng(64)
+    lens = rng.integers(1, 301, 32)
+    prompts = [rng.integers(0, M.VOCAB, n).astype(np.int32) for n in lens]
+    n_dec = 4
+    with M.Batch(model, 64, 320) as b:
+        for s in range(64):
+            b.prefill(s, prompts[s % 32])
+        out = b.decode(n_dec)
+        lb = b.logits()
+        ms = b.timing()
+    print(f"batch of 64 (prompts 1..300): {n_dec} steps {ms:.2f} ms", flush=True)
+    assert np.array_equal(out[:32], out[32:])
+    assert np.array_equal(lb[:32], lb[32:])
+    for s in (int(np.argmax(lens)), int(np.argmin(lens)), 7):
+        _forward_all(model, np.concatenate([prompts[s], out[s, :n_dec]]))
+        err = float(np.abs(model.logits().astype(np.float64) - lb[s]).max())
+        assert err <= LOGIT_TOL, f"seq {s} (prompt {lens[s]}): max abs logit diff {err:.3e}"
+
+
+def test_batch_errors(model):
+    with pytest.raises(runtime.Qwen3HipError):
+        M.Batch(model, 0, 64)
+    with pytest.raises(runtime.Qwen3HipError):
+        M.Batch(model, 129, 64)
+    with pytest.raises(runtime.Qwen3HipError):
+        M.Batch(model, 2, model.max_seq + 1)
+    with M.Batch(model, 2, 16) as b:
+        with pytest.raises(runtime.Qwen3HipError):
+            b.decode(1)                            # nothing prefilled
+        b.prefill(0, [1, 2, 3])
+        with pytest.raises(runtime.Qwen3HipError):
+            b.decode(1)                            # sequence 1 not prefilled
+        with pytest.raises(runtime.Qwen3HipError):
+            b.prefill(2, [1])                      # no sequence 2
+        with pytest.raises(runtime.Qwen3HipError):
+            b.prefill(1, np.arange(16))            # prompt fills the whole context
+        with pytest.raises(runtime.Qwen3HipError):
+            b.prefill(1, [M.VOCAB])                # token out of range
+        with pytest.raises(runtime.Qwen3HipError):
+            b.logits()                             # no decode step yet
+        b.prefill(1, np.arange(10))
+        b.decode(6)                                # sequence 1 reaches position 15
+        with pytest.raises(runtime.Qwen3HipError):
+            b.decode(1)                            # past max_ctx for sequence 1
