@@ -396,8 +396,7 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     //    and at the new position, which comes from sk / vnew instead
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kc + (size_t)g * HD * max_seq, (size_t)HD * max_seq * 4);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc + (size_t)g * max_seq * HD, (size_t)max_seq * HD * 4);
-    f32x4 kk[8], vv[8];
-    auto load_pass = [&](int base) {
+    auto load_pass = [&](int base, f32x4 (&kk)[8], f32x4 (&vv)[8]) {
         const int tk = t0 + base + lane;
         const bool kin = base + lane < n && tk < pos;
 #pragma unroll
@@ -412,7 +411,8 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
                         rv, (i < n && tv < pos) ? (uint32_t)((tv * (HD / 4) + vch) * 16) : BUF_OOB, 0, 0));
         }
     };
-    load_pass(0);
+    f32x4 kk[8], vv[8];
+    load_pass(0, kk, vv);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3. QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
@@ -430,28 +430,40 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
         if (vp == 0) reinterpret_cast<f32x4 *>(vc + ((size_t)g * max_seq + pos) * HD)[vch] = vnew;
     }
 
+    // partial score of the new position over this wave's 32 dims (its cache
+    // loads read zeros): the same chain as below, computed once
+    float an0 = 0.0f, an1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[8 * wave + j];
+        const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[8 * wave + j];
+        const f32x4 kj = reinterpret_cast<const f32x4 *>(sk)[8 * wave + j];
+        an0 = fmaf(q0.x, kj.x, an0); an0 = fmaf(q0.y, kj.y, an0);
+        an0 = fmaf(q0.z, kj.z, an0); an0 = fmaf(q0.w, kj.w, an0);
+        an1 = fmaf(q1.x, kj.x, an1); an1 = fmaf(q1.y, kj.y, an1);
+        an1 = fmaf(q1.z, kj.z, an1); an1 = fmaf(q1.w, kj.w, an1);
+    }
+
     float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;
     f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     for (int base = 0; base < n; base += P) {
-        if (base > 0) load_pass(base);
-        // partial scores over this wave's 32 dims
+        if (base > 0) load_pass(base, kk, vv);
+        // partial scores over this wave's 32 dims; positions past n read
+        // zeros and are masked below, the new position takes an0 / an1
         {
-            // the new position's k comes from sk (a per-element select keeps
-            // kk in registers; positions past n read zeros and are masked below)
-            const bool isnew = t0 + base + lane == pos;
             float a0 = 0.0f, a1 = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
                 const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[8 * wave + j];
                 const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[8 * wave + j];
-                const f32x4 kj = isnew ? reinterpret_cast<const f32x4 *>(sk)[8 * wave + j] : kk[j];
-                a0 = fmaf(q0.x, kj.x, a0); a0 = fmaf(q0.y, kj.y, a0);
-                a0 = fmaf(q0.z, kj.z, a0); a0 = fmaf(q0.w, kj.w, a0);
-                a1 = fmaf(q1.x, kj.x, a1); a1 = fmaf(q1.y, kj.y, a1);
-                a1 = fmaf(q1.z, kj.z, a1); a1 = fmaf(q1.w, kj.w, a1);
+                a0 = fmaf(q0.x, kk[j].x, a0); a0 = fmaf(q0.y, kk[j].y, a0);
+                a0 = fmaf(q0.z, kk[j].z, a0); a0 = fmaf(q0.w, kk[j].w, a0);
+                a1 = fmaf(q1.x, kk[j].x, a1); a1 = fmaf(q1.y, kk[j].y, a1);
+                a1 = fmaf(q1.z, kk[j].z, a1); a1 = fmaf(q1.w, kk[j].w, a1);
             }
-            sc[wave][0][lane] = a0;
-            sc[wave][1][lane] = a1;
+            const bool isnew = t0 + base + lane == pos;
+            sc[wave][0][lane] = isnew ? an0 : a0;
+            sc[wave][1][lane] = isnew ? an1 : a1;
         }
         __syncthreads();
         // every wave sums the four partials of position `lane` and keeps the
@@ -476,11 +488,21 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const float pw0 = pe[0][vp + 8 * j], pw1 = pe[1][vp + 8 * j];   // 0 beyond n
-            const f32x4 v = t0 + base + vp + 8 * j == pos ? vnew : vv[j];
-            o0.x = fmaf(pw0, v.x, o0.x); o0.y = fmaf(pw0, v.y, o0.y);
-            o0.z = fmaf(pw0, v.z, o0.z); o0.w = fmaf(pw0, v.w, o0.w);
-            o1.x = fmaf(pw1, v.x, o1.x); o1.y = fmaf(pw1, v.y, o1.y);
-            o1.z = fmaf(pw1, v.z, o1.z); o1.w = fmaf(pw1, v.w, o1.w);
+            o0.x = fmaf(pw0, vv[j].x, o0.x); o0.y = fmaf(pw0, vv[j].y, o0.y);
+            o0.z = fmaf(pw0, vv[j].z, o0.z); o0.w = fmaf(pw0, vv[j].w, o0.w);
+            o1.x = fmaf(pw1, vv[j].x, o1.x); o1.y = fmaf(pw1, vv[j].y, o1.y);
+            o1.z = fmaf(pw1, vv[j].z, o1.z); o1.w = fmaf(pw1, vv[j].w, o1.w);
+        }
+        // the new position (its cache loads read zeros): v from vnew, once,
+        // in the lanes that own its row of the pass
+        {
+            const int inew = pos - t0 - base;
+            const bool own = inew >= 0 && inew < P && (inew & 7) == vp;
+            const float pn0 = own ? pe[0][inew & (P - 1)] : 0.0f, pn1 = own ? pe[1][inew & (P - 1)] : 0.0f;
+            o0.x = fmaf(pn0, vnew.x, o0.x); o0.y = fmaf(pn0, vnew.y, o0.y);
+            o0.z = fmaf(pn0, vnew.z, o0.z); o0.w = fmaf(pn0, vnew.w, o0.w);
+            o1.x = fmaf(pn1, vnew.x, o1.x); o1.y = fmaf(pn1, vnew.y, o1.y);
+            o1.z = fmaf(pn1, vnew.z, o1.z); o1.w = fmaf(pn1, vnew.w, o1.w);
         }
         __syncthreads();                          // sc / pe reused by the next pass
     }

@@ -204,7 +204,9 @@ class Batch:
 def main(argv=None):
     """Greedy generation on a seeded random-init blob:
     python -m n550_qwen3_bringup_handover_amd.model [--seed S] [--prompt N] [--decode N]
-                                                     [--repeat R] [--eager] [--tile]"""
+                                                     [--repeat R] [--eager] [--tile] [--batch B]
+    With --batch B, B sequences with their own random prompts of --prompt
+    tokens are decoded together (--repeat calls of --decode steps each)."""
     import argparse
     ap = argparse.ArgumentParser(description=main.__doc__)
     ap.add_argument("--seed", type=lambda v: int(v, 0), default=0x03550040)
@@ -213,8 +215,12 @@ def main(argv=None):
     ap.add_argument("--repeat", type=int, default=1)
     ap.add_argument("--eager", action="store_true", help="launch decode kernels one by one instead of a graph replay")
     ap.add_argument("--tile", action="store_true", help="tile-major blob")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="decode this many sequences together (each with its own random prompt)")
     args = ap.parse_args(argv)
     blob = qw3m_random(args.seed, LAYOUT_TILE if args.tile else LAYOUT_ROW, threads=16)
+    if args.batch:
+        return _main_batch(args, blob)
     prompt = np.random.default_rng(args.seed).integers(0, VOCAB, args.prompt).astype(np.int32)
     with Model(blob, max_seq=args.prompt + args.decode) as m:
         del blob
@@ -225,6 +231,25 @@ def main(argv=None):
             rate = args.decode / dec * 1e3 if dec > 0 else float("nan")
             print(f"run {r}: prefill {args.prompt} tokens {pre:.3f} ms; {args.decode} decode steps "
                   f"{dec:.3f} ms ({rate:.1f} tok/s); first tokens {toks[:8].tolist()}", flush=True)
+    return 0
+
+
+def _main_batch(args, blob):
+    import time
+    rng = np.random.default_rng(args.seed)
+    ctx = args.prompt + args.decode * args.repeat
+    with Model(blob, max_seq=ctx) as m, Batch(m, args.batch, ctx) as b:
+        del blob
+        b.set_graph(not args.eager)
+        t0 = time.time()
+        for s in range(args.batch):
+            b.prefill(s, rng.integers(0, VOCAB, args.prompt).astype(np.int32))
+        print(f"prefill: {args.batch} x {args.prompt} tokens in {time.time() - t0:.2f} s", flush=True)
+        for r in range(args.repeat):
+            out = b.decode(args.decode)
+            dec = b.timing()
+            print(f"run {r}: {args.decode} steps of {args.batch} sequences {dec:.3f} ms "
+                  f"({args.batch * args.decode / dec * 1e3:.1f} tok/s); seq 0 {out[0, :8].tolist()}", flush=True)
     return 0
 
 
