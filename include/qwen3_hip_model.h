@@ -131,8 +131,10 @@ int qwen3_hip_model_set_dump(qwen3_hip_model *model, qwen3_hip_dump_fn fn, void 
  * qwen3_hip_model_generate (first index of the maximum).
  *
  * The batch borrows the model's weights, rope tables and activation
- * buffers: close it before the model.  Its calls, like the model's, are
- * synchronous; a batch call discards the model's last logits. */
+ * buffers: close it before the model.  If the model is closed first, the
+ * batch's later calls return QWEN3_HIP_ESTATE (qwen3_hip_batch_close still
+ * frees it).  Its calls, like the model's, are synchronous; a batch call
+ * discards the model's last logits. */
 typedef struct qwen3_hip_batch qwen3_hip_batch;
 
 /* n_seq in 1 .. 128 (QWEN3_MAX_BATCH rows per GEMM); max_ctx in 2 ..

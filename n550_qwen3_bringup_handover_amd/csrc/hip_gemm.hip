@@ -2011,6 +2011,14 @@ static int g_forced_plan = 0;
 static int g_no_xcd_map = 0;      // tuning switch: 1 = row-major tile order
 #define QH_MAX_GRAPHS 16
 static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
+// Workspaces replaced while a graph exists: a captured graph keeps the device
+// addresses it was recorded with, so a grown workspace's old buffer stays
+// allocated until no graph is left (or the library shuts down).
+#define QH_MAX_RETIRED 64
+static void *g_retired[QH_MAX_RETIRED];
+static int g_n_retired = 0;
+static bool any_graph(void);
+static void free_retired(void);
 static int g_capturing = 0;
 static float *g_am_v = nullptr;   // argmax partials (allocated at init)
 static int *g_am_i = nullptr;
@@ -2080,6 +2088,7 @@ extern "C" void qh_shutdown(void) {
     (void)hipStreamSynchronize(g_stream);
     for (int i = 0; i < QH_MAX_GRAPHS; i++)
         if (g_graph_exec[i]) { (void)hipGraphExecDestroy(g_graph_exec[i]); g_graph_exec[i] = nullptr; }
+    free_retired();
     for (int i = 0; i < 64; i++)
         if (g_ev_made[i]) { (void)hipEventDestroy(g_ev[i]); g_ev_made[i] = 0; }
     (void)hipFree(g_abf);
@@ -2571,15 +2580,43 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     return QH_OK;
 }
 
+static bool any_graph(void) {
+    for (int i = 0; i < QH_MAX_GRAPHS; i++)
+        if (g_graph_exec[i]) return true;
+    return false;
+}
+
+// drop a workspace buffer that has been replaced: freed at once when no graph
+// can hold its address, else kept until the last graph is destroyed; false
+// (nothing changed) when the retired list is full
+static bool retire_buffer(void *p) {
+    if (!p) return true;
+    if (!any_graph()) {
+        (void)hipStreamSynchronize(g_stream);   // the old buffer may still be read
+        (void)hipFree(p);
+        return true;
+    }
+    if (g_n_retired >= QH_MAX_RETIRED) return false;
+    g_retired[g_n_retired++] = p;
+    return true;
+}
+
+static void free_retired(void) {
+    if (g_n_retired == 0) return;
+    (void)hipStreamSynchronize(g_stream);
+    for (int i = 0; i < g_n_retired; i++) (void)hipFree(g_retired[i]);
+    g_n_retired = 0;
+}
+
 // the split-K workspace holds at least `bytes` (grows only outside capture)
 static bool part_ensure(size_t bytes) {
     if (bytes >= (1ull << 31)) return false;           // the reduction's 32-bit offsets
     if (bytes <= g_part_bytes) return true;
     if (g_capturing) return false;
+    if (any_graph() && g_n_retired >= QH_MAX_RETIRED) return false;
     float *p = nullptr;
     if (hipMalloc((void **)&p, bytes) != hipSuccess) { (void)hipGetLastError(); return false; }
-    (void)hipStreamSynchronize(g_stream);      // the old buffer may still be read
-    (void)hipFree(g_part);
+    (void)retire_buffer(g_part);               // cannot fail: room checked above
     g_part = p;
     g_part_bytes = bytes;
     return true;
@@ -2743,10 +2780,10 @@ static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b,
 static bool abf_ensure(size_t n) {
     if (n <= g_abf_elems) return true;
     if (g_capturing) return false;
+    if (any_graph() && g_n_retired >= QH_MAX_RETIRED) return false;
     uint16_t *p = nullptr;
     if (hipMalloc((void **)&p, n * sizeof(uint16_t)) != hipSuccess) { (void)hipGetLastError(); return false; }
-    (void)hipStreamSynchronize(g_stream);      // the old buffer may still be read
-    (void)hipFree(g_abf);
+    (void)retire_buffer(g_abf);                // cannot fail: room checked above
     g_abf = p;
     g_abf_elems = n;
     return true;
@@ -2953,6 +2990,7 @@ extern "C" int qh_graph_destroy(int id) {
     if (id < 0 || id >= QH_MAX_GRAPHS || !g_graph_exec[id]) return QH_EINVAL;
     HCHECK(hipGraphExecDestroy(g_graph_exec[id]), QH_ERUNTIME);
     g_graph_exec[id] = nullptr;
+    if (!any_graph()) free_retired();
     return QH_OK;
 }
 

@@ -61,7 +61,10 @@ struct qwen3_hip_model {
     float *dump_host;                  /* staging for dumps */
     int have_logits;
     double t_prefill_ms, t_decode_ms;
+    struct qwen3_hip_batch *batches;   /* open batches on this model (linked by next) */
 };
+
+static void detach_batches(qwen3_hip_model *m);
 
 static double now_ms(void) {
     struct timespec ts;
@@ -127,6 +130,7 @@ static void rope_tables(float *c, float *s, int max_seq) {
 void qwen3_hip_model_close(qwen3_hip_model *m) {
     if (!m) return;
     (void)qh_sync();
+    detach_batches(m);
     if (m->graph_id >= 0) (void)qh_graph_destroy(m->graph_id);
     void *bufs[] = {m->wbuf, m->kc, m->vc, m->rcos, m->rsin, m->x, m->x0, m->x1, m->xb, m->qkv,
                     m->att, m->ob, m->hb, m->dn, m->logits, m->apart, m->tok_in, m->state, m->out_tok};
@@ -505,11 +509,29 @@ struct qwen3_hip_batch {
     int graph_id;
     int have_logits;
     double t_decode_ms;
+    qwen3_hip_batch *next;             /* the model's list of open batches */
 };
+
+/* A batch's graph holds the model's device addresses: when the model closes
+ * first, its batches lose the graph and the model, and later calls on them
+ * return QWEN3_HIP_ESTATE instead of touching freed memory. */
+static void detach_batches(qwen3_hip_model *m) {
+    for (qwen3_hip_batch *b = m->batches; b; b = b->next) {
+        if (b->graph_id >= 0) (void)qh_graph_destroy(b->graph_id);
+        b->graph_id = -1;
+        b->m = NULL;
+    }
+    m->batches = NULL;
+}
 
 void qwen3_hip_batch_close(qwen3_hip_batch *b) {
     if (!b) return;
     (void)qh_sync();
+    if (b->m) {
+        qwen3_hip_batch **pp = &b->m->batches;
+        while (*pp && *pp != b) pp = &(*pp)->next;
+        if (*pp) *pp = b->next;
+    }
     if (b->graph_id >= 0) (void)qh_graph_destroy(b->graph_id);
     void *bufs[] = {b->kc, b->vc, b->logits, b->part, b->tok, b->pos, b->plen, b->out};
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; i++) (void)qh_free(bufs[i]);
@@ -557,6 +579,8 @@ int qwen3_hip_batch_open(qwen3_hip_batch **out, qwen3_hip_model *m, int n_seq, i
     if (!rc) rc = qm_zero_i32(b->plen, n_seq);
     if (!rc) rc = qh_sync();
     if (rc) goto fail;
+    b->next = m->batches;
+    m->batches = b;
     *out = b;
     return QWEN3_HIP_OK;
 fail:
@@ -566,6 +590,7 @@ fail:
 
 int qwen3_hip_batch_set_graph(qwen3_hip_batch *b, int on) {
     if (!b) return QWEN3_HIP_EINVAL;
+    if (!b->m) return QWEN3_HIP_ESTATE;
     b->use_graph = on ? 1 : 0;
     return QWEN3_HIP_OK;
 }
@@ -573,6 +598,7 @@ int qwen3_hip_batch_set_graph(qwen3_hip_batch *b, int on) {
 int qwen3_hip_batch_prefill(qwen3_hip_batch *b, int seq, const int *prompt, int n_prompt) {
     if (!b || !prompt || seq < 0 || seq >= b->n_seq || n_prompt < 1 || n_prompt >= b->max_ctx)
         return QWEN3_HIP_EINVAL;
+    if (!b->m) return QWEN3_HIP_ESTATE;
     int rc = check_tokens(prompt, n_prompt);
     if (rc) return rc;
     qwen3_hip_model *m = b->m;
@@ -626,6 +652,7 @@ static int batch_step(qwen3_hip_batch *b) {
 
 int qwen3_hip_batch_decode(qwen3_hip_batch *b, int n_decode, int *out) {
     if (!b || !out || n_decode < 0) return QWEN3_HIP_EINVAL;
+    if (!b->m) return QWEN3_HIP_ESTATE;
     for (int s = 0; s < b->n_seq; s++)
         if (b->h_next[s] < 0 || (long)b->h_next[s] + n_decode > b->max_ctx) return QWEN3_HIP_EINVAL;
     int rc = QWEN3_HIP_OK;
@@ -671,6 +698,7 @@ int qwen3_hip_batch_decode(qwen3_hip_batch *b, int n_decode, int *out) {
 
 int qwen3_hip_batch_logits(qwen3_hip_batch *b, float *out) {
     if (!b || !out || !b->have_logits) return QWEN3_HIP_EINVAL;
+    if (!b->m) return QWEN3_HIP_ESTATE;
     int rc = qh_d2h(out, b->logits, (size_t)b->n_seq * V * sizeof(float));
     if (!rc) rc = qh_sync();
     return rc;

@@ -59,3 +59,47 @@ def test_graph_replay_matches_eager():
             abi.sync()
     finally:
         runtime.check(L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
+
+
+def test_graph_survives_workspace_growth():
+    """A graph keeps the device addresses it was captured with: when a later
+    call grows a workspace the graph uses (here the bf16 A staging of the
+    `xb` plans, grown by a larger forced call), the old buffer must stay
+    allocated until the graph is destroyed, and replays stay exact."""
+    L = runtime.init()
+    M, K, N = 256, 1024, 256
+    a = oracle.f32_bf16_normal(M * K, 61)
+    w = oracle.bf16_normal(N * K, 62, 0.02)
+    ad, wd, cd = abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(w), abi.DeviceBuffer(4 * M * N)
+    # larger than the initial staging (8192 x 3072 elements)
+    M2, K2, N2 = 8192, 4096, 128
+    a2 = oracle.f32_bf16_normal(M2 * K2, 63)
+    w2 = oracle.bf16_normal(N2 * K2, 64, 0.02)
+    ad2, wd2, cd2 = abi.DeviceBuffer.from_array(a2), abi.DeviceBuffer.from_array(w2), abi.DeviceBuffer(4 * M2 * N2)
+    abi.force_plan(abi.PLANS["xb128x128"])
+    try:
+        abi.gemm_dev(cd.ptr, ad.ptr, wd.ptr, M, K, N)
+        abi.sync()
+        eager = cd.download(np.float32, M * N)
+        numerics.compare(eager, a, w, M, K, N)
+        runtime.check(L.qwen3_hip_capture_begin(), "capture_begin")
+        abi.gemm_dev(cd.ptr, ad.ptr, wd.ptr, M, K, N)
+        gid = ctypes.c_int(-1)
+        runtime.check(L.qwen3_hip_capture_end(ctypes.byref(gid)), "capture_end")
+        try:
+            abi.gemm_dev(cd2.ptr, ad2.ptr, wd2.ptr, M2, K2, N2)     # grows the staging buffer
+            abi.sync()
+            big = cd2.download(np.float32, M2 * N2)
+            numerics.compare(big[:16 * N2], a2[:16 * K2], w2, 16, K2, N2)
+            for rep in range(3):
+                cd.upload(np.full(M * N, np.nan, np.float32))
+                runtime.check(L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+                abi.sync()
+                got = cd.download(np.float32, M * N)
+                assert np.array_equal(eager.view(np.uint32), got.view(np.uint32)), rep
+                abi.gemm_dev(cd2.ptr, ad2.ptr, wd2.ptr, M2, K2, N2)   # eager work between replays
+                abi.sync()
+        finally:
+            runtime.check(L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
+    finally:
+        abi.force_plan(0)

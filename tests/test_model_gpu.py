@@ -401,3 +401,21 @@ def test_batch_errors(model):
         b.decode(6)                                # sequence 1 reaches position 15
         with pytest.raises(runtime.Qwen3HipError):
             b.decode(1)                            # past max_ctx for sequence 1
+
+
+def test_batch_after_model_close_is_refused(blob):
+    """Closing the model first takes the batch's graph down with it; the
+    batch's later calls are refused instead of touching freed memory."""
+    with M.Model(blob, max_seq=64) as m:
+        b = M.Batch(m, 2, 32)
+        b.prefill(0, [1, 2, 3])
+        b.prefill(1, [4, 5])
+        out = b.decode(3)                      # captures the step graph
+        assert out.shape == (2, 4)
+    try:
+        with pytest.raises(runtime.Qwen3HipError, match="state"):
+            b.decode(1)
+        with pytest.raises(runtime.Qwen3HipError, match="state"):
+            b.prefill(0, [1])
+    finally:
+        b.close()
