@@ -47,7 +47,7 @@ def gemv_bytes(K, N, nb=1):
     return 2 * N * K * nb + 4 * K + 4 * N
 
 
-# the 197 reference GEMV calls of one decode token (cfg 2)
+# the 197 reference GEMV calls of one decode token (M = 1)
 STEP_BYTES = LAYERS * (gemv_bytes(H, Q) + 2 * gemv_bytes(H, KV) + gemv_bytes(Q, H)
                        + 2 * gemv_bytes(H, I) + gemv_bytes(I, H)) + gemv_bytes(H, V)
 assert STEP_BYTES == 1195103744
@@ -215,7 +215,7 @@ def host_path(steps=5):
             "error": err}
 
 
-def model_cfg4(n_prompt=128, n_decode=128):
+def model_forward_p128_d128(n_prompt=128, n_decode=128):
     """Full Qwen3-0.6B forward on the device (include/qwen3_hip_model.h):
     random-init weights, a 128-token random prompt in one prefill chunk, then
     128 greedy decode steps (one graph replay each)."""
@@ -490,8 +490,9 @@ SHAPES = {"q": (H, Q, False), "k_v": (H, KV, False), "o": (Q, H, False),
 
 
 def gemm_tables(g):
-    """BASELINE configs 1, 3 and 5 plus an M sweep, on the automatic plans.
-    Warm: the same operands every launch (resident in L2/MALL); config 3
+    """The M = 16 gate_proj GEMM, the M = 512 prefill set, the M = 64 batched-
+    decode set and an M sweep, on the automatic plans.  Warm: the same
+    operands every launch (resident in L2/MALL); the M = 512 set
     also cold, rotating through weight copies larger than the last-level
     cache."""
     Mmax = 4096
@@ -501,33 +502,33 @@ def gemm_tables(g):
     w = g.alloc(2 * 2 * I * H)
     g.fill_bf16(w, 2 * I * H, 22)
     out = {}
-    # config 1: one gate_proj GEMM at M = 16 (HBM-bound)
-    out["cfg1_m16_gate_proj"] = gemm_entry(g, 16, H, I, False, a, c, w)
-    # config 3: M = 512, warm and cold
+    # one gate_proj GEMM at M = 16 (HBM-bound)
+    out["m16_gate_proj"] = gemm_entry(g, 16, H, I, False, a, c, w)
+    # prefill at M = 512, warm and cold
     ncopy = 48                                   # 48 x 12.6 MB = 604 MB of weights
     wrot = [g.alloc(2 * 2 * I * H) for _ in range(ncopy)]
     for p in wrot:
         g.fill_bf16(p, 2 * I * H, 23)
-    cfg3 = {}
+    m512 = {}
     for name, (K, N, gated) in SHAPES.items():
-        cfg3[name] = gemm_entry(g, 512, K, N, gated, a, c, w)
-        cfg3[name]["cold_us"] = gemm_entry(g, 512, K, N, gated, a, c, w, wrot=wrot, reps=ncopy)["us"]
-    out["cfg3_m512"] = cfg3
+        m512[name] = gemm_entry(g, 512, K, N, gated, a, c, w)
+        m512[name]["cold_us"] = gemm_entry(g, 512, K, N, gated, a, c, w, wrot=wrot, reps=ncopy)["us"]
+    out["m512_prefill"] = m512
     # M sweep (warm)
     sweep = {}
     for M in (1024, 2048, 4096):
         sweep[str(M)] = {name: gemm_entry(g, M, K, N, gated, a, c, w) for name, (K, N, gated) in SHAPES.items()}
     out["m_sweep"] = sweep
-    # config 5: one GPU's share of batched decode, M = 64, incl. lm_head 64 x 1024 x 151936
+    # one GPU's share of batched decode of 64 sequences, M = 64, incl. lm_head 64 x 1024 x 151936
     emb = g.alloc(2 * V * H)
     g.fill_bf16(emb, V * H, 24)
-    cfg5 = {name: gemm_entry(g, 64, K, N, gated, a, c, w) for name, (K, N, gated) in SHAPES.items()}
+    m64 = {name: gemm_entry(g, 64, K, N, gated, a, c, w) for name, (K, N, gated) in SHAPES.items()}
     cl = g.alloc(4 * 64 * V)
-    cfg5["lm_head"] = gemm_entry(g, 64, H, V, False, a, cl, emb, reps=16)
-    layer_us = sum(cfg5[n]["us"] for n in ("qkv_fused", "o", "gate_up_silu", "down"))
-    cfg5["step_us"] = round(LAYERS * layer_us + cfg5["lm_head"]["us"], 1)
-    cfg5["tok_s_projections"] = round(64 / (cfg5["step_us"] * 1e-6), 1)
-    out["cfg5_m64"] = cfg5
+    m64["lm_head"] = gemm_entry(g, 64, H, V, False, a, cl, emb, reps=16)
+    layer_us = sum(m64[n]["us"] for n in ("qkv_fused", "o", "gate_up_silu", "down"))
+    m64["step_us"] = round(LAYERS * layer_us + m64["lm_head"]["us"], 1)
+    m64["tok_s_projections"] = round(64 / (m64["step_us"] * 1e-6), 1)
+    out["m64_batched_decode"] = m64
     return out
 
 
@@ -562,7 +563,7 @@ def main():
                     help="launch the 113 kernels of a step one by one instead of replaying a graph")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 64 MiB copy kernel (traffic-counter calibration)")
-    ap.add_argument("--no-model", action="store_true", help="skip the full-forward (cfg 4) measurement")
+    ap.add_argument("--no-model", action="store_true", help="skip the full-forward and batched-decode measurements")
     ap.add_argument("--gemm-shape", default=None, metavar="M,K,N,GATED",
                     help="only time one GEMM shape on its automatic plan (--steps launches, "
                          "graph-replayed) and print one JSON line; for profiling runs")
@@ -590,8 +591,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the hot path is a "
-                                   "single-GPU GEMM/GEMV library; see DESIGN.md for how it "
-                                   "would shard", "n_gpus": args.gpus}))
+                                   "single-GPU GEMM/GEMV library; sharding is designed, "
+                                   "not built", "n_gpus": args.gpus}))
         return 2
 
     # CPU baselines first, before this process touches the GPU
@@ -647,7 +648,7 @@ def main():
 
     model = batch = None
     if not args.no_model:
-        model = model_cfg4()
+        model = model_forward_p128_d128()
         model["cpu_baseline"] = cpu_model
         batch = model_batch_decode()
     hostp = None if args.no_extras else host_path()
@@ -668,7 +669,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kclasses,
         "gemm": gemms,
-        "model_cfg4": model,
+        "model_forward_p128_d128": model,
         "model_batch_decode": batch,
         "host_pointer_path": hostp,
     }

@@ -20,7 +20,7 @@ The blob itself (1.19 GB) is not stored: tests rebuild it from the seed with
 the library's QW3M writer and compare the checksum first.  The prompt comes
 from the oracle's SplitMix64 stream.  Usage:
 
-    python tests/golden/make_model_fixtures.py [short|cfg4|batch|dump|all]
+    python tests/golden/make_model_fixtures.py [short|p128_d128|batch|dump|all]
 """
 import ctypes
 import os
@@ -43,7 +43,7 @@ PROMPT_SEED = SEED + 0x1000
 CASES = {
     # name: (n_prompt, n_decode, keep prefill logits)
     "short": (5, 8, True),
-    "cfg4": (128, 128, False),
+    "p128_d128": (128, 128, False),
 }
 
 

@@ -117,14 +117,14 @@ def test_short_greedy_tokens(model):
     assert_tokens(got, fx, "short")
 
 
-def test_cfg4_greedy_tokens(model):
-    fx = fixture("cfg4")
+def test_p128_d128_greedy_tokens(model):
+    fx = fixture("p128_d128")
     n_decode = len(fx["tokens"]) - 1
     got = model.generate(fx["prompt"], n_decode)
     pre, dec = model.timing()
-    print(f"cfg4: prefill {len(fx['prompt'])} tokens {pre:.2f} ms, {n_decode} decode steps "
+    print(f"128-token prompt: prefill {len(fx['prompt'])} tokens {pre:.2f} ms, {n_decode} decode steps "
           f"{dec:.2f} ms = {n_decode / dec * 1e3:.1f} tok/s", flush=True)
-    assert_tokens(got, fx, "cfg4")
+    assert_tokens(got, fx, "p128_d128")
 
 
 def test_graph_and_eager_decode_agree(model):
@@ -216,7 +216,7 @@ def _ref_hip():
     return L
 
 
-@pytest.mark.parametrize("case", ["short", "cfg4"])
+@pytest.mark.parametrize("case", ["short", "p128_d128"])
 def test_reference_forward_with_gpu_plugin(blob, case):
     """The reference's own forward (qwen3.c + ops_scalar.c) linked with this
     plug-in as its KERNEL: every GEMM of the forward goes through qwen3_gemm /
@@ -246,12 +246,12 @@ def test_reference_forward_with_gpu_plugin(blob, case):
 
 def _batch_cases():
     """(prompt, tokens, margins) per sequence: the three batch prompts and
-    the short and cfg4 prompts, interleaved so prompt lengths are ragged."""
+    the short and 128-token prompts, interleaved so prompt lengths are ragged."""
     fb = fixture("batch")
     lens = fb["prompt_lens"]
     starts = np.concatenate([[0], np.cumsum(lens)])
     extra = [(fb["prompts"][starts[i]:starts[i + 1]], fb["tokens"][i], fb["margins"][i]) for i in range(len(lens))]
-    fs, fc = fixture("short"), fixture("cfg4")
+    fs, fc = fixture("short"), fixture("p128_d128")
     return [extra[0], (fs["prompt"], fs["tokens"], fs["margins"]), extra[1],
             (fc["prompt"], fc["tokens"], fc["margins"]), extra[2]]
 
@@ -338,16 +338,16 @@ def test_batch_split_calls_graph_and_eager_agree(model):
 def test_batch_reprefill_one_sequence(model):
     """Re-prefilling one sequence restarts it while the others continue."""
     cases = _batch_cases()
-    fc = fixture("cfg4")
+    fc = fixture("p128_d128")
     with M.Batch(model, len(cases), 160) as b:
         for s, (p, _, _) in enumerate(cases):
             b.prefill(s, p)
         first = b.decode(3)
         b.prefill(1, cases[0][0])                 # sequence 1 now holds prompt 0
         second = b.decode(5)
-    # cfg4 (sequence 3) continues: its 9 tokens over both calls
+    # the 128-token prompt (sequence 3) continues: its 9 tokens over both calls
     cont = np.concatenate([first[3], second[3, 1:]])
-    _check_row(cont, fc["tokens"][:9], fc["margins"], "cfg4 continued")
+    _check_row(cont, fc["tokens"][:9], fc["margins"], "128-token prompt continued")
     _check_row(second[1], cases[0][1][:6], cases[0][2], "re-prefilled seq 1")
     _check_row(np.concatenate([first[0], second[0, 1:]]), cases[0][1][:9], cases[0][2], "seq 0 continued")
 
