@@ -419,3 +419,27 @@ def test_batch_after_model_close_is_refused(blob):
             b.prefill(0, [1])
     finally:
         b.close()
+
+
+@pytest.mark.parametrize("n_seq", [1, 128])
+def test_batch_size_limits(model, n_seq):
+    """The smallest batch (every projection an M = 1 GEMV) and the largest
+    (M = 128 GEMMs): each sequence's logits after a few steps equal the
+    single-sequence forward of its prompt plus the fed tokens."""
+    rng = np.random.default_rng(100 + n_seq)
+    lens = rng.integers(1, 40, n_seq)
+    prompts = [rng.integers(0, M.VOCAB, n).astype(np.int32) for n in lens]
+    n_dec = 3
+    with M.Batch(model, n_seq, 48) as b:
+        for s in range(n_seq):
+            b.prefill(s, prompts[s])
+        out = b.decode(n_dec)
+        lb = b.logits()
+    assert out.shape == (n_seq, n_dec + 1)
+    assert np.all((out >= 0) & (out < M.VOCAB))
+    for s in sorted({0, n_seq // 2, n_seq - 1}):
+        _forward_all(model, np.concatenate([prompts[s], out[s, :n_dec]]))
+        ls = model.logits()
+        err = float(np.abs(ls.astype(np.float64) - lb[s]).max())
+        assert err <= LOGIT_TOL, f"n_seq {n_seq}, seq {s}: max abs logit diff {err:.3e}"
+        assert out[s, n_dec] == int(np.argmax(lb[s]))
