@@ -443,3 +443,30 @@ def test_batch_size_limits(model, n_seq):
         err = float(np.abs(ls.astype(np.float64) - lb[s]).max())
         assert err <= LOGIT_TOL, f"n_seq {n_seq}, seq {s}: max abs logit diff {err:.3e}"
         assert out[s, n_dec] == int(np.argmax(lb[s]))
+
+
+def test_longest_context(blob):
+    """max_seq = 8192, the largest cache (the prefill attention then keeps
+    2 x 8192 scores in 70.7 KB of LDS, past the default 64 KB): an
+    8,180-token prompt prefilled in chunks of 128 and in chunks of 100 gives
+    the same last logits within LOGIT_TOL; 11 decode steps to position 8190
+    follow, and the last step's logits equal a forward of the whole
+    sequence."""
+    rng = np.random.default_rng(8192)
+    prompt = rng.integers(0, M.VOCAB, 8180).astype(np.int32)
+    with M.Model(blob, max_seq=8192) as m:
+        toks = m.generate(prompt, 11)                 # prefill in chunks of 128, then 11 steps
+        l_gen = m.logits()
+        assert len(toks) == 12 and np.all((toks >= 0) & (toks < M.VOCAB))
+        for p0 in range(0, len(prompt), 100):        # other chunk boundaries
+            m.forward(prompt[p0:p0 + 100], p0)
+        l100 = m.logits()
+        top2 = np.sort(l100)[-2:]
+        assert toks[0] == int(np.argmax(l100)) or top2[1] - top2[0] < TIE_TOL
+        seq = np.concatenate([prompt, toks[:11]])    # the 11 fed tokens, last at position 8190
+        for p0 in range(8180, len(seq), 128):
+            m.forward(seq[p0:p0 + 128], p0)
+        l_fwd = m.logits()
+    err = float(np.abs(l_fwd.astype(np.float64) - l_gen).max())
+    print(f"context 8191: decode vs forward max abs logit diff {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
