@@ -320,7 +320,7 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 // ---------------------------------------------------------------------------
 // Decode attention split over positions: partials, merged by the o GEMV
 // ---------------------------------------------------------------------------
-// grid = (NKV * QM_ATT_SPLITS, n_seq): block (g, s) takes positions
+// grid = (NKV * S, n_seq): block (g, s) takes positions
 // [s*chunk, min(ctx, (s+1)*chunk)) of kv head g, chunk = ceil(ctx / splits),
 // for both query heads of the group.  Every block normalises and ropes the
 // group's two q heads itself (and the new k); block s = 0 writes the new k/v
@@ -342,7 +342,8 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 // out at entry, before the q prologue: one memory round trip per launch.
 // Batched decode: blockIdx.y is the sequence, with its own qkv row, position
 // pos_d[seq], cache (kv_seq floats after the previous sequence's) and
-// partials (QM_ATT_PART_FLOATS after the previous sequence's).
+// partials (8 * S * 2 * QM_ATT_PART floats after the previous sequence's).
+template <int S>
 __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv,
                                                    float *__restrict__ part,
                                                    float *__restrict__ kc, float *__restrict__ vc,
@@ -352,7 +353,6 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
                                                    const float *__restrict__ rsin,
                                                    const int *__restrict__ pos_d, int max_seq,
                                                    size_t kv_seq, float eps, float scale) {
-    constexpr int S = QM_ATT_SPLITS;
     constexpr int P = 64;                        // positions per pass
     const int g = blockIdx.x % NKV, sp = blockIdx.x / NKV;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -361,7 +361,7 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     qkv += (size_t)seq * QKV_LD;
     kc += (size_t)seq * kv_seq;
     vc += (size_t)seq * kv_seq;
-    part += (size_t)seq * QM_ATT_PART_FLOATS;
+    part += (size_t)seq * (8 * S * GRP * QM_ATT_PART);
     const int pos = pos_d[seq];
     if (pos < 0 || pos >= max_seq) return;      // uniform per launch
     const int ctx = pos + 1;
@@ -529,11 +529,11 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
 // prologue: out = sum_s e^(m_s - M) o_s / sum_s e^(m_s - M) l_s, M = max_s m_s.
 // grid = (NKV, n_seq), 256 threads = 2 query heads x 128 dims.
 // ---------------------------------------------------------------------------
+template <int S>
 __global__ __launch_bounds__(NTH) void k_attn_merge(float *__restrict__ att, const float *__restrict__ part) {
-    constexpr int S = QM_ATT_SPLITS;
     const int g = blockIdx.x, seq = blockIdx.y, tid = threadIdx.x;
     const int h = tid >> 7, d = tid & (HD - 1);
-    const float *pp = part + (size_t)seq * QM_ATT_PART_FLOATS + (size_t)(g * S * GRP + h) * QM_ATT_PART;
+    const float *pp = part + (size_t)seq * (8 * S * GRP * QM_ATT_PART) + (size_t)(g * S * GRP + h) * QM_ATT_PART;
     float m[S], l[S], o[S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
@@ -680,7 +680,7 @@ extern "C" int qm_attention_decode_part(const float *qkv, float *part, float *kc
     if (!qkv || !part || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
     const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
-    hipLaunchKernelGGL(k_attn_part, dim3(NKV * QM_ATT_SPLITS), dim3(NTH), 0, stream(), qkv, part, kc, vc,
+    hipLaunchKernelGGL(k_attn_part<QM_ATT_SPLITS>, dim3(NKV * QM_ATT_SPLITS), dim3(NTH), 0, stream(), qkv, part, kc, vc,
                        qn, kn, rcos, rsin, pos_d, max_seq, (size_t)0, eps, scale);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
@@ -694,10 +694,10 @@ extern "C" int qm_attention_decode_batch(const float *qkv, float *att, float *pa
     if (n_seq <= 0 || n_seq > QM_MAX_CHUNK || max_seq <= 0 || max_seq > QM_MAX_SEQ) return QH_EINVAL;
     if (kv_seq < (size_t)NKV * HD * max_seq) return QH_EINVAL;     // sequences' caches must not overlap
     const float scale = 0.08838834764831845f;   // 1 / sqrt(head_dim), qwen3.c:311
-    hipLaunchKernelGGL(k_attn_part, dim3(NKV * QM_ATT_SPLITS, n_seq), dim3(NTH), 0, stream(), qkv, part, kc,
-                       vc, qn, kn, rcos, rsin, pos_d, max_seq, kv_seq, eps, scale);
+    hipLaunchKernelGGL(k_attn_part<QM_BATCH_SPLITS>, dim3(NKV * QM_BATCH_SPLITS, n_seq), dim3(NTH), 0, stream(),
+                       qkv, part, kc, vc, qn, kn, rcos, rsin, pos_d, max_seq, kv_seq, eps, scale);
     if (hipGetLastError() != hipSuccess) return QH_ELAUNCH;
-    hipLaunchKernelGGL(k_attn_merge, dim3(NKV, n_seq), dim3(NTH), 0, stream(), att, part);
+    hipLaunchKernelGGL(k_attn_merge<QM_BATCH_SPLITS>, dim3(NKV, n_seq), dim3(NTH), 0, stream(), att, part);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

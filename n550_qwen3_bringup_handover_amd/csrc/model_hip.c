@@ -499,7 +499,7 @@ struct qwen3_hip_batch {
     size_t kv_seq;                     /* floats of one sequence's cache in one layer */
     float *kc, *vc;                    /* [NL][n_seq][kv_seq] */
     float *logits;                     /* [n_seq][V] of the last decode step */
-    float *part;                       /* [n_seq][QM_ATT_PART_FLOATS] */
+    float *part;                       /* [n_seq][QM_BATCH_PART_FLOATS] */
     int *tok, *pos, *plen;             /* [n_seq]: next token fed, its position, prompt length */
     int *out;                          /* [n_seq][out_ld]: token i of a sequence at i = pos - plen + 1 */
     int *h_next;                       /* host: position of each sequence's next fed token (-1: empty) */
@@ -568,7 +568,7 @@ int qwen3_hip_batch_open(qwen3_hip_batch **out, qwen3_hip_model *m, int n_seq, i
     DEV(b->kc, kv_bytes);
     DEV(b->vc, kv_bytes);
     DEV(b->logits, (size_t)n_seq * V * sizeof(float));
-    DEV(b->part, (size_t)n_seq * QM_ATT_PART_FLOATS * sizeof(float));
+    DEV(b->part, (size_t)n_seq * QM_BATCH_PART_FLOATS * sizeof(float));
     DEV(b->tok, (size_t)n_seq * sizeof(int));
     DEV(b->pos, (size_t)n_seq * sizeof(int));
     DEV(b->plen, (size_t)n_seq * sizeof(int));

@@ -41,9 +41,14 @@ int qm_attention_decode_part(const float *qkv_d, float *part_d, float *kc_d, flo
 
 /* batched decode attention for n_seq sequences, one token each: row s of
  * qkv is sequence s's token at position pos[s]; its cache starts kv_seq
- * floats after sequence s-1's (same layout as above); part holds
- * QM_ATT_PART_FLOATS per sequence.  The split partials are merged into
- * att[n_seq][2048] (two launches) */
+ * floats after sequence s-1's (same layout as above); each kv head's
+ * positions are split into QM_BATCH_SPLITS ranges, whose partials (part:
+ * QM_BATCH_PART_FLOATS per sequence) are merged into att[n_seq][2048]
+ * (two launches) */
+#ifndef QM_BATCH_SPLITS
+#define QM_BATCH_SPLITS 8
+#endif
+#define QM_BATCH_PART_FLOATS (8 * QM_BATCH_SPLITS * 2 * QM_ATT_PART)
 int qm_attention_decode_batch(const float *qkv_d, float *att_d, float *part_d, float *kc_d, float *vc_d,
                               size_t kv_seq, const uint16_t *qn_d, const uint16_t *kn_d,
                               const float *rcos_d, const float *rsin_d, const int *pos_d, int n_seq,
