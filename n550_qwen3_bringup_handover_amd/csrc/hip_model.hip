@@ -14,8 +14,9 @@
 //   V cache       [layer][kv_head][max_seq][128]        (as qwen3.h:62-76)
 //   rope tables   [max_seq][64] cos and sin, built on the host with the
 //                 reference formula (ops_scalar.c:21-35)
-// The attention kernels keep 2 x max_seq scores in LDS (up to 69 KB at
-// QM_MAX_SEQ), above the default 64 KB limit that they raise once.
+// The chunk attention keeps its tokens' scores in LDS, sized by the chunk's
+// context: up to 69 KB at QM_MAX_SEQ with one token per block, above the
+// default 64 KB limit, which it raises once.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -195,125 +196,148 @@ __global__ __launch_bounds__(NTH) void k_qk_rope_cache(float *__restrict__ qkv, 
 }
 
 // ---------------------------------------------------------------------------
-// Chunk step 2: causal GQA attention (qwen3.c:377-436) for token i of the
-// chunk and kv head g (block (i, g), its GRP query heads), with roped q in
-// qkv and every key/value t <= pos0 + i in the cache (written by step 1).
-//   scores s[h][t] = q_h . k_t / sqrt(128); softmax over t (ops_scalar.c:
-//   37-44), normalised as there; out_h = sum_t p[h][t] v_t.
-// grid = (nt, NKV), 256 threads, dynamic LDS = qm_attention_lds_bytes().
+// Chunk step 2: causal GQA attention (qwen3.c:377-436) for QT consecutive
+// tokens of the chunk and kv head g: block (b, g) takes tokens QT b ..
+// QT b + QT - 1 (those below nt) with their GRP query heads, R = QT GRP rows
+// (row r = token r / GRP, head r % GRP), roped q in qkv and every key/value
+// t <= pos0 + i in the cache (written by step 1).
+//   scores s[r][t] = q_r . k_t / sqrt(128); softmax over t (ops_scalar.c:
+//   37-44), normalised as there; out_r = sum_t p[r][t] v_t.
+// Every K and V row a block loads serves all R rows, so the cache traffic
+// of a chunk falls by QT.  Positions past a row's own context score -inf
+// and weigh 0: its max, sums and weighted V are those of a one-token block
+// bit for bit (only exact zeros are added, after its own positions).
+// grid = (ceil(nt / QT), NKV), 256 threads, dynamic LDS =
+// qm_attention_lds_bytes(QT, ldp); ldp >= pos0 + nt is the score row stride.
 // ---------------------------------------------------------------------------
+template <int QT>
 __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv,
                                                    float *__restrict__ out,
                                                    const float *__restrict__ kc,
                                                    const float *__restrict__ vc,
-                                                   const int *__restrict__ pos_d, int max_seq,
-                                                   float scale) {
-    const int i = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+                                                   const int *__restrict__ pos_d, int nt, int max_seq,
+                                                   int ldp, float scale) {
+    constexpr int R = QT * GRP;
+    const int i0 = blockIdx.x * QT, g = blockIdx.y, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int pos0 = *pos_d;
-    const int pos = pos0 + i;
-    if (pos0 < 0 || pos >= max_seq) return;   // uniform per block, before any barrier
-    const int ctx = pos + 1;
+    const int nq = min(QT, nt - i0);           // tokens of this block
+    const int ctxmax = pos0 + i0 + nq;         // context of its last token
+    // uniform per block, before any barrier
+    if (pos0 < 0 || nq <= 0 || ctxmax > max_seq || ctxmax > ldp) return;
 
     extern __shared__ float sm[];
-    float *sq = sm;                            // [GRP][HD]
-    float *red = sq + GRP * HD;                // [4][GRP][HD] partial outputs
-    float *sred = red + 4 * GRP * HD;          // [2][4] block reductions
-    float *p = sred + 8;                       // [GRP][max_seq]
+    float *sq = sm;                            // [R][HD]
+    float *red = sq + R * HD;                  // [4][R][HD] partial outputs
+    float *sred = red + 4 * R * HD;            // [R][4] block reductions
+    float *p = sred + 4 * R;                   // [R][ldp]
 
-    sq[tid] = qkv[(size_t)i * QKV_LD + (size_t)g * GRP * HD + tid];   // 256 threads = GRP x HD
+    for (int e = tid; e < R * HD; e += NTH) {
+        const int r = e / HD, ti = i0 + r / GRP;
+        sq[e] = ti < nt ? qkv[(size_t)ti * QKV_LD + (size_t)(g * GRP + r % GRP) * HD + e % HD] : 0.0f;
+    }
     __syncthreads();
 
-    // scores
+    // scores: thread t loads key t once for all R rows
     const f32x4 *kbase = reinterpret_cast<const f32x4 *>(kc) + (size_t)g * (HD / 4) * max_seq;
-    for (int t = tid; t < ctx; t += NTH) {
+    for (int t = tid; t < ctxmax; t += NTH) {
         f32x4 kv[HD / 4];
 #pragma unroll
         for (int d4 = 0; d4 < HD / 4; d4++) kv[d4] = kbase[(size_t)d4 * max_seq + t];
-        float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
-        for (int d4 = 0; d4 < HD / 4; d4++) {
-            const f32x4 q0 = reinterpret_cast<const f32x4 *>(sq)[d4];
-            const f32x4 q1 = reinterpret_cast<const f32x4 *>(sq + HD)[d4];
-            s0 = fmaf(q0.x, kv[d4].x, s0); s0 = fmaf(q0.y, kv[d4].y, s0);
-            s0 = fmaf(q0.z, kv[d4].z, s0); s0 = fmaf(q0.w, kv[d4].w, s0);
-            s1 = fmaf(q1.x, kv[d4].x, s1); s1 = fmaf(q1.y, kv[d4].y, s1);
-            s1 = fmaf(q1.z, kv[d4].z, s1); s1 = fmaf(q1.w, kv[d4].w, s1);
+        for (int r = 0; r < R; r++) {
+            float sr = 0.0f;
+#pragma unroll
+            for (int d4 = 0; d4 < HD / 4; d4++) {
+                const f32x4 q = reinterpret_cast<const f32x4 *>(sq + r * HD)[d4];
+                sr = fmaf(q.x, kv[d4].x, sr); sr = fmaf(q.y, kv[d4].y, sr);
+                sr = fmaf(q.z, kv[d4].z, sr); sr = fmaf(q.w, kv[d4].w, sr);
+            }
+            p[r * ldp + t] = t <= pos0 + i0 + r / GRP ? sr * scale : -INFINITY;
         }
-        p[t] = s0 * scale;
-        p[max_seq + t] = s1 * scale;
     }
     __syncthreads();
 
-    // softmax per query head
-    float m0 = -INFINITY, m1 = -INFINITY;
-    for (int t = tid; t < ctx; t += NTH) {
-        m0 = fmaxf(m0, p[t]);
-        m1 = fmaxf(m1, p[max_seq + t]);
+    // softmax per row
+    float mr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) mr[r] = -INFINITY;
+    for (int t = tid; t < ctxmax; t += NTH)
+#pragma unroll
+        for (int r = 0; r < R; r++) mr[r] = fmaxf(mr[r], p[r * ldp + t]);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        mr[r] = wave_max(mr[r]);
+        if (lane == 0) sred[r * 4 + wave] = mr[r];
     }
-    m0 = wave_max(m0);
-    m1 = wave_max(m1);
-    if (lane == 0) { sred[wave] = m0; sred[4 + wave] = m1; }
     __syncthreads();
-    m0 = fmaxf(fmaxf(sred[0], sred[1]), fmaxf(sred[2], sred[3]));
-    m1 = fmaxf(fmaxf(sred[4], sred[5]), fmaxf(sred[6], sred[7]));
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        mr[r] = fmaxf(fmaxf(sred[r * 4 + 0], sred[r * 4 + 1]), fmaxf(sred[r * 4 + 2], sred[r * 4 + 3]));
     __syncthreads();
-    float e0 = 0.0f, e1 = 0.0f;
-    for (int t = tid; t < ctx; t += NTH) {
-        const float a0 = expf(p[t] - m0), a1 = expf(p[max_seq + t] - m1);
-        p[t] = a0;
-        p[max_seq + t] = a1;
-        e0 += a0;
-        e1 += a1;
+    float er[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) er[r] = 0.0f;
+    for (int t = tid; t < ctxmax; t += NTH)
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float av = expf(p[r * ldp + t] - mr[r]);
+            p[r * ldp + t] = av;
+            er[r] += av;
+        }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        er[r] = wave_sum(er[r]);
+        if (lane == 0) sred[r * 4 + wave] = er[r];
     }
-    e0 = wave_sum(e0);
-    e1 = wave_sum(e1);
-    if (lane == 0) { sred[wave] = e0; sred[4 + wave] = e1; }
     __syncthreads();
-    e0 = (sred[0] + sred[1]) + (sred[2] + sred[3]);
-    e1 = (sred[4] + sred[5]) + (sred[6] + sred[7]);
-    for (int t = tid; t < ctx; t += NTH) {
-        p[t] = p[t] / e0;
-        p[max_seq + t] = p[max_seq + t] / e1;
-    }
+#pragma unroll
+    for (int r = 0; r < R; r++) er[r] = (sred[r * 4 + 0] + sred[r * 4 + 1]) + (sred[r * 4 + 2] + sred[r * 4 + 3]);
+    for (int t = tid; t < ctxmax; t += NTH)
+#pragma unroll
+        for (int r = 0; r < R; r++) p[r * ldp + t] = p[r * ldp + t] / er[r];
     __syncthreads();
 
-    // out_h[d] = sum_t p[h][t] v_t[d]: wave w takes t = w, w+4, ...; lane l
-    // owns d = 2l, 2l+1 of both heads
-    f32x2 o0 = {0.f, 0.f}, o1 = {0.f, 0.f};
+    // out_r[d] = sum_t p[r][t] v_t[d]: wave w takes t = w, w+4, ...; lane l
+    // owns d = 2l, 2l+1 of every row; each V row serves all R rows
+    f32x2 o[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) o[r] = f32x2{0.f, 0.f};
     const f32x2 *vcache = reinterpret_cast<const f32x2 *>(vc + (size_t)g * max_seq * HD) + lane;
     int t = wave;
-    for (; t + 4 * 7 < ctx; t += 4 * 8) {      // 8 loads in flight per lane
+    for (; t + 4 * 7 < ctxmax; t += 4 * 8) {   // 8 loads in flight per lane
         f32x2 v[8];
 #pragma unroll
         for (int u = 0; u < 8; u++) v[u] = vcache[(size_t)(t + 4 * u) * (HD / 2)];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const float p0 = p[t + 4 * u], p1 = p[max_seq + t + 4 * u];
-            o0.x = __fadd_rn(o0.x, __fmul_rn(p0, v[u].x));
-            o0.y = __fadd_rn(o0.y, __fmul_rn(p0, v[u].y));
-            o1.x = __fadd_rn(o1.x, __fmul_rn(p1, v[u].x));
-            o1.y = __fadd_rn(o1.y, __fmul_rn(p1, v[u].y));
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float pw = p[r * ldp + t + 4 * u];
+                o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v[u].x));
+                o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v[u].y));
+            }
+    }
+    for (; t < ctxmax; t += 4) {
+        const f32x2 v = vcache[(size_t)t * (HD / 2)];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float pw = p[r * ldp + t];
+            o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v.x));
+            o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v.y));
         }
     }
-    for (; t < ctx; t += 4) {
-        const f32x2 v = vcache[(size_t)t * (HD / 2)];
-        const float p0 = p[t], p1 = p[max_seq + t];
-        o0.x = __fadd_rn(o0.x, __fmul_rn(p0, v.x));
-        o0.y = __fadd_rn(o0.y, __fmul_rn(p0, v.y));
-        o1.x = __fadd_rn(o1.x, __fmul_rn(p1, v.x));
-        o1.y = __fadd_rn(o1.y, __fmul_rn(p1, v.y));
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        red[(wave * R + r) * HD + 2 * lane] = o[r].x;
+        red[(wave * R + r) * HD + 2 * lane + 1] = o[r].y;
     }
-    red[(wave * GRP + 0) * HD + 2 * lane] = o0.x;
-    red[(wave * GRP + 0) * HD + 2 * lane + 1] = o0.y;
-    red[(wave * GRP + 1) * HD + 2 * lane] = o1.x;
-    red[(wave * GRP + 1) * HD + 2 * lane + 1] = o1.y;
     __syncthreads();
-    {
-        const int h = tid >> 7, d = tid & (HD - 1);   // 256 threads = GRP x HD
-        const float sacc = (red[(0 * GRP + h) * HD + d] + red[(1 * GRP + h) * HD + d]) +
-                           (red[(2 * GRP + h) * HD + d] + red[(3 * GRP + h) * HD + d]);
-        out[(size_t)i * (NKV * GRP * HD) + (size_t)(g * GRP + h) * HD + d] = sacc;
+    for (int e = tid; e < nq * GRP * HD; e += NTH) {
+        const int r = e / HD, d = e % HD;
+        const float sacc = (red[(0 * R + r) * HD + d] + red[(1 * R + r) * HD + d]) +
+                           (red[(2 * R + r) * HD + d] + red[(3 * R + r) * HD + d]);
+        out[(size_t)(i0 + r / GRP) * (NKV * GRP * HD) + (size_t)(g * GRP + r % GRP) * HD + d] = sacc;
     }
 }
 
@@ -635,8 +659,9 @@ __global__ void k_zero_i32(int *p, int n) {
 // ---------------------------------------------------------------------------
 static inline hipStream_t stream() { return (hipStream_t)qh_stream(); }
 
-extern "C" size_t qm_attention_lds_bytes(int max_seq) {
-    return sizeof(float) * ((size_t)GRP * HD + 4 * GRP * HD + 8 + (size_t)GRP * max_seq);
+extern "C" size_t qm_attention_lds_bytes(int qt, int ldp) {
+    const size_t r = (size_t)qt * GRP;
+    return sizeof(float) * (r * HD + 4 * r * HD + 4 * r + r * (size_t)ldp);
 }
 
 extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const int *tok, int emb_rows,
@@ -649,17 +674,27 @@ extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 
+// tokens per block of the chunk attention: two while their scores fit in
+// 64 KB (contexts up to ~3,440), else one.  Measured prefill of 128 / 512 /
+// 1024 / 2048 tokens: 1.92 / 8.2 / 18.5 / 45.1 ms with two, 2.00 / 9.0 /
+// 21.4 / 56.3 with one, 2.15 / 9.7 / 23.3 / 52.2 with four (fewer blocks
+// than CUs at short contexts)
+static int attention_qt(int ldp) {
+    return qm_attention_lds_bytes(2, ldp) <= 65536 ? 2 : 1;
+}
+
 extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const uint16_t *qn,
                             const uint16_t *kn, const float *rcos, const float *rsin, const int *pos_d,
-                            int nt, int max_seq, float eps) {
+                            int nt, int max_seq, int ctx_bound, float eps) {
     if (!stream()) return QH_ESTATE;
     if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (nt <= 0 || max_seq <= 0 || nt > QM_MAX_CHUNK || max_seq > QM_MAX_SEQ) return QH_EINVAL;
-    const size_t lds = qm_attention_lds_bytes(max_seq);
+    if (ctx_bound < nt || ctx_bound > max_seq) return QH_EINVAL;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute((const void *)k_attention, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)qm_attention_lds_bytes(QM_MAX_SEQ)) != hipSuccess)
+        // one token per block at the longest context needs more than the default 64 KB
+        if (hipFuncSetAttribute((const void *)k_attention<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)qm_attention_lds_bytes(1, QM_MAX_SEQ)) != hipSuccess)
             return QH_ELAUNCH;
         attr_set = true;
     }
@@ -668,8 +703,15 @@ extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const 
     hipLaunchKernelGGL(k_qk_rope_cache, dim3(nt, (NKV * GRP + NKV) / 4), dim3(NTH), 0, stream(), qkv, kc, vc,
                        qn, kn, rcos, rsin, pos_d, max_seq, eps);
     if (hipGetLastError() != hipSuccess) return QH_ELAUNCH;
-    hipLaunchKernelGGL(k_attention, dim3(nt, NKV), dim3(NTH), lds, stream(), qkv, out, kc, vc, pos_d, max_seq,
-                       scale);
+    const int qt = attention_qt(ctx_bound);
+    const size_t lds = qm_attention_lds_bytes(qt, ctx_bound);
+    const dim3 grid((nt + qt - 1) / qt, NKV);
+    if (qt == 2)
+        hipLaunchKernelGGL(k_attention<2>, grid, dim3(NTH), lds, stream(), qkv, out, kc, vc, pos_d, nt, max_seq,
+                           ctx_bound, scale);
+    else
+        hipLaunchKernelGGL(k_attention<1>, grid, dim3(NTH), lds, stream(), qkv, out, kc, vc, pos_d, nt, max_seq,
+                           ctx_bound, scale);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

@@ -304,10 +304,10 @@ static kv_t model_kv(qwen3_hip_model *m) {
     return kv;
 }
 
-/* nt tokens already in tok_in at positions pos0.. (pos0 set by the caller in
- * state[1]) of the sequence whose cache is kv; logits of the last row when
- * want_logits */
-static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int want_logits) {
+/* nt tokens already in tok_in at positions pos0.. (pos0 also set by the
+ * caller in state[1]) of the sequence whose cache is kv; logits of the last
+ * row when want_logits */
+static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int pos0, int want_logits) {
     int rc;
     const float eps = QW3M_RMS_EPS;
     /* with a dump callback the residual add of down_proj is done at the end
@@ -330,7 +330,7 @@ static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int want_logits
         DUMP(l, "v_proj_out", m->qkv, QKV_N, QW3M_Q_DIM + QW3M_KV_DIM, QW3M_KV_DIM);
         if (!rc) rc = qm_attention(m->qkv, m->att, kv->kc + l * kv->layer_stride,
                                    kv->vc + l * kv->layer_stride, L->qn, L->kn, m->rcos, m->rsin,
-                                   m->state + 1, nt, kv->max_seq, eps);
+                                   m->state + 1, nt, kv->max_seq, pos0 + nt, eps);
         DUMP(l, "attn_out", m->att, QW3M_Q_DIM, 0, QW3M_Q_DIM);
         if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, nt, QW3M_Q_DIM, H);
         DUMP(l, "o_proj_out", m->ob, H, 0, H);
@@ -408,7 +408,7 @@ int qwen3_hip_model_forward(qwen3_hip_model *m, const int *tokens, int n_token, 
     int rc = check_tokens(tokens, n_token);
     const kv_t kv = model_kv(m);
     if (!rc) rc = load_chunk(m, tokens, n_token, pos0);
-    if (!rc) rc = run_chunk(m, &kv, n_token, 1);
+    if (!rc) rc = run_chunk(m, &kv, n_token, pos0, 1);
     m->have_logits = rc == 0;
     return rc;
 }
@@ -442,7 +442,7 @@ int qwen3_hip_model_generate(qwen3_hip_model *m, const int *prompt, int n_prompt
     for (int p0 = 0; p0 < n_prompt && !rc; p0 += QM_MAX_CHUNK) {
         nt = n_prompt - p0 < QM_MAX_CHUNK ? n_prompt - p0 : QM_MAX_CHUNK;
         rc = load_chunk(m, prompt + p0, nt, p0);
-        if (!rc) rc = run_chunk(m, &kv, nt, p0 + nt == n_prompt);
+        if (!rc) rc = run_chunk(m, &kv, nt, p0, p0 + nt == n_prompt);
     }
     /* first token; state[1] = pos0 of the last chunk + nt = n_prompt */
     if (!rc) rc = qm_set_i32(m->state + 2, 0);
@@ -609,7 +609,7 @@ int qwen3_hip_batch_prefill(qwen3_hip_batch *b, int seq, const int *prompt, int 
     for (int p0 = 0; p0 < n_prompt && !rc; p0 += QM_MAX_CHUNK) {
         const int nt = n_prompt - p0 < QM_MAX_CHUNK ? n_prompt - p0 : QM_MAX_CHUNK;
         rc = load_chunk(m, prompt + p0, nt, p0);
-        if (!rc) rc = run_chunk(m, &kv, nt, p0 + nt == n_prompt);
+        if (!rc) rc = run_chunk(m, &kv, nt, p0, p0 + nt == n_prompt);
     }
     /* first token: out[seq][0] at pos - plen + 1 = 0, then pos = n_prompt */
     if (!rc) rc = qm_set_i32(b->pos + seq, n_prompt - 1);

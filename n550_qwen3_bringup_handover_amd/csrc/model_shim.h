@@ -22,11 +22,15 @@ int qm_rows_norm(float *x_d, const float *r_d, const uint16_t *emb_d, const int 
 
 /* QK-norm + RoPE + KV-cache write, then causal GQA attention, for nt tokens
  * at positions *pos_d .. *pos_d + nt - 1 of one layer (two launches); the
- * q part of qkv is left normalised and roped */
+ * q part of qkv is left normalised and roped.  ctx_bound (host-known,
+ * nt .. max_seq) must be >= *pos_d + nt: it sizes the scores in LDS (tokens
+ * whose context exceeds it are skipped) */
 int qm_attention(float *qkv_d, float *out_d, float *kc_d, float *vc_d, const uint16_t *qn_d,
                  const uint16_t *kn_d, const float *rcos_d, const float *rsin_d, const int *pos_d,
-                 int nt, int max_seq, float eps);
-size_t qm_attention_lds_bytes(int max_seq);
+                 int nt, int max_seq, int ctx_bound, float eps);
+/* dynamic LDS of the chunk attention with qt tokens per block and score
+ * rows of ldp floats */
+size_t qm_attention_lds_bytes(int qt, int ldp);
 
 /* decode attention split into QM_ATT_SPLITS position ranges per kv head:
  * writes softmax partials (m, l, o[128] per head and range, QM_ATT_PART
