@@ -26,7 +26,8 @@ static int g_layout;                    /* 0 ROW, 1 TILE */
 static int g_tile_n = 128, g_tile_k = 32;
 
 static void  *g_a_d;  static size_t g_a_cap;     /* device staging for A */
-static void  *g_c_d;  static size_t g_c_cap;     /* device staging for C */
+static void  *g_a_h;  static size_t g_a_hcap;    /* pinned host staging for A */
+static void  *g_c_h;  static size_t g_c_hcap;    /* pinned host staging for C */
 
 typedef struct {
     const unsigned char *host;
@@ -123,9 +124,12 @@ void qwen3_hip_release(void) {
     for (int i = 0; i < g_nmaps; i++) (void)qh_free(g_maps[i].dev);
     g_nmaps = 0;
     (void)qh_free(g_a_d);
-    (void)qh_free(g_c_d);
-    g_a_d = g_c_d = NULL;
-    g_a_cap = g_c_cap = 0;
+    g_a_d = NULL;
+    g_a_cap = 0;
+    (void)qh_host_free(g_a_h);
+    (void)qh_host_free(g_c_h);
+    g_a_h = g_c_h = NULL;
+    g_a_hcap = g_c_hcap = 0;
     qh_shutdown();
     g_ready = 0;
 }
@@ -336,6 +340,20 @@ drop:
 }
 
 /* ---- staging ------------------------------------------------------------------------ */
+static int grow_host(void **p, size_t *cap, size_t need) {
+    if (need <= *cap) return 0;
+    size_t n = *cap ? *cap : (1u << 20);
+    while (n < need) n *= 2;
+    (void)qh_sync();
+    (void)qh_host_free(*p);
+    *p = NULL;
+    *cap = 0;
+    int rc = qh_host_alloc(p, n);
+    if (rc) return rc;
+    *cap = n;
+    return 0;
+}
+
 static int grow(void **p, size_t *cap, size_t need) {
     if (need <= *cap) return 0;
     size_t n = *cap ? *cap : (1u << 20);
@@ -367,16 +385,25 @@ static int gemm_host(float *c, const float *a, const uint16_t *b, const uint16_t
     const uint16_t *bd2 = NULL;
     if (gated && !(bd2 = weight_dev(b2, N, K, layout, &rc))) return rc;
 
+    /* A goes host -> pinned staging (memcpy) -> device by the library's copy
+     * kernel, on the same stream as the GEMM (a runtime copy from host memory
+     * adds a cross-engine wait to every call); the GEMM writes C straight
+     * into pinned staging, which the host copies out after the sync.  Per
+     * M = 1 call: 17 us instead of 26 us with runtime copies both ways. */
     const size_t abytes = (size_t)M * (size_t)K * sizeof(float);
     const size_t cbytes = (size_t)M * (size_t)N * sizeof(float);
-    if ((rc = grow(&g_a_d, &g_a_cap, abytes))) return rc;
-    if ((rc = grow(&g_c_d, &g_c_cap, cbytes))) return rc;
-    if ((rc = qh_h2d(g_a_d, a, abytes))) return rc;
-    rc = gated ? qh_gemm_gate_up_silu((float *)g_c_d, (const float *)g_a_d, bd, bd2, M, K, N)
-               : qh_gemm((float *)g_c_d, (const float *)g_a_d, bd, M, K, N);
+    const size_t a16 = (abytes + 15) & ~(size_t)15;     /* the copy kernel moves 16-byte units */
+    if ((rc = grow(&g_a_d, &g_a_cap, a16))) return rc;
+    if ((rc = grow_host(&g_a_h, &g_a_hcap, a16))) return rc;
+    if ((rc = grow_host(&g_c_h, &g_c_hcap, cbytes))) return rc;
+    memcpy(g_a_h, a, abytes);
+    if ((rc = qh_copy(g_a_d, g_a_h, a16))) return rc;
+    rc = gated ? qh_gemm_gate_up_silu((float *)g_c_h, (const float *)g_a_d, bd, bd2, M, K, N)
+               : qh_gemm((float *)g_c_h, (const float *)g_a_d, bd, M, K, N);
     if (rc) return rc;
-    if ((rc = qh_d2h(c, g_c_d, cbytes))) return rc;
-    return qh_sync();
+    if ((rc = qh_sync())) return rc;
+    memcpy(c, g_c_h, cbytes);
+    return 0;
 }
 
 void qwen3_gemm(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
