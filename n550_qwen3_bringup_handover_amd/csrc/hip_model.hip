@@ -420,19 +420,21 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     //    and at the new position, which comes from sk / vnew instead
     const __amdgpu_buffer_rsrc_t rk = buf_rsrc(kc + (size_t)g * HD * max_seq, (size_t)HD * max_seq * 4);
     const __amdgpu_buffer_rsrc_t rv = buf_rsrc(vc + (size_t)g * max_seq * HD, (size_t)max_seq * HD * 4);
+    // non-temporal (aux 2): each cache entry is read once per step; measured
+    // +5% batched decode at context 2048 and +4% single-sequence decode
     auto load_pass = [&](int base, f32x4 (&kk)[8], f32x4 (&vv)[8]) {
         const int tk = t0 + base + lane;
         const bool kin = base + lane < n && tk < pos;
 #pragma unroll
         for (int j = 0; j < 8; j++)
             kk[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                        rk, kin ? (uint32_t)(((8 * wave + j) * max_seq + tk) * 16) : BUF_OOB, 0, 0));
+                        rk, kin ? (uint32_t)(((8 * wave + j) * max_seq + tk) * 16) : BUF_OOB, 0, 2));
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int i = base + vp + 8 * j;
             const int tv = t0 + i;
             vv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                        rv, (i < n && tv < pos) ? (uint32_t)((tv * (HD / 4) + vch) * 16) : BUF_OOB, 0, 0));
+                        rv, (i < n && tv < pos) ? (uint32_t)((tv * (HD / 4) + vch) * 16) : BUF_OOB, 0, 2));
         }
     };
     f32x4 kk[8], vv[8];
