@@ -2711,7 +2711,7 @@ static int skinny_slices(int K, int N) {
 // 2 GiB (checked by the caller); more than one slice needs the split-K workspace
 template <int MT, bool GATED>
 static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
-                           int M, int K, int N) {
+                           int M, int K, int N, bool reduce = true) {
     const int ks = skinny_slices(K, N);
     if (ks <= 0) return QH_EINVAL;
     const int nblk = (N + 63) / 64;
@@ -2724,7 +2724,7 @@ static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const ui
     hipLaunchKernelGGL((k_gemm_skinny<MT, GATED>), dim3(nblk, ks), dim3(NTHREADS), 0, g_stream, c, part, a, b, b2,
                        M, K, N, K / ks);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
-    if (ks > 1) {
+    if (ks > 1 && reduce) {
         size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
         if (blocks > 2048) blocks = 2048;
         hipLaunchKernelGGL((k_stream_reduce<GATED>), dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream,
@@ -2929,6 +2929,39 @@ extern "C" int qh_gemm_gate_up_silu_bf16a(float *h, const uint16_t *x, const uin
 }
 
 extern "C" int qh_gemm(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    return gemm_common(c, a, b, nullptr, M, K, N, false);
+}
+
+// qh_gemm, except that when the automatic plan is the skinny kernel with more
+// than one K slice, the slices' fp32 sums are left in the split-K workspace
+// ([ks][M][N], *part) for the caller to add in slice order -- the sums
+// k_stream_reduce would form -- instead of a second launch.  Otherwise C is
+// written and *ks = 0.  The partials last until the next call that uses the
+// workspace.
+extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M, int K, int N,
+                             const float **part, int *ks) {
+    if (!part || !ks) return QH_EINVAL;
+    *part = nullptr;
+    *ks = 0;
+    if (!g_inited) return QH_ESTATE;
+    const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
+    if (vec && !g_forced_plan && choose_plan(M, K, N, false, vec) == PLAN_SKINNY && M <= 64 && K % 64 == 0 &&
+        (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31)) {
+        const int s = skinny_slices(K, N);
+        if (s > 1 && part_ensure((size_t)s * M * N * sizeof(float))) {
+            int rc;
+            switch (stream_mt(M)) {
+                case 1: rc = launch_skinny_t<1, false>(c, a, b, nullptr, M, K, N, false); break;
+                case 2: rc = launch_skinny_t<2, false>(c, a, b, nullptr, M, K, N, false); break;
+                default: rc = launch_skinny_t<4, false>(c, a, b, nullptr, M, K, N, false); break;
+            }
+            if (rc == QH_OK) {
+                *part = g_part;
+                *ks = s;
+            }
+            return rc;
+        }
+    }
     return gemm_common(c, a, b, nullptr, M, K, N, false);
 }
 

@@ -94,15 +94,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t
 
 // ---------------------------------------------------------------------------
 // rows: x[row] = emb[tok[row]] (bf16 -> fp32)   when emb is set, else
-//       x[row] = x[row] + r[row]                 when r is set;
+//       x[row] = x[row] + r[row]                 when r is set, else
+//       x[row] = x[row] + sum_s part[s][row]     when ks > 0 (split-K slice
+//                sums added in slice order: the reduction pass's sums);
 //       xb[row] = rmsnorm(x[row]) * nw           (ops_scalar.c:11-16)
-// grid = nt blocks of 256 threads; K % 4 == 0, K <= 4096.
+// grid = nt blocks of 256 threads; K % 4 == 0, K <= 4096, ks <= KS_MAX.
 // ---------------------------------------------------------------------------
+#define KS_MAX 16
 __global__ __launch_bounds__(NTH) void k_rows_norm(float *__restrict__ x, const float *__restrict__ r,
                                                    const uint16_t *__restrict__ emb,
                                                    const int *__restrict__ tok, int emb_rows,
                                                    const uint16_t *__restrict__ nw,
-                                                   float *__restrict__ xb, int K, float eps) {
+                                                   float *__restrict__ xb, int K, float eps,
+                                                   const float *__restrict__ part, int ks, size_t pstride) {
     const int row = blockIdx.x, tid = threadIdx.x;
     const int n4 = K >> 2;
     f32x4 v[4];
@@ -123,8 +127,23 @@ __global__ __launch_bounds__(NTH) void k_rows_norm(float *__restrict__ x, const 
             } else {
                 v[j] = reinterpret_cast<const f32x4 *>(x + (size_t)row * K)[c];
                 if (r) v[j] += reinterpret_cast<const f32x4 *>(r + (size_t)row * K)[c];
+                if (ks > 0) {
+                    // every slice's load first, then the sum in slice order
+                    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(part, pstride * (size_t)ks * 4);
+                    f32x4 p[KS_MAX];
+#pragma unroll
+                    for (int s = 0; s < KS_MAX; s++)
+                        p[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                   rp, s < ks ? (uint32_t)(((size_t)s * pstride + (size_t)row * K + 4 * c) * 4) : BUF_OOB,
+                                   0, 0));
+                    f32x4 sum = p[0];
+#pragma unroll
+                    for (int s = 1; s < KS_MAX; s++)
+                        if (s < ks) sum += p[s];
+                    v[j] += sum;
+                }
             }
-            if (emb || r) reinterpret_cast<f32x4 *>(x + (size_t)row * K)[c] = v[j];
+            if (emb || r || ks > 0) reinterpret_cast<f32x4 *>(x + (size_t)row * K)[c] = v[j];
             ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
         }
     }
@@ -668,11 +687,20 @@ extern "C" size_t qm_attention_lds_bytes(int qt, int ldp) {
 
 extern "C" int qm_rows_norm(float *x, const float *r, const uint16_t *emb, const int *tok, int emb_rows,
                             const uint16_t *nw, float *xb, int nt, int K, float eps) {
+    return qm_rows_norm_split(x, r, emb, tok, emb_rows, nw, xb, nt, K, eps, nullptr, 0);
+}
+
+extern "C" int qm_rows_norm_split(float *x, const float *r, const uint16_t *emb, const int *tok, int emb_rows,
+                                  const uint16_t *nw, float *xb, int nt, int K, float eps, const float *part,
+                                  int ks) {
     if (!stream()) return QH_ESTATE;
     if (!x || !nw || !xb || nt <= 0 || K <= 0 || K % 4 || K > 4 * 4 * NTH) return QH_EINVAL;
     if (emb && (!tok || emb_rows <= 0)) return QH_EINVAL;
+    if (ks < 0 || ks > KS_MAX || (ks > 0 && (!part || emb || r))) return QH_EINVAL;
+    const size_t pstride = (size_t)nt * K;                  // one slice: [nt][K]
+    if (ks > 0 && pstride * ks * 4 >= ((size_t)1 << 31)) return QH_EINVAL;
     hipLaunchKernelGGL(k_rows_norm, dim3(nt), dim3(NTH), 0, stream(), x, emb ? nullptr : r, emb, tok,
-                       emb_rows, nw, xb, K, eps);
+                       emb_rows, nw, xb, K, eps, part, ks, pstride);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
 }
 

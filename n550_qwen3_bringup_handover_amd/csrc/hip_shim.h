@@ -48,6 +48,13 @@ void *qh_stream(void);                                    /* hipStream_t */
  * lda = ldb = K, ldc = N.  A is rounded to bf16 (RNE) on the load path. */
 int qh_gemm(float *c_d, const float *a_d, const uint16_t *b_d,
             int M, int K, int N);
+/* qh_gemm, but when the automatic plan splits K over the skinny kernel's
+ * blocks the ks > 1 fp32 slice sums are left in library workspace
+ * (*part_d: [ks][M][N]) for the caller to add in slice order instead of a
+ * reduction launch; otherwise C is written and *ks = 0.  The partials are
+ * valid until the next library call that uses the split-K workspace. */
+int qh_gemm_split(float *c_d, const float *a_d, const uint16_t *b_d, int M, int K, int N,
+                  const float **part_d, int *ks);
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */
 int qh_gemm_gate_up_silu(float *h_d, const float *x_d, const uint16_t *wg_d,
                          const uint16_t *wu_d, int M, int K, int N);

@@ -624,27 +624,34 @@ int qwen3_hip_batch_prefill(qwen3_hip_batch *b, int seq, const int *prompt, int 
     return rc;
 }
 
-/* one decode step of every sequence: token tok[s] at position pos[s] */
+/* one decode step of every sequence: token tok[s] at position pos[s].  When
+ * the o and down projections split K (the skinny kernel at small n), their
+ * slice sums are added by the residual + RMSNorm kernel that consumes them
+ * (the sums a reduction launch would form), one launch fewer each. */
 static int batch_step(qwen3_hip_batch *b) {
     qwen3_hip_model *m = b->m;
     const int n = b->n_seq;
     const float eps = QW3M_RMS_EPS;
     const size_t lstride = (size_t)n * b->kv_seq;
     int rc = QWEN3_HIP_OK;
+    const float *dpart = NULL, *opart = NULL;
+    int dks = 0, oks = 0;
     for (int l = 0; l < NL && !rc; l++) {
         const layer_t *L = &m->L[l];
         if (l == 0) rc = qm_rows_norm(m->x, NULL, m->embed, b->tok, V, L->in_norm, m->xb, n, H, eps);
-        else rc = qm_rows_norm(m->x, m->dn, NULL, NULL, 0, L->in_norm, m->xb, n, H, eps);
+        else rc = qm_rows_norm_split(m->x, dks ? NULL : m->dn, NULL, NULL, 0, L->in_norm, m->xb, n, H, eps, dpart, dks);
         if (!rc) rc = qh_gemm(m->qkv, m->xb, L->wqkv, n, H, QKV_N);
         if (!rc) rc = qm_attention_decode_batch(m->qkv, m->att, b->part, b->kc + l * lstride, b->vc + l * lstride,
                                                 b->kv_seq, L->qn, L->kn, m->rcos, m->rsin, b->pos, n,
                                                 b->max_ctx, eps);
-        if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, n, QW3M_Q_DIM, H);
-        if (!rc) rc = qm_rows_norm(m->x, m->ob, NULL, NULL, 0, L->post_norm, m->xb, n, H, eps);
+        if (!rc) rc = qh_gemm_split(m->ob, m->att, L->wo, n, QW3M_Q_DIM, H, &opart, &oks);
+        if (!rc) rc = qm_rows_norm_split(m->x, oks ? NULL : m->ob, NULL, NULL, 0, L->post_norm, m->xb, n, H, eps,
+                                         opart, oks);
         if (!rc) rc = qh_gemm_gate_up_silu(m->hb, m->xb, L->wg, L->wu, n, H, QW3M_INTER);
-        if (!rc) rc = qh_gemm(m->dn, m->hb, L->wd, n, QW3M_INTER, H);
+        if (!rc) rc = qh_gemm_split(m->dn, m->hb, L->wd, n, QW3M_INTER, H, &dpart, &dks);
     }
-    if (!rc) rc = qm_rows_norm(m->x, m->dn, NULL, NULL, 0, m->final_norm, m->xb, n, H, eps);
+    if (!rc) rc = qm_rows_norm_split(m->x, dks ? NULL : m->dn, NULL, NULL, 0, m->final_norm, m->xb, n, H, eps,
+                                     dpart, dks);
     if (!rc) rc = qh_gemm(b->logits, m->xb, m->embed, n, H, V);
     if (!rc) rc = qm_argmax_rows(b->logits, V, n, b->tok, b->pos, b->plen, b->out, b->out_ld);
     return rc;

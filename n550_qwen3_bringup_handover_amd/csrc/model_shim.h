@@ -19,6 +19,11 @@ extern "C" {
  * xb[row] = rmsnorm(x[row]) * nw;  nt rows of K floats */
 int qm_rows_norm(float *x_d, const float *r_d, const uint16_t *emb_d, const int *tok_d, int emb_rows,
                  const uint16_t *nw_d, float *xb_d, int nt, int K, float eps);
+/* the same with x[row] += sum of ks (<= 16) split-K slices of part_d
+ * ([ks][nt][K], added in slice order) instead of r (r_d and emb_d NULL) */
+int qm_rows_norm_split(float *x_d, const float *r_d, const uint16_t *emb_d, const int *tok_d, int emb_rows,
+                       const uint16_t *nw_d, float *xb_d, int nt, int K, float eps, const float *part_d,
+                       int ks);
 
 /* QK-norm + RoPE + KV-cache write, then causal GQA attention, for nt tokens
  * at positions *pos_d .. *pos_d + nt - 1 of one layer (two launches); the
