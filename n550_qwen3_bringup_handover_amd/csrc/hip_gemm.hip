@@ -1827,8 +1827,8 @@ __global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__rest
 // Skinny GEMM for M <= 64 with small N (batched-decode projections)
 // ---------------------------------------------------------------------------
 // C[M,N] = A[M,K]·B[N,K]^T with A short: blockIdx.x owns 64 rows of B (four
-// waves, 16 rows each) and blockIdx.y a K slice of KSL (a multiple of 64, at
-// most 256).  The block stages its slice of A once in LDS as bf16 (RNE), rows
+// waves, 16 rows each), blockIdx.y a K slice of KSL (a multiple of 64, at
+// most 256) and blockIdx.z a slab of 64 rows of A and C.  The block stages its slice of A once in LDS as bf16 (RNE), rows
 // of 16-byte chunks XOR-swizzled by row, so that the four waves read their
 // v_mfma_f32_16x16x32_bf16 A fragments from one copy instead of each block
 // re-reading A per 16-row tile; each wave issues all of its B loads (one 16-B
@@ -1850,6 +1850,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.y * ksl;
+    const int m0 = blockIdx.z * 64;                    // this block's 64-row slab of A and C
     const int ncs = ksl >> 3;                           // 16-byte chunks per row of the slice
     const int nst = ksl >> 5;                           // 32-deep steps
 
@@ -1863,7 +1864,8 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
     for (int i = 0; i < CPT; i++) {
         const int q = tid + NTHREADS * i;
         const int m = q / ncs, ch = q % ncs;
-        const uint32_t off = (q < total && m < M) ? (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4) : BUF_OOB;
+        const uint32_t off = (q < total && m0 + m < M) ? (uint32_t)(((size_t)(m0 + m) * K + k0 + 8 * ch) * 4)
+                                                         : BUF_OOB;
         alo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
         ahi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0);
     }
@@ -1931,7 +1933,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
         for (int mt = 0; mt < MT; mt++)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = 16 * mt + 4 * g + r;
+                const int m = m0 + 16 * mt + 4 * g + r;
                 if (m < M) {
                     const size_t o = (size_t)m * N + n;
                     if (part) {
@@ -2696,8 +2698,9 @@ static int launch_stream_t(float *c, const float *a, const uint16_t *b, const ui
 
 // K slices of the skinny kernel: multiples of 64, at most 256 deep; the
 // fewest that give every CU a 64-row block (else the most)
-static int skinny_slices(int K, int N) {
-    const long nblk = (N + 63) / 64;
+#define SKINNY_MMAX 256          // rows of A the skinny plan takes (slabs of 64)
+static int skinny_slices(int K, int N, int M = 64) {
+    const long nblk = (long)((N + 63) / 64) * ((M + 63) / 64);
     int best = 0;
     for (int ks = 1; ks <= K / 64 && ks <= RMAX; ks++) {
         if (K % ks || (K / ks) % 64 || K / ks > 256) continue;
@@ -2712,17 +2715,18 @@ static int skinny_slices(int K, int N) {
 template <int MT, bool GATED>
 static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                            int M, int K, int N, bool reduce = true) {
-    const int ks = skinny_slices(K, N);
+    const int ks = skinny_slices(K, N, M);
     if (ks <= 0) return QH_EINVAL;
     const int nblk = (N + 63) / 64;
+    const int mslab = (M + 63) / 64;
     const size_t MN = (size_t)M * N;
     float *part = nullptr;
     if (ks > 1) {
         if (!part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) return QH_ETOOBIG;
         part = g_part;
     }
-    hipLaunchKernelGGL((k_gemm_skinny<MT, GATED>), dim3(nblk, ks), dim3(NTHREADS), 0, g_stream, c, part, a, b, b2,
-                       M, K, N, K / ks);
+    hipLaunchKernelGGL((k_gemm_skinny<MT, GATED>), dim3(nblk, ks, mslab), dim3(NTHREADS), 0, g_stream, c, part, a,
+                       b, b2, M, K, N, K / ks);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     if (ks > 1 && reduce) {
         size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
@@ -2879,8 +2883,8 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
     if (is_xb_plan(plan) && !abf_ensure((size_t)M * K))            // no room for the bf16 copy of A
         plan = PLAN_X128x256;
     if (plan == PLAN_SKINNY) {
-        const int ks = (M <= 64 && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
-                        (size_t)N * K * 2 < (1ull << 31)) ? skinny_slices(K, N) : 0;
+        const int ks = (M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
+                        (size_t)N * K * 2 < (1ull << 31)) ? skinny_slices(K, N, M) : 0;
         const size_t part = (size_t)ks * (gated ? 2 : 1) * M * N * sizeof(float);
         if (ks <= 0 || (ks > 1 && !part_ensure(part))) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
     }
@@ -2945,9 +2949,9 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     *ks = 0;
     if (!g_inited) return QH_ESTATE;
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
-    if (vec && !g_forced_plan && choose_plan(M, K, N, false, vec) == PLAN_SKINNY && M <= 64 && K % 64 == 0 &&
-        (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31)) {
-        const int s = skinny_slices(K, N);
+    if (vec && !g_forced_plan && choose_plan(M, K, N, false, vec) == PLAN_SKINNY && M <= SKINNY_MMAX &&
+        K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31)) {
+        const int s = skinny_slices(K, N, M);
         if (s > 1 && part_ensure((size_t)s * M * N * sizeof(float))) {
             int rc;
             switch (stream_mt(M)) {

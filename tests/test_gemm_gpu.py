@@ -186,12 +186,13 @@ def test_stream_variants(plan, M, K, N):
 
 @pytest.mark.parametrize("M,K,N", [(64, 2048, 1024), (64, 3072, 1024), (64, 1024, 4096), (5, 1024, 100),
                                    (33, 640, 1000), (17, 64, 77), (64, 256, 151936), (48, 3072, 130),
-                                   (64, 4096, 2048), (16, 2048, 64), (1, 3072, 1024)])
+                                   (64, 4096, 2048), (16, 2048, 64), (1, 3072, 1024),
+                                   (128, 2048, 1024), (96, 3072, 1024), (200, 1024, 4096), (256, 3072, 1000)])
 def test_skinny_kernel(M, K, N):
-    """The skinny kernel for M <= 64 (A slice staged in LDS, K split over
-    blocks and summed in slice order): slice counts from 1 to 16, rows of M
-    and N that leave partial tiles, one slice of 64; repeated calls are
-    bit-identical."""
+    """The skinny kernel (A slice staged in LDS per 64-row slab, K split
+    over blocks and summed in slice order): slice counts from 1 to 16, one
+    to four slabs, rows of M and N that leave partial tiles, one slice of
+    64; repeated calls are bit-identical."""
     a, b = inputs(M, K, N, 4300 + M + K + N)
     abi.force_plan(abi.PLANS["skinny"])
     try:
