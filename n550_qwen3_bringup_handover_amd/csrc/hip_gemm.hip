@@ -2936,12 +2936,15 @@ extern "C" int qh_gemm(float *c, const float *a, const uint16_t *b, int M, int K
     return gemm_common(c, a, b, nullptr, M, K, N, false);
 }
 
-// qh_gemm, except that when the automatic plan is the skinny kernel with more
-// than one K slice, the slices' fp32 sums are left in the split-K workspace
-// ([ks][M][N], *part) for the caller to add in slice order -- the sums
-// k_stream_reduce would form -- instead of a second launch.  Otherwise C is
-// written and *ks = 0.  The partials last until the next call that uses the
-// workspace.
+// qh_gemm, except that when the skinny kernel splits K the slices' fp32 sums
+// are left in the split-K workspace ([ks][M][N], *part) for the caller to add
+// in slice order -- the sums k_stream_reduce would form -- instead of a second
+// launch.  Taken where the automatic plan is the skinny kernel, and for
+// M <= 128, K >= 2048, N <= 2048, where the kernel in 64-row slabs ties or
+// beats the 32x64 tiles once the reduction launch is gone (measured at
+// M = 96 / 128: down 13.2 / 13.2 -> ~9 us, o 9.6 / 9.8 -> ~6.5 us).
+// Otherwise C is written and *ks = 0.  The partials last until the next call
+// that uses the workspace.
 extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M, int K, int N,
                              const float **part, int *ks) {
     if (!part || !ks) return QH_EINVAL;
@@ -2949,8 +2952,10 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     *ks = 0;
     if (!g_inited) return QH_ESTATE;
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
-    if (vec && !g_forced_plan && choose_plan(M, K, N, false, vec) == PLAN_SKINNY && M <= SKINNY_MMAX &&
-        K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31)) {
+    const bool take = vec && !g_forced_plan &&
+                      (choose_plan(M, K, N, false, vec) == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
+    if (take && M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
+        (size_t)N * K * 2 < (1ull << 31)) {
         const int s = skinny_slices(K, N, M);
         if (s > 1 && part_ensure((size_t)s * M * N * sizeof(float))) {
             int rc;

@@ -315,13 +315,19 @@ static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int pos0, int w
     const int dumping = m->dump != NULL;
 #define DUMP(layer, name, ptr, ld, col0, cols) \
     do { if (!rc && dumping) rc = dump_dev(m, (layer), (name), (ptr), nt, (ld), (col0), (cols)); } while (0)
+    /* without dumps, the o and down projections may leave split-K slice sums
+       (qh_gemm_split) that the next residual + RMSNorm adds itself; the last
+       layer's down is written out for the lm_head GEMV's prologue */
+    const float *opart = NULL, *dpart = NULL;
+    int oks = 0, dks = 0;
     for (int l = 0; l < NL; l++) {
         const layer_t *L = &m->L[l];
         if (l == 0) {
             rc = qm_rows_norm(m->x, NULL, m->embed, m->tok_in, V, L->in_norm, m->xb, nt, H, eps);
             DUMP(-1, "embed_out", m->x, H, 0, H);
         } else {
-            rc = qm_rows_norm(m->x, dumping ? NULL : m->dn, NULL, NULL, 0, L->in_norm, m->xb, nt, H, eps);
+            rc = qm_rows_norm_split(m->x, dumping || dks ? NULL : m->dn, NULL, NULL, 0, L->in_norm, m->xb, nt, H,
+                                    eps, dpart, dks);
         }
         DUMP(l, "input_layernorm_out", m->xb, H, 0, H);
         if (!rc) rc = qh_gemm(m->qkv, m->xb, L->wqkv, nt, H, QKV_N);
@@ -332,14 +338,18 @@ static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int pos0, int w
                                    kv->vc + l * kv->layer_stride, L->qn, L->kn, m->rcos, m->rsin,
                                    m->state + 1, nt, kv->max_seq, pos0 + nt, eps);
         DUMP(l, "attn_out", m->att, QW3M_Q_DIM, 0, QW3M_Q_DIM);
-        if (!rc) rc = qh_gemm(m->ob, m->att, L->wo, nt, QW3M_Q_DIM, H);
+        if (!rc) rc = dumping ? qh_gemm(m->ob, m->att, L->wo, nt, QW3M_Q_DIM, H)
+                              : qh_gemm_split(m->ob, m->att, L->wo, nt, QW3M_Q_DIM, H, &opart, &oks);
         DUMP(l, "o_proj_out", m->ob, H, 0, H);
-        if (!rc) rc = qm_rows_norm(m->x, m->ob, NULL, NULL, 0, L->post_norm, m->xb, nt, H, eps);
+        if (!rc) rc = qm_rows_norm_split(m->x, oks ? NULL : m->ob, NULL, NULL, 0, L->post_norm, m->xb, nt, H, eps,
+                                         opart, oks);
         DUMP(l, "x_after_attn_residual", m->x, H, 0, H);
         DUMP(l, "post_attn_norm_out", m->xb, H, 0, H);
         if (!rc) rc = qh_gemm_gate_up_silu(m->hb, m->xb, L->wg, L->wu, nt, H, QW3M_INTER);
         DUMP(l, "silu_gate_mul_up", m->hb, QW3M_INTER, 0, QW3M_INTER);
-        if (!rc) rc = qh_gemm(m->dn, m->hb, L->wd, nt, QW3M_INTER, H);
+        dks = 0;
+        if (!rc) rc = (dumping || l == NL - 1) ? qh_gemm(m->dn, m->hb, L->wd, nt, QW3M_INTER, H)
+                                               : qh_gemm_split(m->dn, m->hb, L->wd, nt, QW3M_INTER, H, &dpart, &dks);
         DUMP(l, "down_proj_out", m->dn, H, 0, H);
         if (!rc && dumping) {
             /* x += down (xb is scratch here; the next layer recomputes it) */
