@@ -2329,6 +2329,12 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
     // stay on the tiles, which hold both weight rows of a block in one pass
     if (!gated && stream_fits(M, K, N) && (M <= 16 || (M <= 32 && N <= 2048))) return PLAN_STREAM;
+    // and for every M <= 64 when N is very wide (the tied lm_head of a decode
+    // batch; measured on MI355X, 64 / 48 / 32 x 1024 x 151936: 76-79 / 70-73 /
+    // 62-63 us against 81-84 / 74-75 / 68-70 on the 64- and 32-row tiles; a
+    // kernel staging A once per CU, each wave streaming its own weight tiles
+    // with no barrier, measured 77-83 us at M = 64 and was not kept)
+    if (!gated && stream_fits(M, K, N) && N >= 32768) return PLAN_STREAM;
     const int bno = gated ? 2 : 1;   // gated tiles produce half as many output columns
     auto blocks = [&](int bm, int bn) {
         return (long)((M + bm - 1) / bm) * (long)((N + bn / bno - 1) / (bn / bno));
@@ -2420,17 +2426,18 @@ static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const 
     return QH_OK;
 }
 
-// M = 1 with K <= 4096.  Rows per wave: as many as keep >= 2048 waves in the
-// grid (8 per CU) and <= 16 weight loads of 16 B in flight per lane.
+// M = 1 with K <= 4096.  Rows per wave: at most 4, as many as keep >= 2048
+// waves in the grid (8 per CU) and <= 16 weight loads of 16 B in flight per
+// lane (measured on MI355X, lm_head 1024 -> 151936: 8 rows per wave stream
+// 6.5 TB/s, 4, 2 or 1 rows 7.1-7.2 TB/s)
 template <bool PRO>
 static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                           int K, int N, bool gated, const GemvPro &pro) {
     const int cpl = (K / 8 + WAVE - 1) / WAVE;
     const int per_row = gated ? 2 * cpl : cpl;
-    int rows = 8;
+    int rows = 4;
     while (rows > 1 && (long)(N + rows - 1) / rows < 2048) rows /= 2;
     while (rows > 1 && rows * per_row > 16) rows /= 2;
-    if (gated && rows > 4) rows = 4;
     switch (rows) {
         case 1: return gated ? launch_gemv1_rows<1, true, PRO>(c, a, b, b2, K, N, cpl, pro)
                              : launch_gemv1_rows<1, false, PRO>(c, a, b, b2, K, N, cpl, pro);
@@ -2438,7 +2445,6 @@ static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uin
                              : launch_gemv1_rows<2, false, PRO>(c, a, b, b2, K, N, cpl, pro);
         case 4: return gated ? launch_gemv1_rows<4, true, PRO>(c, a, b, b2, K, N, cpl, pro)
                              : launch_gemv1_rows<4, false, PRO>(c, a, b, b2, K, N, cpl, pro);
-        case 8: return launch_gemv1_rows<8, false, PRO>(c, a, b, b2, K, N, cpl, pro);
         default: return QH_EINVAL;
     }
 }

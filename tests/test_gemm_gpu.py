@@ -113,6 +113,8 @@ def test_batched_m64(name, K, N):
     """M = 64 (one GPU's share of 64-sequence decode), incl. lm_head 64x1024x151936."""
     M = 64
     a, b = inputs(M, K, N, 0x03550000 + 16 * 5 + sid(name))
+    if name == "lm_head":
+        assert abi.plan(M, K, N) == "stream"      # the weight-streaming kernel for very wide N
     c = run_gemm(a, b, M, K, N, row=(name == "lm_head"))
     cols = None if N <= 4096 else np.unique(np.concatenate(
         [np.arange(256), np.linspace(0, N - 1, 2048).astype(int), np.arange(N - 256, N)]))
