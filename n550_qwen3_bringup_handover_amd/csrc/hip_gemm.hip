@@ -2010,7 +2010,6 @@ static char g_devname[256];
 static hipEvent_t g_ev[64];
 static int g_ev_made[64];
 static int g_forced_plan = 0;
-static int g_no_xcd_map = 0;      // tuning switch: 1 = row-major tile order
 #define QH_MAX_GRAPHS 16
 static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
 // Workspaces replaced while a graph exists: a captured graph keeps the device
@@ -2067,10 +2066,6 @@ extern "C" int qh_init(int device) {
     }
     strncpy(g_devname, prop.gcnArchName, sizeof g_devname - 1);
     if (prop.multiProcessorCount > 0) g_cus = prop.multiProcessorCount;
-    {
-        const char *e = getenv("QWEN3_HIP_NO_XCD_MAP");   // A/B switch for tile order
-        g_no_xcd_map = (e && e[0] == '1') ? 1 : 0;
-    }
     HCHECK(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking), QH_ERUNTIME);
     HCHECK(hipMalloc((void **)&g_am_v, AM_BLOCKS * sizeof(float)), QH_ENOMEM);
     HCHECK(hipMalloc((void **)&g_am_i, AM_BLOCKS * sizeof(int)), QH_ENOMEM);
@@ -2520,15 +2515,12 @@ static long make_map(TileMap &map, int M, int N, int K, int BM, int BN, int BNO)
     if (tiles > 0x7FFFFFFFL) return -1;
     map.rm = 0;
     map.rn = 0;
-    if (!g_no_xcd_map) {
-        double best = 0.0;
-        for (int rm = 1; rm <= 8; rm *= 2) {
-            const int rn = 8 / rm;
-            if (map.MT % rm || map.NT % rn) continue;
-            const double slab = (double)(map.MT / rm) * BM * K * 4.0 +
-                                (double)(map.NT / rn) * BN * K * 2.0;
-            if (map.rm == 0 || slab < best) { best = slab; map.rm = rm; map.rn = rn; }
-        }
+    double best = 0.0;
+    for (int rm = 1; rm <= 8; rm *= 2) {
+        const int rn = 8 / rm;
+        if (map.MT % rm || map.NT % rn) continue;
+        const double slab = (double)(map.MT / rm) * BM * K * 4.0 + (double)(map.NT / rn) * BN * K * 2.0;
+        if (map.rm == 0 || slab < best) { best = slab; map.rm = rm; map.rn = rn; }
     }
     return tiles;
 }
