@@ -2421,17 +2421,19 @@ static int launch_gemv1_rows(float *c, const float *a, const uint16_t *b, const 
     return QH_OK;
 }
 
-// M = 1 with K <= 4096.  Rows per wave: at most 4, as many as keep >= 2048
-// waves in the grid (8 per CU) and <= 16 weight loads of 16 B in flight per
-// lane (measured on MI355X, lm_head 1024 -> 151936: 8 rows per wave stream
-// 6.5 TB/s, 4, 2 or 1 rows 7.1-7.2 TB/s)
+// M = 1 with K <= 4096.  Rows per wave: at most 4, as many as keep >= 4096
+// waves in the grid (16 per CU) and <= 16 weight loads of 16 B in flight per
+// lane (measured on MI355X: lm_head 1024 -> 151936 streams 6.5 TB/s with 8
+// rows per wave, 7.1-7.2 TB/s with 4, 2 or 1; q|k|v 1024 -> 4096 at one row
+// per wave instead of two: the 113-launch decode step 2,486-2,492 ->
+// 2,504 tok/s)
 template <bool PRO>
 static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                           int K, int N, bool gated, const GemvPro &pro) {
     const int cpl = (K / 8 + WAVE - 1) / WAVE;
     const int per_row = gated ? 2 * cpl : cpl;
     int rows = 4;
-    while (rows > 1 && (long)(N + rows - 1) / rows < 2048) rows /= 2;
+    while (rows > 1 && (long)(N + rows - 1) / rows < 4096) rows /= 2;
     while (rows > 1 && rows * per_row > 16) rows /= 2;
     switch (rows) {
         case 1: return gated ? launch_gemv1_rows<1, true, PRO>(c, a, b, b2, K, N, cpl, pro)
