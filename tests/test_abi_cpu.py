@@ -39,6 +39,26 @@ def test_kernel_name():
     assert abi.kernel_name() == "hip-gfx950"
 
 
+H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
+
+
+@pytest.mark.parametrize("M,K,N,gated,plan", [
+    (1, H, Q + 2 * KV, False, "gemv"), (1, Q, H, False, "gemv"), (1, H, V, False, "gemv"),
+    (16, H, I, False, "stream"),                                  # gate_proj at M = 16
+    (64, H, V, False, "stream"),                                  # lm_head of a 64-sequence batch
+    (32, H, V, False, "stream"),
+    (64, Q, H, False, "skinny"), (64, I, H, False, "skinny"),     # o, down at M = 64
+    (64, H, Q + 2 * KV, False, "pipe32x64k128s4"), (64, H, I, True, "pipe32x64k128s4"),
+    (512, H, Q + 2 * KV, False, "xl64x128"), (512, H, I, True, "xl128x128"),
+    (512, H, Q, False, "pipe32x64k64s4"), (512, I, H, False, "pipe32x64k128s4"),
+    (8, 33, 128, False, "mfma64x64-scalar"),                      # K % 8 != 0: element-wise loads
+])
+def test_automatic_plan_table(M, K, N, gated, plan):
+    """The automatic kernel choice for the Qwen3-0.6B shapes is host logic
+    (measured on MI355X and fixed in the library); it needs no device."""
+    assert abi.plan(M, K, N, gated) == plan
+
+
 @pytest.mark.parametrize("layout,tn,tk,ok", [
     (0, 0, 0, True), (0, 128, 32, True),          # ROW ignores tile sizes (qwen3.c:67-73)
     (1, 128, 32, True),                           # the AME tile (kernels.h:20-23)
