@@ -17,6 +17,7 @@
 // The chunk attention keeps its tokens' scores in LDS, sized by the chunk's
 // context: up to 69 KB at QM_MAX_SEQ with one token per block, above the
 // default 64 KB limit, which it raises once.
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -318,34 +319,36 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
     __syncthreads();
 
     // out_r[d] = sum_t p[r][t] v_t[d]: wave w takes t = w, w+4, ...; lane l
-    // owns d = 2l, 2l+1 of every row; each V row serves all R rows
+    // owns d = 2l, 2l+1 of every row; each V row serves all R rows.  Passes
+    // of 16, then 8, 4 and 1 rows in flight per lane (each pass one L2 round
+    // trip; measured on MI355X against one 8-row pass and the 1-row tail:
+    // 64 x 2014-token batch prefill 2.71 -> 2.60 s), always adding in
+    // ascending t
     f32x2 o[R];
 #pragma unroll
     for (int r = 0; r < R; r++) o[r] = f32x2{0.f, 0.f};
     const f32x2 *vcache = reinterpret_cast<const f32x2 *>(vc + (size_t)g * max_seq * HD) + lane;
     int t = wave;
-    for (; t + 4 * 7 < ctxmax; t += 4 * 8) {   // 8 loads in flight per lane
-        f32x2 v[8];
+    auto vpass = [&](auto UC) {
+        constexpr int U = decltype(UC)::value;
+        for (; t + 4 * (U - 1) < ctxmax; t += 4 * U) {
+            f32x2 v[U];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = vcache[(size_t)(t + 4 * u) * (HD / 2)];
+            for (int u = 0; u < U; u++) v[u] = vcache[(size_t)(t + 4 * u) * (HD / 2)];
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+            for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float pw = p[r * ldp + t + 4 * u];
-                o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v[u].x));
-                o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v[u].y));
-            }
-    }
-    for (; t < ctxmax; t += 4) {
-        const f32x2 v = vcache[(size_t)t * (HD / 2)];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float pw = p[r * ldp + t];
-            o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v.x));
-            o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v.y));
+                for (int r = 0; r < R; r++) {
+                    const float pw = p[r * ldp + t + 4 * u];
+                    o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v[u].x));
+                    o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v[u].y));
+                }
         }
-    }
+    };
+    vpass(std::integral_constant<int, 16>{});
+    vpass(std::integral_constant<int, 8>{});
+    vpass(std::integral_constant<int, 4>{});
+    vpass(std::integral_constant<int, 1>{});
 #pragma unroll
     for (int r = 0; r < R; r++) {
         red[(wave * R + r) * HD + 2 * lane] = o[r].x;
