@@ -347,6 +347,10 @@ class Gpu:
     def plan(self, M, K, N, gated=False):
         return self.L.qwen3_hip_plan(M, K, N, int(gated)).decode()
 
+    def last_plan(self):
+        """the plan the last GEMM call launched (after any fall-back)"""
+        return self.L.qwen3_hip_last_plan().decode()
+
 
 def build_decode_model(g):
     """device weights in the QW3M tensor order: q|k|v and gate|up contiguous"""
@@ -411,7 +415,11 @@ def time_launches(g, launch, reps):
 
 def time_launches_graph(g, launch, reps):
     """average time per launch of `reps` back-to-back launches replayed from
-    one captured graph (events around the replay, on the library stream)"""
+    one captured graph (events around the replay, on the library stream).
+    One eager launch first: a workspace the call needs is grown there, since
+    the library grows none during capture."""
+    launch(0)
+    g.sync()
     g.rt.check(g.L.qwen3_hip_capture_begin(), "capture_begin")
     for r in range(reps):
         launch(r)
@@ -476,7 +484,7 @@ def gemm_entry(g, M, K, N, gated, a, c, w, wrot=None, reps=32):
         byts = 2 * N * K + 4 * M * K + 4 * M * N
     ms = time_launches_graph(g, fn, reps)
     tf = flops / (ms * 1e-3) / 1e12
-    return {"M": M, "K": K, "N": N, "gated": gated, "kernel": g.plan(M, K, N, gated),
+    return {"M": M, "K": K, "N": N, "gated": gated, "kernel": g.last_plan(),
             "us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
             "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
             "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
@@ -625,6 +633,9 @@ def main():
     wall = time.perf_counter() - t0
     ms_step = g.elapsed(60, 61) / args.steps
     value = 1000.0 / ms_step
+    if not args.no_graph:
+        # no graph outlives its section: a workspace grown later is then freed at once
+        g.rt.check(g.L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
 
     kclasses = None if args.no_extras else kernel_classes(g, layers, emb, act)
     roofline = None
@@ -664,6 +675,8 @@ def main():
                    "M": 1, "layers": LAYERS, "step_bytes": STEP_BYTES,
                    "launches_per_step": 4 * LAYERS + 1, "hip_graph": not args.no_graph},
         "hbm_GBps_step": round(STEP_BYTES / (ms_step * 1e-3) / 1e9, 1),
+        # the full Qwen3-0.6B forward (128-token prompt + 128 greedy steps, batch 1): decode tok/s
+        "model_decode_tok_s": model["decode_tok_s"] if model else None,
         "wall_s": round(wall, 3),
         "roofline": roofline,
         "cpu_baseline": cpu,

@@ -17,15 +17,18 @@
  * Host-pointer entry points are synchronous: on return C is complete in host
  * memory (SRC/kernels_ame.c:426-444 gives the same guarantee).
  *
- * Weights: B is read-only for as long as the library may use it
- * (SRC/qwen3.h:203-207).  Device copies are made on first use and reused:
+ * Weights: B is read-only during a call (SRC/qwen3.h:203-207).
  *   - B inside a range given to qwen3_hip_map_weights() is served from one
  *     device copy of that whole range (the model blob), at zero per-call cost;
- *   - any other B is cached by address and verified on each call against a
- *     sampled fingerprint of its contents (shape, first/last 256 bytes and
- *     512 sampled 8-byte words); a changed buffer is re-uploaded.  A buffer changed
- *     only outside the sampled words is NOT detected: call
- *     qwen3_hip_forget_weights() after modifying a weight buffer in place.
+ *     the range must stay unchanged until it is unmapped;
+ *   - any other B is copied to the device on every call (default), so, as
+ *     with the reference kernels, a caller may change B between calls;
+ *   - opt-in (qwen3_hip_set_weight_cache(1) or QWEN3_HIP_WEIGHT_CACHE=1):
+ *     other B are instead cached by address and verified on each call against
+ *     a sampled fingerprint of their contents (shape, first/last 256 bytes and
+ *     512 sampled 8-byte words); a buffer changed only outside the sampled
+ *     words is NOT detected, so call qwen3_hip_forget_weights() after
+ *     modifying a cached weight buffer in place.
  *
  * Errors: the reference ABI is void, so a failure inside qwen3_gemm /
  * qwen3_gemm_row / qwen3_gemm_gate_up_silu prints one line to stderr and
@@ -112,6 +115,10 @@ int qwen3_hip_map_weights(const void *blob, size_t size);
 int qwen3_hip_unmap_weights(const void *blob);
 /* Drop the cached device copy for B (or every unmapped copy if b == NULL). */
 void qwen3_hip_forget_weights(const void *b);
+/* 1 = cache unmapped B by address (sampled fingerprint, see above); 0 (the
+ * default, unless QWEN3_HIP_WEIGHT_CACHE=1) = copy unmapped B on every call.
+ * Turning it off drops the cached copies. */
+void qwen3_hip_set_weight_cache(int on);
 /* Bytes of device memory held for weights (mapped ranges + cached copies). */
 size_t qwen3_hip_weight_bytes(void);
 
@@ -167,6 +174,8 @@ int qwen3_hip_timer_elapsed_ms(int a, int b, float *ms);
  * to force one (0 = automatic) */
 const char *qwen3_hip_plan(int M, int K, int N, int gated);
 int qwen3_hip_force_plan(int plan_id);
+/* the plan the last GEMM call launched (after any fall-back) */
+const char *qwen3_hip_last_plan(void);
 /* name of the device in use (gfx arch string), "" before init */
 const char *qwen3_hip_device_name(void);
 

@@ -171,16 +171,17 @@ def force_plan(plan_id):
     check(runtime.lib().qwen3_hip_force_plan(plan_id), "qwen3_hip_force_plan")
 
 
+# plan ids of csrc/hip_gemm.hip (qwen3_hip_force_plan); checked against the
+# library's own names by tests/test_abi_cpu.py
 PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4,
          "mfma32x128": 5, "mfma16x64": 6, "mfma64x64-scalar": 7,
-         "ring32x64k128s4": 8, "ring64x64k64s4": 9, "ring64x64k64s6": 10, "ring64x64k128s3": 11,
-         "ring64x128k64s4": 12, "ring128x128k64s3": 13, "ring128x64k64s3": 14,
-         "ring32x64k64s6": 15, "ring64x64k32s6": 16, "ring32x64k32s4": 17,
-         "pipe32x64k128s3": 18, "pipe32x64k128s4": 19, "pipe64x64k128s3": 20, "pipe64x64k64s4": 21,
-         "pipe64x128k64s4": 22, "pipe128x128k64s3": 23, "pipe128x64k64s3": 24, "pipe32x64k64s4": 25,
-         "pipe64x64k64s3": 26, "xl128x256": 27, "xl256x256": 28, "xl256x128": 29, "xl128x128": 30, "xl128x256k32": 31, "xl256x128k32": 32,
-         "xb256x256": 33, "xb256x256k32": 34, "xb128x256": 35, "xb256x128": 36, "xb128x128": 37,
-         "xl64x256": 38, "xl64x128": 39,
-         "xl256x256s1": 40, "xb256x256s1": 41,
-         "stream": 42, "stream-ks1": 43, "stream-ks2": 44, "stream-ks4": 45, "stream-ks8": 46,
-         "xl128x128sk": 47, "skinny": 48}
+         "pipe32x64k128s4": 8, "pipe32x64k64s4": 9, "pipe64x64k64s3": 10,
+         "xl128x128": 11, "xl256x256": 12, "xl64x128": 13,
+         "xb256x256k32": 14, "xb128x128": 15, "xb256x256s1": 16,
+         "stream": 17, "stream-ks1": 18, "stream-ks2": 19, "stream-ks4": 20, "stream-ks8": 21,
+         "skinny": 22}
+
+
+def last_plan():
+    """the plan the last GEMM call launched (after any fall-back)"""
+    return runtime.lib().qwen3_hip_last_plan().decode()

@@ -804,182 +804,14 @@ struct RingCfg {
     static_assert(STAGES >= 2 && (STAGES - 2) * LPS <= 63, "vmcnt range");
 };
 
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_ring(float *__restrict__ c,
-                                                          const float *__restrict__ a,
-                                                          const uint16_t *__restrict__ b,
-                                                          const uint16_t *__restrict__ b2,
-                                                          int M, int K, int N, TileMap map) {
-    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_>;
-    extern __shared__ __align__(16) unsigned char smem[];
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    tile_of(blockIdx.x, map, tm, tn);
-    const int m0 = tm * BM;
-    const int n0 = tn * R::BNO;
-    const int nk = K / R::BK;
-
-    // per-lane global source rows/chunks for this wave's copies (fixed over k)
-    const float *asrc[R::A_DMA];
-    const uint16_t *bsrc[R::B_DMA];
-#pragma unroll
-    for (int i = 0; i < R::A_DMA; i++) {
-        const int seg = wave * R::A_DMA + i;            // 64 / CA rows per 1 KB
-        const int r = seg * (64 / R::CA) + lane / R::CA;
-        const int cl = (lane % R::CA) ^ swz<R::CA>(r);
-        const int gm = min(m0 + r, M - 1);              // rows >= M: any valid row
-        asrc[i] = a + (size_t)gm * K + cl * 4;
-    }
-#pragma unroll
-    for (int i = 0; i < R::B_DMA; i++) {
-        const int seg = wave * R::B_DMA + i;            // 64 / CB rows per 1 KB
-        const int r = seg * (64 / R::CB) + lane / R::CB;
-        const int cl = (lane % R::CB) ^ swz<R::CB>(r);
-        const uint16_t *src = b;
-        int gn;
-        if constexpr (GATED) {
-            const bool up = r >= R::BNO;
-            gn = n0 + (up ? r - R::BNO : r);
-            src = up ? b2 : b;
-        } else {
-            gn = n0 + r;
-        }
-        gn = min(gn, N - 1);                            // cols >= N: any valid row
-        bsrc[i] = src + (size_t)gn * K + cl * 8;
-    }
-
-    auto issue = [&](int step) {
-        unsigned char *slot = smem + (step % STAGES) * R::STAGE;
-        const int k0 = step * R::BK;
-#pragma unroll
-        for (int i = 0; i < R::A_DMA; i++)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(asrc[i] + k0),
-                (__attribute__((address_space(3))) void *)(slot + (wave * R::A_DMA + i) * 1024),
-                16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < R::B_DMA; i++)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(bsrc[i] + k0),
-                (__attribute__((address_space(3))) void *)(slot + R::A_BYTES + (wave * R::B_DMA + i) * 1024),
-                16, 0, 0);
-    };
-
-    f32x4 acc[R::TM][R::TN];
-#pragma unroll
-    for (int i = 0; i < R::TM; i++)
-#pragma unroll
-        for (int j = 0; j < R::TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int pro = nk < STAGES - 1 ? nk : STAGES - 1;
-    for (int s = 0; s < pro; s++) issue(s);
-
-    const int lrow = lane & 15, lgrp = lane >> 4;
-    for (int it = 0; it < nk; it++) {
-        // wait for this wave's copies of step `it`: the later steps issued so
-        // far may stay in flight
-        const int later = min(nk - 1 - it, STAGES - 2);
-        // (cases above STAGES-2 are unreachable; their counts are clamped so
-        // every immediate stays a valid encoding)
-        switch (later) {
-            case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
-            case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
-            case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
-            case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
-            case 4: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
-            case 5: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(5))); break;
-            default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(6))); break;
-        }
-        // all waves' copies of `it` have landed, and all waves are done with
-        // step it-1, whose slot the next copy reuses
-        __builtin_amdgcn_s_barrier();
-        if (it + STAGES - 1 < nk) issue(it + STAGES - 1);
-
-        const unsigned char *slot = smem + (it % STAGES) * R::STAGE;
-        // every fragment read of the stage first (raw fp32 for A), then the
-        // conversions and MFMAs, so LDS latency overlaps across k-steps
-        u32x4 araw[R::KS][R::TM][2], bfr[R::KS][R::TN];
-#pragma unroll
-        for (int t = 0; t < R::KS; t++) {
-#pragma unroll
-            for (int i = 0; i < R::TM; i++) {
-                const int row = wm * R::WTM + 16 * i + lrow;
-                const int sw = swz<R::CA>(row);
-                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + row * (R::CA * 16));
-                araw[t][i][0] = rowp[(8 * t + 2 * lgrp) ^ sw];
-                araw[t][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ sw];
-            }
-#pragma unroll
-            for (int j = 0; j < R::TN; j++) {
-                const int row = b_tile_row<BN, WN, R::TN, GATED>(wn, j) + lrow;
-                const u32x4 *rowp =
-                    reinterpret_cast<const u32x4 *>(slot + R::A_BYTES + row * (R::CB * 16));
-                bfr[t][j] = rowp[(4 * t + lgrp) ^ swz<R::CB>(row)];
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < R::KS; t++) {
-            bf16x8 af[R::TM];
-#pragma unroll
-            for (int i = 0; i < R::TM; i++) {
-                const f32x4 x0 = __builtin_bit_cast(f32x4, araw[t][i][0]);
-                const f32x4 x1 = __builtin_bit_cast(f32x4, araw[t][i][1]);
-                u32x4 w;
-                w.x = pack_bf16x2(x0.x, x0.y);
-                w.y = pack_bf16x2(x0.z, x0.w);
-                w.z = pack_bf16x2(x1.x, x1.y);
-                w.w = pack_bf16x2(x1.z, x1.w);
-                af[i] = __builtin_bit_cast(bf16x8, w);
-            }
-#pragma unroll
-            for (int i = 0; i < R::TM; i++)
-#pragma unroll
-                for (int j = 0; j < R::TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        af[i], __builtin_bit_cast(bf16x8, bfr[t][j]), acc[i][j], 0, 0, 0);
-        }
-    }
-
-    // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
-#pragma unroll
-    for (int i = 0; i < R::TM; i++) {
-        const int rbase = m0 + wm * R::WTM + 16 * i + 4 * lgrp;
-        if constexpr (!GATED) {
-#pragma unroll
-            for (int j = 0; j < R::TN; j++) {
-                const int col = n0 + wn * R::WTN + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (rbase + r < M) c[(size_t)(rbase + r) * N + col] = acc[i][j][r];
-                }
-            }
-        } else {
-            constexpr int TNO = R::TN / 2;
-#pragma unroll
-            for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (R::BNO / WN) + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (rbase + r < M)
-                            c[(size_t)(rbase + r) * N + col] = silu_mul(acc[i][j][r], acc[i][j + TNO][r]);
-                }
-            }
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
 // Software-pipelined ring GEMM
 // ---------------------------------------------------------------------------
 template <int V> struct IC { static constexpr int value = V; };
 
-// Same LDS ring and copies as k_gemm_ring, but the phases of consecutive
-// stages overlap inside each wave: while the MFMAs of stage `it` run on
+// A and B stream straight into an LDS ring of STAGES slots with
+// global_load_lds (16-byte copies, explicit vmcnt waits, one barrier per
+// stage), and the phases of consecutive stages overlap inside each wave: while the MFMAs of stage `it` run on
 // fragments already in registers, the LDS reads of stage it+1 fill a second
 // register set and the copies of stage it+STAGES-1 are in flight.  Per stage:
 //   wait (own copies of it+1) -> barrier -> issue copies of it+STAGES-1 ->
@@ -2012,13 +1844,13 @@ static int g_ev_made[64];
 static int g_forced_plan = 0;
 #define QH_MAX_GRAPHS 16
 static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
+static void *g_graph_ws[QH_MAX_GRAPHS][2];   // library workspaces each graph uses (abf, part)
 // Workspaces replaced while a graph exists: a captured graph keeps the device
 // addresses it was recorded with, so a grown workspace's old buffer stays
 // allocated until no graph is left (or the library shuts down).
 #define QH_MAX_RETIRED 64
 static void *g_retired[QH_MAX_RETIRED];
 static int g_n_retired = 0;
-static bool any_graph(void);
 static void free_retired(void);
 static int g_capturing = 0;
 static float *g_am_v = nullptr;   // argmax partials (allocated at init)
@@ -2083,8 +1915,10 @@ extern "C" int qh_init(int device) {
 extern "C" void qh_shutdown(void) {
     if (!g_inited) return;
     (void)hipStreamSynchronize(g_stream);
-    for (int i = 0; i < QH_MAX_GRAPHS; i++)
+    for (int i = 0; i < QH_MAX_GRAPHS; i++) {
         if (g_graph_exec[i]) { (void)hipGraphExecDestroy(g_graph_exec[i]); g_graph_exec[i] = nullptr; }
+        g_graph_ws[i][0] = g_graph_ws[i][1] = nullptr;
+    }
     free_retired();
     for (int i = 0; i < 64; i++)
         if (g_ev_made[i]) { (void)hipEventDestroy(g_ev[i]); g_ev_made[i] = 0; }
@@ -2179,82 +2013,49 @@ extern "C" int qh_timer_elapsed_ms(int a, int b, float *ms) {
 }
 
 // ---- plans ------------------------------------------------------------------
+// Every plan below is one that choose_plan / choose_bf16a_plan returns, or the
+// fall-back (mfma64x64) taken when a plan's alignment or size conditions fail.
 enum {
     PLAN_AUTO = 0,
-    PLAN_GEMV = 1,
-    PLAN_T128x128 = 2,
+    PLAN_GEMV = 1,             // M <= 4: HBM-streaming GEMV
+    PLAN_T128x128 = 2,         // register-staged 16x16x32 MFMA tiles (K % 8 == 0)
     PLAN_T64x128 = 3,
-    PLAN_T64x64 = 4,
+    PLAN_T64x64 = 4,           // the fall-back
     PLAN_T32x128 = 5,
     PLAN_T16x64 = 6,
-    PLAN_SCALAR64 = 7,     // MFMA 64x64 with element-wise loads (any K, any alignment)
-    // ring-pipelined (K % BK == 0): tile, k per stage, LDS stages
-    PLAN_R32x64k128s4 = 8,
-    PLAN_R64x64k64s4 = 9,
-    PLAN_R64x64k64s6 = 10,
-    PLAN_R64x64k128s3 = 11,
-    PLAN_R64x128k64s4 = 12,
-    PLAN_R128x128k64s3 = 13,
-    PLAN_R128x64k64s3 = 14,
-    PLAN_R32x64k64s6 = 15,
-    PLAN_R64x64k32s6 = 16,
-    PLAN_R32x64k32s4 = 17,
-    // software-pipelined ring (K % BK == 0)
-    PLAN_P32x64k128s3 = 18,
-    PLAN_P32x64k128s4 = 19,
-    PLAN_P64x64k128s3 = 20,
-    PLAN_P64x64k64s4 = 21,
-    PLAN_P64x128k64s4 = 22,
-    PLAN_P128x128k64s3 = 23,
-    PLAN_P128x64k64s3 = 24,
-    PLAN_P32x64k64s4 = 25,
-    PLAN_P64x64k64s3 = 26,
-    // large tiles, 32x32x16 MFMA (K % BK == 0)
-    PLAN_X128x256 = 27,        // BK 64
-    PLAN_X256x256 = 28,        // BK 32
-    PLAN_X256x128 = 29,        // BK 64
-    PLAN_X128x128 = 30,        // BK 64
-    PLAN_X128x256k32 = 31,
-    PLAN_X256x128k32 = 32,
-    // A converted to bf16 by one extra pass, then bf16 x bf16 large tiles
-    PLAN_XB256x256 = 33,       // BK 64
-    PLAN_XB256x256k32 = 34,
-    PLAN_XB128x256 = 35,       // BK 64
-    PLAN_XB256x128 = 36,       // BK 64
-    PLAN_XB128x128 = 37,       // BK 64
-    // 64-row tiles (batched decode, M <= 64), BK 64
-    PLAN_X64x256 = 38,
-    PLAN_X64x128 = 39,
-    // one register set, BK 64
-    PLAN_X256x256s1 = 40,
-    PLAN_XB256x256s1 = 41,
+    PLAN_SCALAR64 = 7,         // MFMA 64x64 with element-wise loads (any K, any alignment)
+    // software-pipelined LDS ring (K % BK == 0): tile, k per stage, LDS stages
+    PLAN_P32x64k128s4 = 8,
+    PLAN_P32x64k64s4 = 9,
+    PLAN_P64x64k64s3 = 10,
+    // large tiles, 32x32x16 MFMA, fp32 A rounded on the load path (K % BK == 0)
+    PLAN_X128x128 = 11,        // BK 64
+    PLAN_X256x256 = 12,        // BK 32
+    PLAN_X64x128 = 13,         // BK 64
+    // A rounded to bf16 by one extra pass into the workspace, then bf16 x bf16
+    PLAN_XB256x256k32 = 14,
+    PLAN_XB128x128 = 15,       // BK 64
+    PLAN_XB256x256s1 = 16,     // BK 64, one register set
     // weight-streaming MFMA GEMM for M <= 64 (K % 256 == 0): KS chosen per
     // shape, or forced (wave k range 32*KS; K / (256*KS) block slices)
-    PLAN_STREAM = 42,
-    PLAN_STREAM_KS1 = 43,
-    PLAN_STREAM_KS2 = 44,
-    PLAN_STREAM_KS4 = 45,
-    PLAN_STREAM_KS8 = 46,
-    // 128x128 large tiles with K split over blocks when the tiles leave CUs idle
-    PLAN_X128x128SK = 47,
+    PLAN_STREAM = 17,
+    PLAN_STREAM_KS1 = 18,
+    PLAN_STREAM_KS2 = 19,
+    PLAN_STREAM_KS4 = 20,
+    PLAN_STREAM_KS8 = 21,
     // skinny M <= 64: A slice staged in LDS, K split over blocks (K % 64 == 0)
-    PLAN_SKINNY = 48,
-    PLAN_COUNT = 49
+    PLAN_SKINNY = 22,
+    PLAN_COUNT = 23
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
-    "ring32x64k128s4", "ring64x64k64s4", "ring64x64k64s6", "ring64x64k128s3", "ring64x128k64s4",
-    "ring128x128k64s3", "ring128x64k64s3", "ring32x64k64s6", "ring64x64k32s6", "ring32x64k32s4",
-    "pipe32x64k128s3", "pipe32x64k128s4", "pipe64x64k128s3", "pipe64x64k64s4", "pipe64x128k64s4",
-    "pipe128x128k64s3", "pipe128x64k64s3", "pipe32x64k64s4", "pipe64x64k64s3",
-    "xl128x256", "xl256x256", "xl256x128", "xl128x128", "xl128x256k32", "xl256x128k32",
-    "xb256x256", "xb256x256k32", "xb128x256", "xb256x128", "xb128x128", "xl64x256", "xl64x128",
-    "xl256x256s1", "xb256x256s1", "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "xl128x128sk", "skinny"};
-static inline bool is_ring_plan(int p) { return p >= PLAN_R32x64k128s4 && p <= PLAN_P64x64k64s3; }
-static inline bool is_xl_plan(int p) { return (p >= PLAN_X128x256 && p <= PLAN_XB256x256s1) || p == PLAN_X128x128SK; }
-static inline bool is_xb_plan(int p) {
-    return (p >= PLAN_XB256x256 && p <= PLAN_XB128x128) || p == PLAN_XB256x256s1;
-}
+    "pipe32x64k128s4", "pipe32x64k64s4", "pipe64x64k64s3",
+    "xl128x128", "xl256x256", "xl64x128",
+    "xb256x256k32", "xb128x128", "xb256x256s1",
+    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny"};
+static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
+static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
+static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
 static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
 static inline int stream_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // the stream kernel's limits: M <= 64, whole 256-deep block slices, byte
@@ -2281,18 +2082,8 @@ static int stream_ks(int M, int K, int N, int cus) {
     }
     return smallest;
 }
-static inline int xl_bk(int p) {
-    return (p == PLAN_X256x256 || p == PLAN_X128x256k32 || p == PLAN_X256x128k32 ||
-            p == PLAN_XB256x256k32) ? 32 : 64;
-}
-static inline int ring_bk(int p) {
-    switch (p) {
-        case PLAN_R32x64k128s4: case PLAN_R64x64k128s3:
-        case PLAN_P32x64k128s3: case PLAN_P32x64k128s4: case PLAN_P64x64k128s3: return 128;
-        case PLAN_R64x64k32s6: case PLAN_R32x64k32s4: return 32;
-        default: return 64;
-    }
-}
+static inline int xl_bk(int p) { return (p == PLAN_X256x256 || p == PLAN_XB256x256k32) ? 32 : 64; }
+static inline int pipe_bk(int p) { return p == PLAN_P32x64k128s4 ? 128 : 64; }
 
 static inline bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
@@ -2359,9 +2150,8 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
                 if (K <= 1024 && blocks(64, 128) >= 256) return PLAN_X64x128;
                 if (blocks(64, 64) <= 512) return PLAN_P64x64k64s3;
             }
-            if (!gated && blocks(256, 256) >= 256)
-                return (size_t)M * K <= g_abf_elems ? PLAN_XB256x256s1 : PLAN_X256x256;
-            if (gated && M >= 2048 && (size_t)M * K <= g_abf_elems) return PLAN_XB128x128;
+            if (!gated && blocks(256, 256) >= 256) return PLAN_XB256x256s1;
+            if (gated && M >= 2048) return PLAN_XB128x128;
             return PLAN_X128x128;
         }
         if (M > 128 && blocks(128, 128) >= 128)
@@ -2539,28 +2329,6 @@ static int launch_tile(float *c, const float *a, const uint16_t *b, const uint16
     return QH_OK;
 }
 
-// requires K % 32 == 0 and 16-byte aligned a, b, b2 (checked by the caller)
-// requires K % BK == 0 and 16-byte aligned a, b, b2 (checked by the caller)
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32>
-static int launch_ring(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
-                       int M, int K, int N) {
-    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK>;
-    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
-    if (!attr_set) {
-        HCHECK(hipFuncSetAttribute((const void *)k_gemm_ring<BM, BN, WM, WN, STAGES, GATED, BK>,
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS),
-               QH_ELAUNCH);
-        attr_set = true;
-    }
-    TileMap map;
-    const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
-    if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_ring<BM, BN, WM, WN, STAGES, GATED, BK>), dim3((unsigned)tiles),
-                       dim3(NTHREADS), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
-    HCHECK(hipGetLastError(), QH_ELAUNCH);
-    return QH_OK;
-}
-
 // requires K % BK == 0 and 16-byte aligned a, b, b2 (checked by the caller)
 template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32>
 static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
@@ -2582,18 +2350,46 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     return QH_OK;
 }
 
-static bool any_graph(void) {
+// ---- workspace ----------------------------------------------------------------
+// Device memory beyond a GEMM's inputs and outputs: the bf16 copy of A (xb
+// plans) or the fp32 slice sums of a K split (skinny, stream).  No plan uses
+// both at once.  The library's own pair (g_abf, g_part) grows on demand
+// outside graph capture; a fixed workspace (`grow` false) does not.
+struct Ws {
+    uint16_t *abf;
+    size_t abf_elems;
+    float *part;
+    size_t part_bytes;
+    bool grow;
+};
+
+// A captured graph keeps the device addresses it was recorded with.  Each
+// graph slot lists the library workspace buffers its kernels use; a buffer
+// replaced by a larger one is freed at once when no live graph lists it, and
+// otherwise parked in g_retired until the last graph listing it is destroyed.
+static bool g_cap_abf = false, g_cap_part = false;   // used by the graph being captured
+
+static bool graph_holds(const void *p) {
     for (int i = 0; i < QH_MAX_GRAPHS; i++)
-        if (g_graph_exec[i]) return true;
+        if (g_graph_exec[i] && (g_graph_ws[i][0] == p || g_graph_ws[i][1] == p)) return true;
     return false;
 }
 
-// drop a workspace buffer that has been replaced: freed at once when no graph
-// can hold its address, else kept until the last graph is destroyed; false
-// (nothing changed) when the retired list is full
+// a library workspace about to be written by a launch on the stream
+static uint16_t *use_abf(const Ws &ws) {
+    if (ws.grow && g_capturing) g_cap_abf = true;
+    return ws.abf;
+}
+static float *use_part(const Ws &ws) {
+    if (ws.grow && g_capturing) g_cap_part = true;
+    return ws.part;
+}
+
+// drop a replaced workspace buffer: freed now unless a live graph uses it;
+// false (nothing changed) when it must be parked and the list is full
 static bool retire_buffer(void *p) {
     if (!p) return true;
-    if (!any_graph()) {
+    if (!graph_holds(p)) {
         (void)hipStreamSynchronize(g_stream);   // the old buffer may still be read
         (void)hipFree(p);
         return true;
@@ -2603,55 +2399,67 @@ static bool retire_buffer(void *p) {
     return true;
 }
 
+// free every parked buffer that no live graph uses any more
 static void free_retired(void) {
-    if (g_n_retired == 0) return;
-    (void)hipStreamSynchronize(g_stream);
-    for (int i = 0; i < g_n_retired; i++) (void)hipFree(g_retired[i]);
-    g_n_retired = 0;
+    int j = 0;
+    bool synced = false;
+    for (int i = 0; i < g_n_retired; i++) {
+        if (graph_holds(g_retired[i])) {
+            g_retired[j++] = g_retired[i];
+            continue;
+        }
+        if (!synced) { (void)hipStreamSynchronize(g_stream); synced = true; }
+        (void)hipFree(g_retired[i]);
+    }
+    g_n_retired = j;
 }
 
-// the split-K workspace holds at least `bytes` (grows only outside capture)
-static bool part_ensure(size_t bytes) {
+// ws holds at least `bytes` of slice sums: the library's grows (outside
+// capture only), a fixed workspace does not
+static bool part_ensure(Ws &ws, size_t bytes) {
     if (bytes >= (1ull << 31)) return false;           // the reduction's 32-bit offsets
-    if (bytes <= g_part_bytes) return true;
-    if (g_capturing) return false;
-    if (any_graph() && g_n_retired >= QH_MAX_RETIRED) return false;
+    if (bytes <= ws.part_bytes) return true;
+    if (!ws.grow || g_capturing) return false;
+    if (graph_holds(g_part) && g_n_retired >= QH_MAX_RETIRED) return false;
     float *p = nullptr;
     if (hipMalloc((void **)&p, bytes) != hipSuccess) { (void)hipGetLastError(); return false; }
     (void)retire_buffer(g_part);               // cannot fail: room checked above
     g_part = p;
     g_part_bytes = bytes;
+    ws.part = p;
+    ws.part_bytes = bytes;
     return true;
 }
+
+// ws holds at least n bf16 elements
+static bool abf_ensure(Ws &ws, size_t n) {
+    if (n <= ws.abf_elems) return true;
+    if (!ws.grow || g_capturing) return false;
+    if (graph_holds(g_abf) && g_n_retired >= QH_MAX_RETIRED) return false;
+    uint16_t *p = nullptr;
+    if (hipMalloc((void **)&p, n * sizeof(uint16_t)) != hipSuccess) { (void)hipGetLastError(); return false; }
+    (void)retire_buffer(g_abf);                // cannot fail: room checked above
+    g_abf = p;
+    g_abf_elems = n;
+    ws.abf = p;
+    ws.abf_elems = n;
+    return true;
+}
+
+static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, true}; }
 
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
 template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
-                     int M, int K, int N, bool allow_split = false) {
+                     int M, int K, int N) {
     using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    // split K when the tiles leave most CUs idle: slices of >= 4 stages,
-    // doubled until every CU has a block; the fp32 partials need workspace
-    int ks = 1;
-    if (allow_split)
-        while (tiles * ks < g_cus && 2 * ks <= RMAX && (K / (2 * ks)) % BK == 0 && K / (2 * ks) >= 4 * BK) ks *= 2;
-    float *part = nullptr;
-    const size_t MN = (size_t)M * N;
-    if (ks > 1 && !part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) ks = 1;
-    if (ks > 1) part = g_part;
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, ks), dim3(NTHREADS), 0,
-                       g_stream, c, a, b, b2, M, K, N, map, part, K / ks);
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, 1), dim3(NTHREADS), 0,
+                       g_stream, c, a, b, b2, M, K, N, map, (float *)nullptr, K);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
-    if (ks > 1) {
-        size_t blocks = (MN + NTHREADS - 1) / NTHREADS;
-        if (blocks > 2048) blocks = 2048;
-        hipLaunchKernelGGL((k_stream_reduce<GATED>), dim3((unsigned)blocks), dim3(NTHREADS), 0, g_stream,
-                           c, part, MN, ks);
-        HCHECK(hipGetLastError(), QH_ELAUNCH);
-    }
     return QH_OK;
 }
 
@@ -2666,11 +2474,17 @@ static int launch_cvt_bf16(uint16_t *dst, const float *src, size_t n) {
     return QH_OK;
 }
 
+// fp32 bytes of the slice sums a stream plan with KS needs (0: no K split)
+static inline size_t stream_part_bytes(int M, int K, int N, int ks, bool gated) {
+    const int ksplit = K / (256 * ks);
+    return ksplit > 1 ? (size_t)ksplit * (gated ? 2 : 1) * M * N * sizeof(float) : 0;
+}
+
 // weight-streaming GEMM: K % (256*KS) == 0, M <= 64, 16-byte aligned a, b,
-// b2 and sizes within stream_fits (checked by the caller).  K / (256*KS) > 1
-// slices sum through the workspace and one k_stream_reduce pass.
+// b2, sizes within stream_fits and the slice sums within ws (checked by the
+// caller).  K / (256*KS) > 1 slices sum through ws and one k_stream_reduce pass.
 template <int MT, int KS, bool GATED>
-static int launch_stream_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+static int launch_stream_t(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                            int M, int K, int N) {
     constexpr int ST = KS >= 8 ? 2 : KS >= 4 ? 3 : KS >= 2 ? 4 : 8;   // tiles in flight per wave
     const int ksplit = K / (256 * KS);
@@ -2679,9 +2493,8 @@ static int launch_stream_t(float *c, const float *a, const uint16_t *b, const ui
     float *part = nullptr;
     const size_t MN = (size_t)M * N;
     if (ksplit > 1) {
-        const size_t need = (size_t)ksplit * (GATED ? 2 : 1) * MN * sizeof(float);
-        if (need > g_abf_elems * sizeof(uint16_t)) return QH_ETOOBIG;
-        part = reinterpret_cast<float *>(g_abf);
+        if (stream_part_bytes(M, K, N, KS, GATED) > ws.part_bytes) return QH_ETOOBIG;
+        part = use_part(ws);
     }
     hipLaunchKernelGGL((k_gemm_stream<MT, KS, ST, GATED>), dim3(gx, ksplit), dim3(STREAM_THREADS), 0,
                        g_stream, c, part, a, b, b2, M, K, N, ntiles);
@@ -2710,10 +2523,11 @@ static int skinny_slices(int K, int N, int M = 64) {
     return best;
 }
 
-// skinny GEMM: M <= 64, K % 64 == 0, 16-byte aligned a, b, b2 and sizes below
-// 2 GiB (checked by the caller); more than one slice needs the split-K workspace
+// skinny GEMM: M <= SKINNY_MMAX, K % 64 == 0, 16-byte aligned a, b, b2 and
+// sizes below 2 GiB (checked by the caller); more than one slice needs the
+// slice sums in ws
 template <int MT, bool GATED>
-static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+static int launch_skinny_t(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                            int M, int K, int N, bool reduce = true) {
     const int ks = skinny_slices(K, N, M);
     if (ks <= 0) return QH_EINVAL;
@@ -2722,8 +2536,8 @@ static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const ui
     const size_t MN = (size_t)M * N;
     float *part = nullptr;
     if (ks > 1) {
-        if (!part_ensure((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float))) return QH_ETOOBIG;
-        part = g_part;
+        if ((size_t)ks * (GATED ? 2 : 1) * MN * sizeof(float) > ws.part_bytes) return QH_ETOOBIG;
+        part = use_part(ws);
     }
     hipLaunchKernelGGL((k_gemm_skinny<MT, GATED>), dim3(nblk, ks, mslab), dim3(NTHREADS), 0, g_stream, c, part, a,
                        b, b2, M, K, N, K / ks);
@@ -2738,29 +2552,30 @@ static int launch_skinny_t(float *c, const float *a, const uint16_t *b, const ui
     return QH_OK;
 }
 template <bool GATED>
-static int launch_skinny(float *c, const float *a, const uint16_t *b, const uint16_t *b2, int M, int K, int N) {
+static int launch_skinny(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                         int M, int K, int N) {
     switch (stream_mt(M)) {
-        case 1: return launch_skinny_t<1, GATED>(c, a, b, b2, M, K, N);
-        case 2: return launch_skinny_t<2, GATED>(c, a, b, b2, M, K, N);
-        default: return launch_skinny_t<4, GATED>(c, a, b, b2, M, K, N);
+        case 1: return launch_skinny_t<1, GATED>(ws, c, a, b, b2, M, K, N);
+        case 2: return launch_skinny_t<2, GATED>(ws, c, a, b, b2, M, K, N);
+        default: return launch_skinny_t<4, GATED>(ws, c, a, b, b2, M, K, N);
     }
 }
 
 template <bool GATED>
-static int launch_stream(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+static int launch_stream(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N, int ks) {
     switch (stream_mt(M) * 100 + ks) {
-        case 101: return launch_stream_t<1, 1, GATED>(c, a, b, b2, M, K, N);
-        case 102: return launch_stream_t<1, 2, GATED>(c, a, b, b2, M, K, N);
-        case 104: return launch_stream_t<1, 4, GATED>(c, a, b, b2, M, K, N);
-        case 108: return launch_stream_t<1, 8, GATED>(c, a, b, b2, M, K, N);
-        case 201: return launch_stream_t<2, 1, GATED>(c, a, b, b2, M, K, N);
-        case 202: return launch_stream_t<2, 2, GATED>(c, a, b, b2, M, K, N);
-        case 204: return launch_stream_t<2, 4, GATED>(c, a, b, b2, M, K, N);
-        case 208: return launch_stream_t<2, 8, GATED>(c, a, b, b2, M, K, N);
-        case 401: return launch_stream_t<4, 1, GATED>(c, a, b, b2, M, K, N);
-        case 402: return launch_stream_t<4, 2, GATED>(c, a, b, b2, M, K, N);
-        case 404: return launch_stream_t<4, 4, GATED>(c, a, b, b2, M, K, N);
+        case 101: return launch_stream_t<1, 1, GATED>(ws, c, a, b, b2, M, K, N);
+        case 102: return launch_stream_t<1, 2, GATED>(ws, c, a, b, b2, M, K, N);
+        case 104: return launch_stream_t<1, 4, GATED>(ws, c, a, b, b2, M, K, N);
+        case 108: return launch_stream_t<1, 8, GATED>(ws, c, a, b, b2, M, K, N);
+        case 201: return launch_stream_t<2, 1, GATED>(ws, c, a, b, b2, M, K, N);
+        case 202: return launch_stream_t<2, 2, GATED>(ws, c, a, b, b2, M, K, N);
+        case 204: return launch_stream_t<2, 4, GATED>(ws, c, a, b, b2, M, K, N);
+        case 208: return launch_stream_t<2, 8, GATED>(ws, c, a, b, b2, M, K, N);
+        case 401: return launch_stream_t<4, 1, GATED>(ws, c, a, b, b2, M, K, N);
+        case 402: return launch_stream_t<4, 2, GATED>(ws, c, a, b, b2, M, K, N);
+        case 404: return launch_stream_t<4, 4, GATED>(ws, c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
     }
 }
@@ -2770,32 +2585,19 @@ template <bool GATED>
 static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b, const uint16_t *b2,
                           int M, int K, int N) {
     switch (p) {
-        case PLAN_XB256x256:    return launch_xl<256, 256, 64, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256k32: return launch_xl<256, 256, 32, GATED, true>(c, a, b, b2, M, K, N);
-        case PLAN_XB128x256:    return launch_xl<128, 256, 64, GATED, true>(c, a, b, b2, M, K, N);
-        case PLAN_XB256x128:    return launch_xl<256, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_XB128x128:    return launch_xl<128, 128, 64, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256s1:  return launch_xl<256, 256, 64, GATED, true, 1>(c, a, b, b2, M, K, N);
         default: return QH_EINVAL;
     }
 }
 
-// the bf16 workspace holds at least n elements (grows only outside capture)
-static bool abf_ensure(size_t n) {
-    if (n <= g_abf_elems) return true;
-    if (g_capturing) return false;
-    if (any_graph() && g_n_retired >= QH_MAX_RETIRED) return false;
-    uint16_t *p = nullptr;
-    if (hipMalloc((void **)&p, n * sizeof(uint16_t)) != hipSuccess) { (void)hipGetLastError(); return false; }
-    (void)retire_buffer(g_abf);                // cannot fail: room checked above
-    g_abf = p;
-    g_abf_elems = n;
-    return true;
-}
+static int g_last_plan = PLAN_AUTO;     // the plan the last GEMM call launched
 
 template <bool GATED>
-static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                     int M, int K, int N) {
+    g_last_plan = plan;
     switch (plan) {
         case PLAN_GEMV:
             switch (M) {
@@ -2811,51 +2613,78 @@ static int dispatch(int plan, float *c, const float *a, const uint16_t *b, const
         case PLAN_T32x128:  return launch_tile<32, 128, 64, 2, 2, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_T16x64:   return launch_tile<16, 128, 64, 1, 4, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_SCALAR64: return launch_tile<64, 64, 64, 2, 2, GATED, false>(c, a, b, b2, M, K, N);
-        case PLAN_R32x64k128s4:  return launch_ring<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
-        case PLAN_R64x64k64s4:   return launch_ring<64, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R64x64k64s6:   return launch_ring<64, 64, 2, 2, 6, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R64x64k128s3:  return launch_ring<64, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
-        case PLAN_R64x128k64s4:  return launch_ring<64, 128, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R128x128k64s3: return launch_ring<128, 128, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R128x64k64s3:  return launch_ring<128, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R32x64k64s6:   return launch_ring<32, 64, 2, 2, 6, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_R64x64k32s6:   return launch_ring<64, 64, 2, 2, 6, GATED, 32>(c, a, b, b2, M, K, N);
-        case PLAN_R32x64k32s4:   return launch_ring<32, 64, 2, 2, 4, GATED, 32>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k128s3:  return launch_pipe<32, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k128s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
-        case PLAN_P64x64k128s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 128>(c, a, b, b2, M, K, N);
-        case PLAN_P64x64k64s4:   return launch_pipe<64, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_P64x128k64s4:  return launch_pipe<64, 128, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_P128x128k64s3: return launch_pipe<128, 128, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_P128x64k64s3:  return launch_pipe<128, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k64s4:   return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_P64x64k64s3:   return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
-        case PLAN_XB256x256: case PLAN_XB256x256k32: case PLAN_XB128x256: case PLAN_XB256x128:
-        case PLAN_XB128x128: case PLAN_XB256x256s1: {
-            const int rc = launch_cvt_bf16(g_abf, a, (size_t)M * K);
+        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k64s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_P64x64k64s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
+        case PLAN_XB256x256k32: case PLAN_XB128x128: case PLAN_XB256x256s1: {
+            if ((size_t)M * K > ws.abf_elems) return QH_ETOOBIG;
+            uint16_t *abf = use_abf(ws);
+            const int rc = launch_cvt_bf16(abf, a, (size_t)M * K);
             if (rc) return rc;
-            return dispatch_bf16a<GATED>(plan, c, g_abf, b, b2, M, K, N);
+            return dispatch_bf16a<GATED>(plan, c, abf, b, b2, M, K, N);
         }
-        case PLAN_X128x256: return launch_xl<128, 256, 64, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X256x128: return launch_xl<256, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X128x128SK: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N, true);
-        case PLAN_SKINNY: return launch_skinny<GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X256x256s1: return launch_xl<256, 256, 64, GATED, false, 1>(c, a, b, b2, M, K, N);
-        case PLAN_X64x256: return launch_xl<64, 256, 64, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X64x128: return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X128x256k32: return launch_xl<128, 256, 32, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X256x128k32: return launch_xl<256, 128, 32, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_STREAM_KS1: return launch_stream<GATED>(c, a, b, b2, M, K, N, 1);
-        case PLAN_STREAM_KS2: return launch_stream<GATED>(c, a, b, b2, M, K, N, 2);
-        case PLAN_STREAM_KS4: return launch_stream<GATED>(c, a, b, b2, M, K, N, 4);
-        case PLAN_STREAM_KS8: return launch_stream<GATED>(c, a, b, b2, M, K, N, 8);
+        case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
+        case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
+        case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
+        case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
+        case PLAN_STREAM_KS8: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 8);
         default: return QH_EINVAL;
     }
 }
 
-static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+// The plan for an M x K x N call and the workspace it needs in ws (grown
+// there when ws is the library's).  A plan whose conditions fail falls back
+// to the 64x64 tiles, or to the fp32-A large tiles when the bf16 copy of A
+// has no room; with a fixed workspace (`strict`) a plan that needs more than
+// it holds is QH_ETOOBIG instead of a fall-back.  Returns the plan, or
+// -QH_E* on error.
+static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool strict) {
+    int plan = g_forced_plan ? g_forced_plan : choose_plan(M, K, N, gated, vec);
+    if (!vec) plan = PLAN_SCALAR64;   // forced plans still need vector-safe inputs
+    if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
+    if (is_pipe_plan(plan) && (K % pipe_bk(plan)) != 0) plan = PLAN_T64x64;   // whole k stages
+    if (is_xl_plan(plan) && ((K % xl_bk(plan)) != 0 ||           // xl copies whole k stages and
+                             (size_t)M * K * 4 >= (1ull << 32) ||   // addresses with 32-bit offsets
+                             (size_t)N * K * 2 >= (1ull << 32)))
+        plan = PLAN_T64x64;
+    if (is_xb_plan(plan) && !abf_ensure(ws, (size_t)M * K)) {     // no room for the bf16 copy of A
+        if (strict) return -QH_ETOOBIG;
+        plan = PLAN_X128x128;
+    }
+    if (plan == PLAN_SKINNY) {
+        const int ks = (M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
+                        (size_t)N * K * 2 < (1ull << 31)) ? skinny_slices(K, N, M) : 0;
+        const size_t part = (size_t)ks * (gated ? 2 : 1) * M * N * sizeof(float);
+        if (ks > 1 && !part_ensure(ws, part)) {
+            if (strict) return -QH_ETOOBIG;
+            plan = PLAN_T64x64;
+        } else if (ks <= 0) {
+            plan = PLAN_T64x64;
+        }
+    }
+    if (is_stream_plan(plan)) {
+        // KS must divide the slices and fit the A registers; more than one
+        // slice needs workspace for the fp32 partial sums
+        const bool fits = stream_fits(M, K, N);
+        const int ks = plan != PLAN_STREAM ? 1 << (plan - PLAN_STREAM_KS1) : fits ? stream_ks(M, K, N, g_cus) : 0;
+        bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16 && K / (256 * ks) <= RMAX;
+        if (ok) {
+            const size_t part = stream_part_bytes(M, K, N, ks, gated);
+            if (part && !part_ensure(ws, part)) {
+                if (strict) return -QH_ETOOBIG;
+                ok = false;
+            }
+        }
+        if (!ok) plan = PLAN_T64x64;
+        else plan = ks == 1 ? PLAN_STREAM_KS1 : ks == 2 ? PLAN_STREAM_KS2 : ks == 4 ? PLAN_STREAM_KS4 : PLAN_STREAM_KS8;
+    }
+    return plan;
+}
+
+static int gemm_common(Ws ws, bool strict, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                        int M, int K, int N, bool gated) {
     if (!g_inited) return QH_ESTATE;
     if (M < 0 || K < 0 || N < 0) return QH_EINVAL;
@@ -2871,38 +2700,10 @@ static int gemm_common(float *c, const float *a, const uint16_t *b, const uint16
         return QH_OK;
     }
     const bool vec = (K % 8) == 0 && aligned16(a) && aligned16(b) && (!gated || aligned16(b2));
-    int plan = g_forced_plan ? g_forced_plan : choose_plan(M, K, N, gated, vec);
-    if (!vec) plan = PLAN_SCALAR64;   // forced plans still need vector-safe inputs
-    if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
-    if (is_ring_plan(plan) && (K % ring_bk(plan)) != 0)           // ring copies whole k stages
-        plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
-    if (is_xl_plan(plan) && ((K % xl_bk(plan)) != 0 ||           // xl copies whole k stages and
-                             (size_t)M * K * 4 >= (1ull << 32) ||   // addresses with 32-bit offsets
-                             (size_t)N * K * 2 >= (1ull << 32)))
-        plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
-    if (is_xb_plan(plan) && !abf_ensure((size_t)M * K))            // no room for the bf16 copy of A
-        plan = PLAN_X128x256;
-    if (plan == PLAN_SKINNY) {
-        const int ks = (M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
-                        (size_t)N * K * 2 < (1ull << 31)) ? skinny_slices(K, N, M) : 0;
-        const size_t part = (size_t)ks * (gated ? 2 : 1) * M * N * sizeof(float);
-        if (ks <= 0 || (ks > 1 && !part_ensure(part))) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
-    }
-    if (is_stream_plan(plan)) {
-        // KS must divide the slices and fit the A registers; more than one
-        // slice needs workspace for the fp32 partial sums
-        const bool fits = stream_fits(M, K, N);
-        const int ks = plan != PLAN_STREAM ? 1 << (plan - PLAN_STREAM_KS1) : fits ? stream_ks(M, K, N, g_cus) : 0;
-        bool ok = fits && ks > 0 && (K / 256) % ks == 0 && stream_mt(M) * ks <= 16 && K / (256 * ks) <= RMAX;
-        if (ok && K / (256 * ks) > 1) {
-            const size_t part = (size_t)(K / (256 * ks)) * (gated ? 2 : 1) * M * N * sizeof(float);
-            ok = part < (1ull << 31) && abf_ensure((part + 1) / sizeof(uint16_t));   // 32-bit offsets
-        }
-        if (!ok) plan = (K % 32) == 0 ? PLAN_R32x64k32s4 : PLAN_T64x64;
-        else plan = ks == 1 ? PLAN_STREAM_KS1 : ks == 2 ? PLAN_STREAM_KS2 : ks == 4 ? PLAN_STREAM_KS4 : PLAN_STREAM_KS8;
-    }
-    return gated ? dispatch<true>(plan, c, a, b, b2, M, K, N)
-                 : dispatch<false>(plan, c, a, b, nullptr, M, K, N);
+    const int plan = resolve_plan(ws, M, K, N, gated, vec, strict);
+    if (plan < 0) return -plan;
+    return gated ? dispatch<true>(plan, ws, c, a, b, b2, M, K, N)
+                 : dispatch<false>(plan, ws, c, a, b, nullptr, M, K, N);
 }
 
 // C = A.B^T with A already bf16 (bits), for callers that hold bf16
@@ -2919,6 +2720,7 @@ static int gemm_bf16a_common(float *c, const uint16_t *a, const uint16_t *b, con
     if ((size_t)M * K * 2 >= (1ull << 32) || (size_t)N * K * 2 >= (1ull << 32)) return QH_ETOOBIG;
     int plan = g_forced_plan;
     if (!is_xb_plan(plan)) plan = choose_bf16a_plan(M, K, N, gated);
+    g_last_plan = plan;
     return gated ? dispatch_bf16a<true>(plan, c, a, b, b2, M, K, N)
                  : dispatch_bf16a<false>(plan, c, a, b, nullptr, M, K, N);
 }
@@ -2933,8 +2735,10 @@ extern "C" int qh_gemm_gate_up_silu_bf16a(float *h, const uint16_t *x, const uin
 }
 
 extern "C" int qh_gemm(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
-    return gemm_common(c, a, b, nullptr, M, K, N, false);
+    return gemm_common(lib_ws(), false, c, a, b, nullptr, M, K, N, false);
 }
+
+extern "C" const char *qh_last_plan(void) { return k_plan_names[g_last_plan]; }
 
 // qh_gemm, except that when the skinny kernel splits K the slices' fp32 sums
 // are left in the split-K workspace ([ks][M][N], *part) for the caller to add
@@ -2954,29 +2758,31 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
     const bool take = vec && !g_forced_plan &&
                       (choose_plan(M, K, N, false, vec) == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
+    Ws ws = lib_ws();
     if (take && M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
         (size_t)N * K * 2 < (1ull << 31)) {
         const int s = skinny_slices(K, N, M);
-        if (s > 1 && part_ensure((size_t)s * M * N * sizeof(float))) {
+        if (s > 1 && part_ensure(ws, (size_t)s * M * N * sizeof(float))) {
             int rc;
+            g_last_plan = PLAN_SKINNY;
             switch (stream_mt(M)) {
-                case 1: rc = launch_skinny_t<1, false>(c, a, b, nullptr, M, K, N, false); break;
-                case 2: rc = launch_skinny_t<2, false>(c, a, b, nullptr, M, K, N, false); break;
-                default: rc = launch_skinny_t<4, false>(c, a, b, nullptr, M, K, N, false); break;
+                case 1: rc = launch_skinny_t<1, false>(ws, c, a, b, nullptr, M, K, N, false); break;
+                case 2: rc = launch_skinny_t<2, false>(ws, c, a, b, nullptr, M, K, N, false); break;
+                default: rc = launch_skinny_t<4, false>(ws, c, a, b, nullptr, M, K, N, false); break;
             }
             if (rc == QH_OK) {
-                *part = g_part;
+                *part = ws.part;
                 *ks = s;
             }
             return rc;
         }
     }
-    return gemm_common(c, a, b, nullptr, M, K, N, false);
+    return gemm_common(ws, false, c, a, b, nullptr, M, K, N, false);
 }
 
 extern "C" int qh_gemm_gate_up_silu(float *h, const float *x, const uint16_t *wg,
                                     const uint16_t *wu, int M, int K, int N) {
-    return gemm_common(h, x, wg, wu, M, K, N, true);
+    return gemm_common(lib_ws(), false, h, x, wg, wu, M, K, N, true);
 }
 
 extern "C" int qh_tile_to_row(uint16_t *dst, const uint16_t *src, int N, int K, int tn, int tk) {
@@ -2997,6 +2803,7 @@ extern "C" int qh_capture_begin(void) {
     if (g_capturing) return QH_ESTATE;
     HCHECK(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal), QH_ERUNTIME);
     g_capturing = 1;
+    g_cap_abf = g_cap_part = false;
     return QH_OK;
 }
 
@@ -3017,6 +2824,9 @@ extern "C" int qh_capture_end(int *graph_id) {
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return fail(e, QH_ERUNTIME);
     g_graph_exec[slot] = exec;
+    // the workspace buffers its kernels read or write stay allocated while it lives
+    g_graph_ws[slot][0] = g_cap_abf ? (void *)g_abf : nullptr;
+    g_graph_ws[slot][1] = g_cap_part ? (void *)g_part : nullptr;
     if (graph_id) *graph_id = slot;
     return QH_OK;
 }
@@ -3032,7 +2842,8 @@ extern "C" int qh_graph_destroy(int id) {
     if (id < 0 || id >= QH_MAX_GRAPHS || !g_graph_exec[id]) return QH_EINVAL;
     HCHECK(hipGraphExecDestroy(g_graph_exec[id]), QH_ERUNTIME);
     g_graph_exec[id] = nullptr;
-    if (!any_graph()) free_retired();
+    g_graph_ws[id][0] = g_graph_ws[id][1] = nullptr;
+    free_retired();
     return QH_OK;
 }
 

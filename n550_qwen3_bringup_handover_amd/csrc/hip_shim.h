@@ -55,6 +55,8 @@ int qh_gemm(float *c_d, const float *a_d, const uint16_t *b_d,
  * valid until the next library call that uses the split-K workspace. */
 int qh_gemm_split(float *c_d, const float *a_d, const uint16_t *b_d, int M, int K, int N,
                   const float **part_d, int *ks);
+/* name of the plan the last GEMM call launched */
+const char *qh_last_plan(void);
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */
 int qh_gemm_gate_up_silu(float *h_d, const float *x_d, const uint16_t *wg_d,
                          const uint16_t *wu_d, int M, int K, int N);

@@ -26,6 +26,10 @@ static int g_layout;                    /* 0 ROW, 1 TILE */
 static int g_tile_n = 128, g_tile_k = 32;
 
 static void  *g_a_d;  static size_t g_a_cap;     /* device staging for A */
+/* device staging for unmapped B, uploaded on every call: [0] B (or Wg),
+ * [1] Wu, [2] a TILE buffer before it is re-laid out row-major */
+static void  *g_b_d[3]; static size_t g_b_cap[3];
+static int g_wcache = -1;               /* address cache of unmapped B: -1 = not yet read from env */
 static void  *g_a_h;  static size_t g_a_hcap;    /* pinned host staging for A */
 static void  *g_c_h;  static size_t g_c_hcap;    /* pinned host staging for C */
 
@@ -126,6 +130,11 @@ void qwen3_hip_release(void) {
     (void)qh_free(g_a_d);
     g_a_d = NULL;
     g_a_cap = 0;
+    for (int i = 0; i < 3; i++) {
+        (void)qh_free(g_b_d[i]);
+        g_b_d[i] = NULL;
+        g_b_cap[i] = 0;
+    }
     (void)qh_host_free(g_a_h);
     (void)qh_host_free(g_c_h);
     g_a_h = g_c_h = NULL;
@@ -250,6 +259,7 @@ size_t qwen3_hip_weight_bytes(void) {
     size_t t = 0;
     for (int i = 0; i < g_nmaps; i++) t += g_maps[i].bytes;
     for (int i = 0; i < g_nwc; i++) t += (size_t)g_wc[i].N * (size_t)g_wc[i].K * 2u;
+    for (int i = 0; i < 3; i++) t += g_b_cap[i];
     return t;
 }
 
@@ -276,9 +286,44 @@ static wcache_t *cache_add(void) {
     return e;
 }
 
+static int grow(void **p, size_t *cap, size_t need);
+
+static int weight_cache_on(void) {
+    if (g_wcache < 0) {
+        const char *e = getenv("QWEN3_HIP_WEIGHT_CACHE");
+        g_wcache = (e && e[0] == '1') ? 1 : 0;
+    }
+    return g_wcache;
+}
+
+void qwen3_hip_set_weight_cache(int on) {
+    if (!on && g_wcache == 1) qwen3_hip_forget_weights(NULL);
+    g_wcache = on ? 1 : 0;
+}
+
+/* Unmapped B without the address cache: copied to device staging on every
+ * call, as the reference reads B on every call (SRC/kernels_scalar.c:9-21),
+ * so a caller may change B between calls.  slot 0 holds B (or Wg), slot 1 Wu;
+ * a TILE buffer goes through slot 2 and is re-laid out row-major into its
+ * slot. */
+static const uint16_t *weight_upload(const uint16_t *b, int N, int K, int layout, int slot, int *rc) {
+    const size_t bytes = (size_t)N * (size_t)K * 2u;
+    if ((*rc = grow(&g_b_d[slot], &g_b_cap[slot], bytes))) return NULL;
+    if (layout == 0) {
+        if ((*rc = qh_h2d(g_b_d[slot], b, bytes))) return NULL;
+        return (const uint16_t *)g_b_d[slot];
+    }
+    if ((*rc = grow(&g_b_d[2], &g_b_cap[2], bytes))) return NULL;
+    if ((*rc = qh_h2d(g_b_d[2], b, bytes))) return NULL;
+    if ((*rc = qh_tile_to_row((uint16_t *)g_b_d[slot], (const uint16_t *)g_b_d[2], N, K,
+                              g_tile_n, g_tile_k)))
+        return NULL;
+    return (const uint16_t *)g_b_d[slot];
+}
+
 /* Device pointer of B[N,K] in row-major form, for a host pointer b stored in
  * `layout`.  Returns NULL and sets *rc on failure. */
-static const uint16_t *weight_dev(const uint16_t *b, int N, int K, int layout, int *rc) {
+static const uint16_t *weight_dev(const uint16_t *b, int N, int K, int layout, int slot, int *rc) {
     const size_t bytes = (size_t)N * (size_t)K * 2u;
     const int tn = g_tile_n, tk = g_tile_k;
     const wmap_t *m = find_map(b, bytes);
@@ -288,6 +333,9 @@ static const uint16_t *weight_dev(const uint16_t *b, int N, int K, int layout, i
         return (const uint16_t *)(m->dev + ((const unsigned char *)b - m->host));
 
     if (layout == 1 && (N % tn || K % tk)) { *rc = QWEN3_HIP_ELAYOUT; return NULL; }
+
+    if (!m && !weight_cache_on())
+        return weight_upload(b, N, K, layout, slot, rc);
 
     wcache_t *e = cache_find(b, N, K, layout, tn, tk);
     uint64_t fp = 0;
@@ -380,10 +428,10 @@ static int gemm_host(float *c, const float *a, const uint16_t *b, const uint16_t
         memset(c, 0, (size_t)M * (size_t)N * sizeof(float));
         return 0;
     }
-    const uint16_t *bd = weight_dev(b, N, K, layout, &rc);
+    const uint16_t *bd = weight_dev(b, N, K, layout, 0, &rc);
     if (!bd) return rc;
     const uint16_t *bd2 = NULL;
-    if (gated && !(bd2 = weight_dev(b2, N, K, layout, &rc))) return rc;
+    if (gated && !(bd2 = weight_dev(b2, N, K, layout, 1, &rc))) return rc;
 
     /* A goes host -> pinned staging (memcpy) -> device by the library's copy
      * kernel, on the same stream as the GEMM (a runtime copy from host memory
@@ -482,4 +530,5 @@ int qwen3_hip_timer_elapsed_ms(int a, int b, float *ms) {
     return note(qh_timer_elapsed_ms(a, b, ms));
 }
 const char *qwen3_hip_plan(int M, int K, int N, int gated) { return qh_gemm_plan(M, K, N, gated); }
+const char *qwen3_hip_last_plan(void) { return qh_last_plan(); }
 int qwen3_hip_force_plan(int plan_id) { return note(qh_force_plan(plan_id)); }

@@ -53,6 +53,7 @@ _PROTOS = {
     "qwen3_hip_map_weights": (ctypes.c_int, [VP, ctypes.c_size_t]),
     "qwen3_hip_unmap_weights": (ctypes.c_int, [VP]),
     "qwen3_hip_forget_weights": (None, [VP]),
+    "qwen3_hip_set_weight_cache": (None, [ctypes.c_int]),
     "qwen3_hip_weight_bytes": (ctypes.c_size_t, []),
     "qwen3_hip_gemm_dev": (ctypes.c_int, [VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_gemm_gate_up_silu_dev": (ctypes.c_int, [VP, VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
@@ -74,6 +75,7 @@ _PROTOS = {
     "qwen3_hip_timer_elapsed_ms": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, F32P]),
     "qwen3_hip_plan": (ctypes.c_char_p, [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_force_plan": (ctypes.c_int, [ctypes.c_int]),
+    "qwen3_hip_last_plan": (ctypes.c_char_p, []),
     "qwen3_hip_device_name": (ctypes.c_char_p, []),
     # include/qwen3_hip_model.h
     "qwen3_hip_qw3m_size": (ctypes.c_size_t, [ctypes.c_int]),

@@ -59,6 +59,19 @@ def test_automatic_plan_table(M, K, N, gated, plan):
     assert abi.plan(M, K, N, gated) == plan
 
 
+def test_plan_ids_match_the_library():
+    """abi.PLANS (the ids tests force) names the library's own plans: a
+    forced plan is what qwen3_hip_plan reports, with no device needed."""
+    try:
+        for name, pid in abi.PLANS.items():
+            abi.force_plan(pid)
+            assert abi.plan(64, 1024, 1024) == (name if pid else abi.plan(64, 1024, 1024))
+        with pytest.raises(runtime.Qwen3HipError):
+            abi.force_plan(len(abi.PLANS))
+    finally:
+        abi.force_plan(0)
+
+
 @pytest.mark.parametrize("layout,tn,tk,ok", [
     (0, 0, 0, True), (0, 128, 32, True),          # ROW ignores tile sizes (qwen3.c:67-73)
     (1, 128, 32, True),                           # the AME tile (kernels.h:20-23)

@@ -313,6 +313,32 @@ def test_mapped_blob_and_cache_invalidation(lib):
     assert not np.array_equal(c1, c2)
 
 
+def test_unmapped_weights_read_on_every_call(lib):
+    """By default an unmapped B is copied on every call, like the reference
+    kernels read it: a change to a single row that a sampled fingerprint
+    would miss still reaches the result.  With the opt-in address cache the
+    same change needs qwen3_hip_forget_weights()."""
+    M, K, N = 2, 1024, 256
+    a = oracle.f32_bf16_normal(M * K, 710)
+    w = oracle.bf16_normal(N * K, 711, 0.02)
+    c1 = run_gemm(a, w, M, K, N)
+    row, col = 77, 5                  # 8-byte word 19,713 of 65,536: not among the 512 sampled
+    w[row * K + col] = 0x3F80         # 1.0
+    c2 = run_gemm(a, w, M, K, N)
+    numerics.compare(c2, a, w, M, K, N)
+    changed = np.nonzero(c1 != c2)[0]
+    assert set(changed % N) == {row}
+    lib.qwen3_hip_set_weight_cache(1)
+    try:
+        w2 = oracle.bf16_normal(N * K, 713, 0.02)
+        numerics.compare(run_gemm(a, w2, M, K, N), a, w2, M, K, N)
+        w2[row * K + col] = 0x3F80
+        lib.qwen3_hip_forget_weights(ctypes.c_void_p(w2.ctypes.data))
+        numerics.compare(run_gemm(a, w2, M, K, N), a, w2, M, K, N)
+    finally:
+        lib.qwen3_hip_set_weight_cache(0)
+
+
 def test_device_api_matches_host_api():
     M, K, N = 33, 1024, 1024
     a, b = inputs(M, K, N, 800)

@@ -91,6 +91,7 @@ def test_graph_survives_workspace_growth():
         try:
             abi.gemm_dev(cd2.ptr, ad2.ptr, wd2.ptr, M2, K2, N2)     # grows the staging buffer
             abi.sync()
+            assert abi.last_plan() == "xb128x128"                    # grown, not a fall-back
             big = cd2.download(np.float32, M2 * N2)
             numerics.compare(big[:16 * N2], a2[:16 * K2], w2, 16, K2, N2)
             for rep in range(3):
