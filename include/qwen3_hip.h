@@ -141,6 +141,20 @@ int qwen3_hip_gemm_bf16a_dev(float *c_d, const uint16_t *a_d, const uint16_t *b_
 int qwen3_hip_gemm_gate_up_silu_bf16a_dev(float *h_d, const uint16_t *x_d,
                                           const uint16_t *wg_d, const uint16_t *wu_d,
                                           int M, int K, int N);
+/* qwen3_hip_gemm_dev that allocates nothing: no counterpart in the
+ * reference ABI; for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Its workspace (the bf16 copy of A or the fp32 K-slice sums some plans use)
+ * is a fixed device array of qwen3_hip_scratch_bytes() = 32 MiB, one per GPU,
+ * held until the process ends; a call whose plan would need more returns
+ * QWEN3_HIP_ETOOBIG and launches nothing.  Results equal qwen3_hip_gemm_dev's.
+ * The library must be initialised first (qwen3_hip_init: QWEN3_HIP_ESTATE
+ * otherwise).  Every call on a GPU shares that GPU's array, which keeps the
+ * last call's contents; calls that overlap on one GPU (graphs replayed on
+ * another stream, other threads or processes) race on it. */
+int qwen3_hip_gemm_noalloc_dev(float *c_d, const float *a_d, const uint16_t *b_d,
+                               int M, int K, int N);
+size_t qwen3_hip_scratch_bytes(void);
 /* device counterpart of qwen3_op_argmax (SRC/ops.h:36-37,
  * SRC/ops_scalar.c:57-62): first index of the maximum, ties -> lowest index,
  * a NaN at index 0 wins as in the reference's strict ">" scan */

@@ -1865,6 +1865,12 @@ static float *g_part = nullptr;    // split-K partial sums of the large-tile GEM
 static size_t g_part_bytes = 0;
 static const size_t ABF_INIT_ELEMS = (size_t)8192 * 3072;   // 48 MiB: M x K up to 8192 x 3072
 
+// the no-allocation entry point's workspace (see qh_gemm_noalloc)
+#define QH_SCRATCH_BYTES ((size_t)32 << 20)
+__device__ __align__(256) unsigned char scratch[QH_SCRATCH_BYTES];
+#define QH_MAX_DEVICES 64
+static void *g_scratch_dev[QH_MAX_DEVICES];   // per device: its copy of `scratch`
+
 static int fail(hipError_t e, int code) {
     g_last_hip = e;
     (void)hipGetLastError();
@@ -1907,6 +1913,10 @@ extern "C" int qh_init(int device) {
     // (e.g. 4 slices x 1024 x 1024 fp32); grown outside graph capture if needed
     HCHECK(hipMalloc((void **)&g_part, PART_INIT_BYTES), QH_ENOMEM);
     g_part_bytes = PART_INIT_BYTES;
+    // the no-allocation entry point's workspace: this device's copy of the
+    // file-scope array (device current here)
+    if (device < QH_MAX_DEVICES && !g_scratch_dev[device])
+        HCHECK(hipGetSymbolAddress(&g_scratch_dev[device], HIP_SYMBOL(scratch)), QH_ERUNTIME);
     g_device = device;
     g_inited = 1;
     return QH_OK;
@@ -2354,7 +2364,8 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
 // Device memory beyond a GEMM's inputs and outputs: the bf16 copy of A (xb
 // plans) or the fp32 slice sums of a K split (skinny, stream).  No plan uses
 // both at once.  The library's own pair (g_abf, g_part) grows on demand
-// outside graph capture; a fixed workspace (`grow` false) does not.
+// outside graph capture; the no-allocation entry point passes the fixed
+// `scratch` array instead (both fields point at it; `grow` false).
 struct Ws {
     uint16_t *abf;
     size_t abf_elems;
@@ -2739,6 +2750,26 @@ extern "C" int qh_gemm(float *c, const float *a, const uint16_t *b, int M, int K
 }
 
 extern "C" const char *qh_last_plan(void) { return k_plan_names[g_last_plan]; }
+
+// ---- the no-allocation entry point ------------------------------------------
+// qh_gemm with a fixed workspace, for callers that cannot allocate (code
+// under graph capture, tight serving loops): the file-scope device array
+// `scratch` (QH_SCRATCH_BYTES, one copy per GPU for the life of the process)
+// replaces the library's growable workspace; a plan that would need more is
+// QH_ETOOBIG, and nothing is allocated or freed.  Host code reaches the array
+// only through the per-device address hipGetSymbolAddress returned at init
+// (g_scratch_dev), never through its name.  Every plan writes all of the
+// workspace it reads, so nothing needs clearing between calls; calls that
+// overlap on one GPU (another stream, another process's graph) race on it.
+extern "C" size_t qh_scratch_bytes(void) { return QH_SCRATCH_BYTES; }
+
+extern "C" int qh_gemm_noalloc(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    if (!g_inited) return QH_ESTATE;
+    void *s = g_scratch_dev[g_device];
+    if (!s) return QH_ESTATE;
+    const Ws ws{(uint16_t *)s, QH_SCRATCH_BYTES / sizeof(uint16_t), (float *)s, QH_SCRATCH_BYTES, false};
+    return gemm_common(ws, true, c, a, b, nullptr, M, K, N, false);
+}
 
 // qh_gemm, except that when the skinny kernel splits K the slices' fp32 sums
 // are left in the split-K workspace ([ks][M][N], *part) for the caller to add

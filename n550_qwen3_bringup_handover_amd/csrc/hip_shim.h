@@ -55,6 +55,11 @@ int qh_gemm(float *c_d, const float *a_d, const uint16_t *b_d,
  * valid until the next library call that uses the split-K workspace. */
 int qh_gemm_split(float *c_d, const float *a_d, const uint16_t *b_d, int M, int K, int N,
                   const float **part_d, int *ks);
+/* qh_gemm with the fixed device array `scratch` (qh_scratch_bytes()) as
+ * workspace: allocates and frees nothing; QH_ETOOBIG when the plan needs
+ * more workspace than the array holds.  Results equal qh_gemm's. */
+int qh_gemm_noalloc(float *c_d, const float *a_d, const uint16_t *b_d, int M, int K, int N);
+size_t qh_scratch_bytes(void);
 /* name of the plan the last GEMM call launched */
 const char *qh_last_plan(void);
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */

@@ -482,6 +482,13 @@ int qwen3_hip_gemm_dev(float *c, const float *a, const uint16_t *b, int M, int K
     return note(qh_gemm(c, a, b, M, K, N));
 }
 
+int qwen3_hip_gemm_noalloc_dev(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    if (!g_ready) return note(QWEN3_HIP_ESTATE);     /* set-up may allocate: not here */
+    return note(qh_gemm_noalloc(c, a, b, M, K, N));
+}
+
+size_t qwen3_hip_scratch_bytes(void) { return qh_scratch_bytes(); }
+
 int qwen3_hip_gemm_gate_up_silu_dev(float *h, const float *x, const uint16_t *wg,
                                     const uint16_t *wu, int M, int K, int N) {
     READY_OR_RETURN();

@@ -57,6 +57,8 @@ _PROTOS = {
     "qwen3_hip_weight_bytes": (ctypes.c_size_t, []),
     "qwen3_hip_gemm_dev": (ctypes.c_int, [VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_gemm_gate_up_silu_dev": (ctypes.c_int, [VP, VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_gemm_noalloc_dev": (ctypes.c_int, [VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_scratch_bytes": (ctypes.c_size_t, []),
     "qwen3_hip_gemm_bf16a_dev": (ctypes.c_int, [VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_gemm_gate_up_silu_bf16a_dev": (ctypes.c_int, [VP, VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_argmax_dev": (ctypes.c_int, [VP, VP, ctypes.c_int]),
