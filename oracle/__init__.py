@@ -175,6 +175,15 @@ def now():
 
 # ---- the reference's own compiled C (oracle/_ref), when present --------------
 
+def hw16mt():
+    """ctypes handle of oracle/libhw16mt.so: this directory's threaded
+    restatement of kernels_hwsim.c (symbol qwen3_gemm), built on demand"""
+    path = os.path.join(HERE, "libhw16mt.so")
+    if not os.path.exists(path):
+        subprocess.run(["make", "-s", "-C", HERE, "libhw16mt.so"], check=True)
+    return ctypes.CDLL(path)
+
+
 def ref(name):
     """ctypes handle of oracle/_ref/lib<name>.so, or None if it was not built."""
     path = os.path.join(REF_DIR, f"lib{name}.so")

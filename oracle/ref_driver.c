@@ -114,3 +114,43 @@ int refdrv_generate(const void *blob, size_t blob_size,
     free(scratch);
     return n_out;
 }
+
+/* refdrv_generate, and also the logits after chosen decode steps: for each
+ * step s in log_steps[0..n_log) (1 <= s <= n_decode: the forward that
+ * produces out[s]), VOCAB floats go to step_logits + i * VOCAB. */
+int refdrv_generate_steps(const void *blob, size_t blob_size,
+                          const int *prompt, int n_prompt, int n_decode,
+                          int *out, float *margins, float *logits_out,
+                          const int *log_steps, int n_log, float *step_logits) {
+    static qwen3_t m;
+    void *scratch = malloc(qwen3_scratch_bytes());
+    if (!scratch) return QWEN3_ERR_OOM;
+    int rc = qwen3_init(&m, blob, blob_size, scratch, qwen3_scratch_bytes());
+    if (rc != QWEN3_OK) { free(scratch); return rc; }
+    if (n_prompt < 1 || n_prompt + n_decode > QWEN3_MAX_SEQ) {
+        free(scratch);
+        return QWEN3_ERR_SHAPE;
+    }
+    for (int p0 = 0; p0 < n_prompt; p0 += QWEN3_MAX_BATCH) {
+        int nt = n_prompt - p0 < QWEN3_MAX_BATCH ? n_prompt - p0 : QWEN3_MAX_BATCH;
+        qwen3_forward_batch(&m, prompt + p0, nt, p0);
+    }
+    if (logits_out)
+        memcpy(logits_out, qwen3_last_logits(&m), sizeof(float) * QWEN3_VOCAB_SIZE);
+    int n_out = 0;
+    int next = qwen3_argmax(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+    if (margins) margins[n_out] = top2_margin(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
+    out[n_out++] = next;
+    for (int step = 0; step < n_decode; step++) {
+        qwen3_forward(&m, next, n_prompt + step);
+        const float *lg = qwen3_last_logits(&m);
+        for (int i = 0; i < n_log; i++)
+            if (log_steps[i] == step + 1)
+                memcpy(step_logits + (size_t)i * QWEN3_VOCAB_SIZE, lg, sizeof(float) * QWEN3_VOCAB_SIZE);
+        next = qwen3_argmax(lg, QWEN3_VOCAB_SIZE);
+        if (margins) margins[n_out] = top2_margin(lg, QWEN3_VOCAB_SIZE);
+        out[n_out++] = next;
+    }
+    free(scratch);
+    return n_out;
+}

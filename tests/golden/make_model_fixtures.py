@@ -21,6 +21,11 @@ the library's QW3M writer and compare the checksum first.  The prompt comes
 from the oracle's SplitMix64 stream.  Usage:
 
     python tests/golden/make_model_fixtures.py [short|p128_d128|batch|dump|all]
+    python tests/golden/make_model_fixtures.py [long|p128_d128_logits|steps]
+
+  model_long.npz, model_p128_d128_logits.npz ("steps"): the reference built
+  with a 2048-position cache; prompt, greedy tokens, margins, the last
+  prefill logits row and the logits after chosen decode steps (float16).
 """
 import ctypes
 import os
@@ -90,6 +95,62 @@ def run(name):
     path = os.path.join(HERE, f"model_{name}.npz")
     np.savez_compressed(path, **arrays)
     print(f"{path}: {n} tokens in {time.time() - t0:.0f} s; min margin {margins.min():.4g}")
+
+
+# The reference forward built with a 2048-position cache (oracle/Makefile
+# target ref-long: qwen3.c with -DQWEN3_MAX_SEQ=2048 and the threaded 16-block
+# GEMM of oracle/hw16_mt.c, bit-exact to kernels_hwsim.c), with logits kept
+# after chosen decode steps (float16: the comparisons' bound is ~1e-2).
+STEP_CASES = {
+    # name: (n_prompt, n_decode, decode steps whose logits are kept, prompt seed)
+    "long": (1100, 8, (1, 4, 8), PROMPT_SEED + 0x100),
+    "p128_d128_logits": (128, 128, (1, 32, 64, 128), PROMPT_SEED),
+}
+
+
+def run_steps(name):
+    n_prompt, n_decode, log_steps, pseed = STEP_CASES[name]
+    L = oracle.ref("ref_model_hw16mt_s2048")
+    if L is None:
+        sys.exit("oracle/_ref/libref_model_hw16mt_s2048.so missing: run `make -C oracle ref-long`")
+    L.refdrv_generate_steps.restype = ctypes.c_int
+    L.refdrv_generate_steps.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
+                                        ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float),
+                                        ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.POINTER(ctypes.c_float)]
+    L.refdrv_max_seq.restype = ctypes.c_int
+    assert L.refdrv_max_seq() == 2048
+    blob = M.qw3m_random(SEED, M.LAYOUT_ROW, threads=8)
+    prompt = prompt_tokens(n_prompt, pseed)
+    out = np.zeros(n_decode + 1, np.int32)
+    margins = np.zeros(n_decode + 1, np.float32)
+    logits = np.zeros(VOCAB, np.float32)
+    steps = np.array(log_steps, np.int32)
+    step_logits = np.zeros((len(steps), VOCAB), np.float32)
+    t0 = time.time()
+    n = L.refdrv_generate_steps(blob.ctypes.data_as(ctypes.c_void_p), blob.nbytes,
+                                prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), n_prompt, n_decode,
+                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                margins.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                logits.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                steps.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), len(steps),
+                                step_logits.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    if n != n_decode + 1:
+        sys.exit(f"refdrv_generate_steps returned {n}")
+    if name == "p128_d128_logits":
+        # the same model and prompt as model_p128_d128.npz (kernels_hwsim.c, a
+        # 256-position build): the threaded 2048-position build must agree
+        old = np.load(os.path.join(HERE, "model_p128_d128.npz"))
+        assert np.array_equal(old["tokens"], out) and np.array_equal(old["margins"], margins)
+    arrays = dict(seed=np.uint64(SEED), layout=np.int32(0), checksum=np.uint64(blob_checksum(blob)),
+                  prompt=prompt, tokens=out, margins=margins, prefill_logits=logits.astype(np.float16),
+                  log_steps=steps, step_logits=step_logits.astype(np.float16),
+                  kernel=np.array("hwsim-threaded"), max_seq=np.int32(2048),
+                  seconds=np.float64(time.time() - t0))
+    path = os.path.join(HERE, f"model_{name}.npz")
+    np.savez_compressed(path, **arrays)
+    print(f"{path}: {n} tokens in {time.time() - t0:.0f} s; min margin {margins.min():.4g}; "
+          f"tokens {out.tolist()[:12]}")
 
 
 # batched decode: more prompts of other lengths (prompt i from the stream
@@ -177,6 +238,13 @@ def dumps():
 
 if __name__ == "__main__":
     which = sys.argv[1] if len(sys.argv) > 1 else "all"
+    if which in STEP_CASES:
+        run_steps(which)
+        sys.exit(0)
+    if which == "steps":
+        for name in STEP_CASES:
+            run_steps(name)
+        sys.exit(0)
     if which in ("dump", "all"):
         dumps()
     if which in ("batch", "all"):

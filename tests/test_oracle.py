@@ -83,6 +83,37 @@ def test_scalar_matches_compiled_reference_live(M, K, N):
                           oracle.ref_gemm(H, a, b, M, K, N).view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 2048), (4, 1024, 256), (8, 33, 128), (129, 64, 130),
+                                   (1, 3072, 1024), (7, 17, 5)])
+def test_threaded_hw16_is_bit_exact(M, K, N, monkeypatch):
+    """oracle/hw16_mt.c (the GEMM the long-context reference build links):
+    bit-exact to orc_gemm_hw16 (itself pinned to the RTL golden vectors) for
+    any thread count, and to the compiled kernels_hwsim.c where it was built;
+    inputs not bf16-representable and K not a multiple of 16 included."""
+    T = oracle.hw16mt()
+    a = oracle.f32_bf16_normal(M * K, 17 + M, 1.0) + np.float32(3e-5)
+    b = oracle.bf16_normal(N * K, 18 + N, 0.02)
+    want = oracle.gemm_hw16(a, b, M, K, N)
+    for threads in ("1", "3", "8"):
+        monkeypatch.setenv("ORC_THREADS", threads)
+        got = oracle.ref_gemm(T, a, b, M, K, N)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), threads
+    H = oracle.ref("ref_hwsim")
+    if H is not None:
+        assert np.array_equal(oracle.ref_gemm(H, a, b, M, K, N).view(np.uint32), want.view(np.uint32))
+
+
+def test_threaded_hw16_on_the_rtl_golden_vectors():
+    """the shipped AME vectors through the threaded GEMM: every output bit-exact"""
+    T = oracle.hw16mt()
+    for path in rtl_cases():
+        z = np.load(path)
+        M, N, K = int(z["M"]), int(z["N"]), int(z["K"])
+        a = oracle.bf16_to_f32(z["a_bf16"]) if "a_bf16" in z else z["a_src"].ravel()
+        got = oracle.ref_gemm(T, a, z["b_bf16"], M, K, N)
+        assert np.array_equal(got.reshape(-1).view(np.uint32), z["c_ref_bits"].reshape(-1)), path
+
+
 def test_bf16_rne_against_independent_fpu_rounding():
     """Every high half (all signs, exponents, mantissas) with low halves that
     cover zero, +-1 around the halfway point and the all-ones carry case."""
