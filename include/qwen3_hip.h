@@ -155,6 +155,27 @@ int qwen3_hip_gemm_gate_up_silu_bf16a_dev(float *h_d, const uint16_t *x_d,
 int qwen3_hip_gemm_noalloc_dev(float *c_d, const float *a_d, const uint16_t *b_d,
                                int M, int K, int N);
 size_t qwen3_hip_scratch_bytes(void);
+/* The M = 1 GEMV set of one decode token for `layers` (1..32) decoder
+ * layers in ONE persistent launch: the q|k|v, o, gate, up and down calls of
+ * SRC/qwen3.c:477-540 with their Qwen3-0.6B shapes, chained as a decode step
+ * chains them when the ops between them are left out (x -> q|k|v; its q part
+ * -> o; o -> silu(gate) * up; that -> down -> x of the next layer).
+ * w: HOST array [layers][5] of device pointers, per layer q|k|v [4096][1024]
+ * (q, k, v rows stacked), o [1024][2048], gate [3072][1024], up [3072][1024],
+ * down [1024][3072] (bf16, row-major [out, in]); x0_d: layer 0's input (1024
+ * fp32); out_d: [layers][qwen3_hip_decode_set_out_ld()] fp32, per layer
+ * q|k|v at 0, o at 4096, silu(gate)*up at 5120, down at 8192.  Every output
+ * equals, bit for bit, the qwen3_hip_gemm_dev / _gate_up_silu_dev call
+ * chain on the same inputs.  Asynchronous on the library stream; may be
+ * captured into a graph.  QWEN3_HIP_ENODEV where the device cannot keep the
+ * launch's 256 workgroups resident (qwen3_hip_decode_set_supported() == 0).
+ * No counterpart in the reference ABI (its GEMMs are separate calls). */
+int qwen3_hip_decode_set_dev(const uint16_t *const *w, const float *x0_d, float *out_d, int layers);
+int qwen3_hip_decode_set_supported(void);
+int qwen3_hip_decode_set_out_ld(void);
+/* error flags of decode-set launches since the last call (synchronises):
+ * 1 = a workgroup stopped waiting for its input (results not valid) */
+int qwen3_hip_decode_set_errors(unsigned *flags);
 /* device counterpart of qwen3_op_argmax (SRC/ops.h:36-37,
  * SRC/ops_scalar.c:57-62): first index of the maximum, ties -> lowest index,
  * a NaN at index 0 wins as in the reference's strict ">" scan */

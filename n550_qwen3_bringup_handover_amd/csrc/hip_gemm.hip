@@ -1918,6 +1918,10 @@ extern "C" int qh_init(int device) {
     if (device < QH_MAX_DEVICES && !g_scratch_dev[device])
         HCHECK(hipGetSymbolAddress(&g_scratch_dev[device], HIP_SYMBOL(scratch)), QH_ERUNTIME);
     g_device = device;
+    {
+        const int rc = qh_persist_init();
+        if (rc) return rc;
+    }
     g_inited = 1;
     return QH_OK;
 }
@@ -1942,6 +1946,7 @@ extern "C" void qh_shutdown(void) {
     (void)hipFree(g_am_i);
     g_am_v = nullptr;
     g_am_i = nullptr;
+    qh_persist_shutdown();
     (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
     g_inited = 0;

@@ -1,0 +1,368 @@
+// Persistent decode step of the M = 1 GEMV set on CDNA4 (gfx950): the 4 x L
+// dependent GEMVs of L decoder layers (fused q|k|v 1024 -> 4096, o 2048 ->
+// 1024 on the q part, fused gate|up 1024 -> 2 x 3072 with silu(gate) * up,
+// down 3072 -> 1024; fpga_bringup/src/src/qwen3.c:477-540 calls them as
+// separate qwen3_gemm calls) in one launch instead of 4 x L.
+//
+// Why: each GEMV streams 4-12 MB of weights, which at ~6.5 TB/s takes
+// 0.6-1.9 us, while a dependent kernel launch costs ~1.6 us on MI355X and
+// cannot start streaming its weights before its predecessor has finished.
+// Here every workgroup stays resident for the whole step and loads the next
+// GEMV's weights while it waits for that GEMV's input, so the weight stream
+// overlaps the exchange of activations between GEMVs.
+//
+// Layout of one launch: 256 workgroups (one per CU), each 4 compute waves
+// and 1 poller wave.  Stage s of layer l has N output rows split evenly over
+// the 1024 compute waves (4, 1, 3 (gate and up) and 1 rows per wave).  A
+// compute wave holds its rows' weights in registers (lane l owns the
+// 16-byte chunks l, l+64, ... of each row, as k_gemv1 does, so every output
+// is the same sum in the same order and bit-identical to the per-call GEMV
+// path), issues the next stage's weight loads, then waits at the workgroup
+// barrier for the stage's input.
+//
+// Activations move between workgroups as 64-bit words {fp32 value, tag}
+// written with agent-scope (sc1) stores; the tag is the launch's epoch, so a
+// word is valid exactly when its tag matches and no flag, counter or cache
+// flush is needed (a 64-bit access is single-copy atomic).  Only the poller
+// wave polls: it reads every word of the stage's input with agent-scope
+// loads until all tags match (bounded: after PS_SPIN rounds it records an
+// error and goes on, so every wave always finishes), rounds the values to
+// bf16 (RNE) into an LDS buffer, and joins the barrier.  The compute waves'
+// memory counter then holds only weight loads, so waiting for one stage's
+// weights never waits for the input poll, and the poll never waits for the
+// weights.  LDS holds two input buffers: stage s reads buffer s % 2 while the
+// poller fills buffer (s + 1) % 2; one barrier per stage separates them.
+//
+// Residency: the 256 workgroups must be resident together (each waits for
+// the others' outputs).  The host checks the occupancy (one workgroup of
+// PS_THREADS threads per CU on all 256 CUs); the bounded polls guarantee
+// termination even if another stream's kernels delayed a workgroup, with
+// the error flag set.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hip_shim.h"
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+#define WAVE 64
+#define PS_CWAVES 4                          // compute waves per workgroup
+#define PS_THREADS ((PS_CWAVES + 1) * WAVE)  // + the poller wave
+#define PS_BLOCKS 256
+#define PS_GW (PS_BLOCKS * PS_CWAVES)        // compute waves of a launch
+#define PS_SPIN (1 << 15)                    // poll rounds before giving up (~30 ms)
+#define PS_LDS_U32 1536                      // one input buffer: 3072 bf16 values
+
+#define H_DIM 1024
+#define QKV_N 4096
+#define Q_N 2048
+#define I_N 3072
+
+// per-layer fp32 outputs: q|k|v (4096), o (1024), h (3072), x (1024)
+#define OUT_QKV 0
+#define OUT_O 4096
+#define OUT_H 5120
+#define OUT_X 8192
+#define OUT_LD 9216
+// per-layer exchange slots of XCH_LD words: q (2048), o (1024), h (3072), x (1024)
+#define XCH_LD 3072
+
+#define PS_MAX_LAYERS 32
+struct PersistArgs {
+    // per layer: q|k|v, o, gate, up, down (row-major bf16).  Held in the kernel
+    // arguments, so each layer's pointers come from scalar loads: a pointer
+    // fetched by a vector load would make every weight load wait for it
+    // (the memory counter is in order) and would not be known to be uniform
+    const uint16_t *w[PS_MAX_LAYERS][5];
+    const float *x0;            // input of layer 0 (1024 fp32)
+    float *out;                 // [layers][OUT_LD]
+    uint64_t *xch;              // [layers][4][XCH_LD] exchange words
+    unsigned *state;            // [0] epoch of the last launch, [1] error flags (1 = poll gave up)
+    int layers;
+};
+
+// ---- helpers (the same arithmetic as the per-call GEMV kernels) -----------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
+}
+#define AUX_NT 2       // non-temporal: each weight is read once per step
+#define AUX_SC1 16     // agent scope: coherent across the XCDs' L2 caches
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t f = {x, y};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+__device__ __forceinline__ float bf16_dot2(uint32_t w, uint32_t x, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), acc,
+                                           false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_partner(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+// sum over the 64 lanes, the same bits in every lane (as wave_sum of hip_gemm.hip)
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_partner<0xB1>(x);
+    x += dpp_partner<0x4E>(x);
+    x += dpp_partner<0x141>(x);
+    x += dpp_partner<0x140>(x);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    x = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
+}
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+// ---- compute waves -----------------------------------------------------------
+// Weights of ROWS consecutive rows (and the matching rows of b2 when GATED)
+// starting at row0, K = 512 * CPL: every row and chunk is in range (the
+// stage shapes divide evenly), so the loads are unconditional.
+template <int ROWS, int CPL, bool GATED>
+struct Wts {
+    u32x4 v[GATED ? 2 * ROWS : ROWS][CPL];
+};
+
+template <int ROWS, int CPL, bool GATED>
+__device__ __forceinline__ void load_wts(Wts<ROWS, CPL, GATED> &w, const uint16_t *b, const uint16_t *b2, int row0,
+                                         int nrows, int lane) {
+    constexpr int K = 512 * CPL;
+    const __amdgpu_buffer_rsrc_t rb = rsrc(b, (size_t)nrows * K * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = rsrc(GATED ? b2 : b, (size_t)nrows * K * 2);
+#pragma unroll
+    for (int r = 0; r < ROWS; r++)
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const uint32_t off = (uint32_t)(row0 + r) * (uint32_t)(K * 2) + (uint32_t)(lane + WAVE * j) * 16u;
+            w.v[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, AUX_NT);
+            if constexpr (GATED) w.v[ROWS + r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, AUX_NT);
+        }
+}
+
+// rows row0 .. row0+ROWS-1 of one GEMV against the bf16 input in LDS: lane r
+// returns row r's output (silu(gate) * up when GATED), other lanes garbage
+template <int ROWS, int CPL, bool GATED>
+__device__ __forceinline__ float gemv_rows(const Wts<ROWS, CPL, GATED> &w, const uint32_t *act, int lane) {
+    constexpr int NB = GATED ? 2 * ROWS : ROWS;
+    u32x4 xc[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; j++) xc[j] = reinterpret_cast<const u32x4 *>(act)[lane + WAVE * j];
+    float acc[NB];
+#pragma unroll
+    for (int r = 0; r < NB; r++) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; j++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) s = bf16_dot2(w.v[r][j][e], xc[j][e], s);
+        acc[r] = s;
+    }
+    float tot = 0.0f, up = 0.0f;
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+        const float t = wave_sum(acc[r]);
+        tot = lane == r ? t : tot;
+        if constexpr (GATED) {
+            const float u = wave_sum(acc[ROWS + r]);
+            up = lane == r ? u : up;
+        }
+    }
+    return GATED ? silu_mul(tot, up) : tot;
+}
+
+// lane r < ROWS writes row row0 + r: fp32 output, and (xch set) its
+// exchange word {value, tag}
+template <int ROWS>
+__device__ __forceinline__ void put_rows(float v, float *out, uint64_t *xch, int row0, unsigned tag, int lane) {
+    if (lane < ROWS) {
+        out[row0 + lane] = v;
+        if (xch) {
+            const uint64_t word = ((uint64_t)tag << 32) | __float_as_uint(v);
+            __hip_atomic_store(xch + row0 + lane, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// ---- poller wave -------------------------------------------------------------
+// Wait until all V words of src carry `tag` (agent-scope loads, two words
+// per 16-byte load), then store the values as bf16 pairs into act
+// (act[i] = {v[2i], v[2i+1]}).  Gives up after PS_SPIN rounds (error flag 1).
+template <int V>
+__device__ __forceinline__ void poll_input(const uint64_t *src, unsigned tag, uint32_t *act, unsigned *state,
+                                           int lane, bool &gave_up) {
+    constexpr int NL = V / 128;                 // 16-byte loads per lane
+    const __amdgpu_buffer_rsrc_t rs = rsrc(src, (size_t)V * 8);
+    u32x4 d[NL];
+#pragma unroll
+    for (int i = 0; i < NL; i++) d[i] = u32x4{0u, 0u, 0u, 0u};
+    uint32_t ready = 0;
+    const uint32_t all = (NL >= 32) ? 0xFFFFFFFFu : ((1u << NL) - 1u);
+    for (int spin = 0;; spin++) {
+#pragma unroll
+        for (int i = 0; i < NL; i++)
+            if (!(ready >> i & 1u))
+                d[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(lane + WAVE * i) * 16u, 0, AUX_SC1);
+#pragma unroll
+        for (int i = 0; i < NL; i++)
+            if (d[i].y == tag && d[i].w == tag) ready |= 1u << i;
+        if (__all(ready == all)) break;
+        if (gave_up || spin >= PS_SPIN) {     // after one give-up, no more waiting in this launch
+            if (lane == 0) atomicOr(state + 1, 1u);
+            gave_up = true;
+            break;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NL; i++)
+        act[lane + WAVE * i] = pack_bf16x2(__uint_as_float(d[i].x), __uint_as_float(d[i].z));
+}
+
+// the first layer's input: plain fp32, written before the launch
+__device__ __forceinline__ void load_input(const float *x0, uint32_t *act, int lane) {
+    const __amdgpu_buffer_rsrc_t rx = rsrc(x0, H_DIM * 4);
+#pragma unroll
+    for (int i = 0; i < H_DIM / (4 * WAVE); i++) {
+        const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rx, (uint32_t)(lane + WAVE * i) * 16u, 0, 0));
+        act[2 * (lane + WAVE * i)] = pack_bf16x2(v.x, v.y);
+        act[2 * (lane + WAVE * i) + 1] = pack_bf16x2(v.z, v.w);
+    }
+}
+
+__global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p) {
+    __shared__ __align__(16) uint32_t act[2][PS_LDS_U32];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const unsigned tag = __hip_atomic_load(p.state, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+
+    if (wave == PS_CWAVES) {
+        // ---- poller: one input per stage, then the barrier -----------------
+        bool gave_up = false;
+        for (int l = 0; l < p.layers; l++) {
+            const uint64_t *x = p.xch + (size_t)l * 4 * XCH_LD;
+            if (l == 0) load_input(p.x0, act[0], lane);
+            else poll_input<H_DIM>(x - XCH_LD, tag, act[0], p.state, lane, gave_up);   // x of layer l-1
+            __syncthreads();
+            poll_input<Q_N>(x, tag, act[1], p.state, lane, gave_up);                   // q
+            __syncthreads();
+            poll_input<H_DIM>(x + XCH_LD, tag, act[0], p.state, lane, gave_up);        // o
+            __syncthreads();
+            poll_input<I_N>(x + 2 * XCH_LD, tag, act[1], p.state, lane, gave_up);      // h
+            __syncthreads();
+        }
+    } else {
+        // ---- compute waves ------------------------------------------------
+        const int gw = blockIdx.x * PS_CWAVES + wave;     // 0 .. 1023
+        Wts<4, 2, false> wa;    // q|k|v: rows 4gw .. 4gw+3 of 4096, K 1024
+        Wts<1, 4, false> wb;    // o: row gw of 1024, K 2048
+        Wts<3, 2, true> wc;     // gate|up: rows 3gw .. 3gw+2 of 3072, K 1024
+        Wts<1, 6, false> wd;    // down: row gw of 1024, K 3072
+        load_wts(wa, p.w[0][0], nullptr, 4 * gw, QKV_N, lane);
+        for (int l = 0; l < p.layers; l++) {
+            const uint16_t *const *wl = p.w[l];
+            float *out = p.out + (size_t)l * OUT_LD;
+            uint64_t *x = p.xch + (size_t)l * 4 * XCH_LD;
+            load_wts(wb, wl[1], nullptr, gw, H_DIM, lane);
+            __syncthreads();
+            float v = gemv_rows(wa, act[0], lane);
+            put_rows<4>(v, out + OUT_QKV, 4 * gw < Q_N ? x : nullptr, 4 * gw, tag, lane);
+
+            load_wts(wc, wl[2], wl[3], 3 * gw, I_N, lane);
+            __syncthreads();
+            v = gemv_rows(wb, act[1], lane);
+            put_rows<1>(v, out + OUT_O, x + XCH_LD, gw, tag, lane);
+
+            load_wts(wd, wl[4], nullptr, gw, H_DIM, lane);
+            __syncthreads();
+            v = gemv_rows(wc, act[0], lane);
+            put_rows<3>(v, out + OUT_H, x + 2 * XCH_LD, 3 * gw, tag, lane);
+
+            // the next layer's q|k|v, unconditionally: after the last layer the
+            // resource is empty (its loads read zeros and touch no memory), so
+            // the compiler counts the loads exactly and stage D waits for its
+            // own weights only
+            const bool more = l + 1 < p.layers;
+            load_wts(wa, p.w[more ? l + 1 : l][0], nullptr, 4 * gw, more ? QKV_N : 0, lane);
+            __syncthreads();
+            v = gemv_rows(wd, act[1], lane);
+            put_rows<1>(v, out + OUT_X, x + 3 * XCH_LD, gw, tag, lane);
+        }
+    }
+    // every workgroup read the epoch before producing anything, and workgroup
+    // 0 gets here only after every workgroup's last outputs reached it
+    if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(p.state, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- host side ------------------------------------------------------------------
+static uint64_t *g_xch = nullptr;     // [PS_MAX_LAYERS][4][XCH_LD] exchange words
+static unsigned *g_state = nullptr;   // epoch, error flags
+static int g_ps_ok = 0;               // 1 = the device keeps the grid resident
+
+// at library init (device current): the exchange words start at tag 0,
+// which no launch uses
+extern "C" int qh_persist_init(void) {
+    int dev = 0, cus = 0, nb = 0;
+    g_ps_ok = hipGetDevice(&dev) == hipSuccess &&
+              hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+              hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_decode_persist, PS_THREADS, 0) == hipSuccess &&
+              cus == PS_BLOCKS && nb >= 1;
+    (void)hipGetLastError();
+    const size_t xb = (size_t)PS_MAX_LAYERS * 4 * XCH_LD * sizeof(uint64_t);
+    if (hipMalloc((void **)&g_xch, xb) != hipSuccess || hipMalloc((void **)&g_state, 64) != hipSuccess ||
+        hipMemset(g_xch, 0, xb) != hipSuccess || hipMemset(g_state, 0, 64) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        (void)hipGetLastError();
+        return QH_ENOMEM;
+    }
+    return QH_OK;
+}
+
+extern "C" void qh_persist_shutdown(void) {
+    (void)hipFree(g_xch);
+    (void)hipFree(g_state);
+    g_xch = nullptr;
+    g_state = nullptr;
+    g_ps_ok = 0;
+}
+
+extern "C" int qh_persist_supported(void) { return g_ps_ok; }
+extern "C" int qh_persist_out_ld(void) { return OUT_LD; }
+
+extern "C" int qh_decode_persist(const uint16_t *const *w, const float *x0_d, float *out_d, int layers) {
+    if (!w || !x0_d || !out_d || layers < 1) return QH_EINVAL;
+    if (layers > PS_MAX_LAYERS) return QH_ETOOBIG;
+    if (!g_xch || !g_ps_ok) return QH_ENODEV;
+    PersistArgs a;
+    for (int l = 0; l < PS_MAX_LAYERS; l++)
+        for (int k = 0; k < 5; k++) {
+            a.w[l][k] = l < layers ? w[5 * l + k] : nullptr;
+            if (l < layers && !a.w[l][k]) return QH_EINVAL;
+        }
+    a.x0 = x0_d;
+    a.out = out_d;
+    a.xch = g_xch;
+    a.state = g_state;
+    a.layers = layers;
+    hipLaunchKernelGGL(k_decode_persist, dim3(PS_BLOCKS), dim3(PS_THREADS), 0, (hipStream_t)qh_stream(), a);
+    return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
+}
+
+// error flags raised by launches since the last call (synchronises the stream)
+extern "C" int qh_persist_errors(unsigned *flags) {
+    if (!g_state || !flags) return QH_ESTATE;
+    unsigned h[2] = {0u, 0u};
+    if (hipStreamSynchronize((hipStream_t)qh_stream()) != hipSuccess ||
+        hipMemcpy(h, g_state, sizeof h, hipMemcpyDeviceToHost) != hipSuccess) {
+        (void)hipGetLastError();
+        return QH_ERUNTIME;
+    }
+    *flags = h[1];
+    if (h[1] && hipMemset(g_state + 1, 0, sizeof(unsigned)) != hipSuccess) {
+        (void)hipGetLastError();
+        return QH_ERUNTIME;
+    }
+    return QH_OK;
+}

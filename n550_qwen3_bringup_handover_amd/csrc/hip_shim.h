@@ -60,6 +60,23 @@ int qh_gemm_split(float *c_d, const float *a_d, const uint16_t *b_d, int M, int 
  * more workspace than the array holds.  Results equal qh_gemm's. */
 int qh_gemm_noalloc(float *c_d, const float *a_d, const uint16_t *b_d, int M, int K, int N);
 size_t qh_scratch_bytes(void);
+/* The M = 1 GEMV set of `layers` (<= 32) decoder layers in one persistent
+ * launch (hip_persist.hip): w = HOST array [layers][5] of device pointers to
+ * q|k|v [4096][1024],
+ * o [1024][2048], gate [3072][1024], up [3072][1024], down [1024][3072];
+ * layer 0 reads x0 (1024 fp32), layer l > 0 the previous down output, o
+ * reads the q part; out_d = [layers][qh_persist_out_ld()] fp32: q|k|v, o,
+ * silu(gate)*up, down at 0, 4096, 5120, 8192.  Outputs equal the per-call
+ * GEMV kernels' bit for bit.  QH_ENODEV if the device cannot keep the grid
+ * resident (256 CUs, one workgroup each). */
+int qh_decode_persist(const uint16_t *const *w, const float *x0_d, float *out_d, int layers);
+int qh_persist_supported(void);
+int qh_persist_out_ld(void);
+/* error flags of launches since the last call (1 = an input poll gave up);
+ * synchronises the stream */
+int qh_persist_errors(unsigned *flags);
+int qh_persist_init(void);
+void qh_persist_shutdown(void);
 /* name of the plan the last GEMM call launched */
 const char *qh_last_plan(void);
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */

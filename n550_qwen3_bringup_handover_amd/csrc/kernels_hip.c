@@ -506,6 +506,19 @@ int qwen3_hip_gemm_gate_up_silu_bf16a_dev(float *h, const uint16_t *x, const uin
     return note(qh_gemm_gate_up_silu_bf16a(h, x, wg, wu, M, K, N));
 }
 
+int qwen3_hip_decode_set_dev(const uint16_t *const *w, const float *x0, float *out, int layers) {
+    READY_OR_RETURN();
+    return note(qh_decode_persist(w, x0, out, layers));
+}
+
+int qwen3_hip_decode_set_supported(void) { return ensure_ready() == 0 && qh_persist_supported(); }
+int qwen3_hip_decode_set_out_ld(void) { return qh_persist_out_ld(); }
+
+int qwen3_hip_decode_set_errors(unsigned *flags) {
+    READY_OR_RETURN();
+    return note(qh_persist_errors(flags));
+}
+
 int qwen3_hip_argmax_dev(int *out, const float *v, int n) {
     READY_OR_RETURN();
     return note(qh_argmax(out, v, n));

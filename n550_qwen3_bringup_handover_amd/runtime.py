@@ -61,6 +61,10 @@ _PROTOS = {
     "qwen3_hip_scratch_bytes": (ctypes.c_size_t, []),
     "qwen3_hip_gemm_bf16a_dev": (ctypes.c_int, [VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_gemm_gate_up_silu_bf16a_dev": (ctypes.c_int, [VP, VP, VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "qwen3_hip_decode_set_dev": (ctypes.c_int, [ctypes.POINTER(VP), VP, VP, ctypes.c_int]),
+    "qwen3_hip_decode_set_supported": (ctypes.c_int, []),
+    "qwen3_hip_decode_set_out_ld": (ctypes.c_int, []),
+    "qwen3_hip_decode_set_errors": (ctypes.c_int, [ctypes.POINTER(ctypes.c_uint)]),
     "qwen3_hip_argmax_dev": (ctypes.c_int, [VP, VP, ctypes.c_int]),
     "qwen3_hip_tile_to_row_dev": (ctypes.c_int, [VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_copy_dev": (ctypes.c_int, [VP, VP, ctypes.c_size_t]),

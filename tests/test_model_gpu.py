@@ -470,3 +470,83 @@ def test_longest_context(blob):
     err = float(np.abs(l_fwd.astype(np.float64) - l_gen).max())
     print(f"context 8191: decode vs forward max abs logit diff {err:.3e}", flush=True)
     assert err <= LOGIT_TOL
+
+
+def _logits_err(got, ref):
+    return float(np.abs(got.astype(np.float64) - ref.astype(np.float64)).max())
+
+
+def test_p128_d128_decode_step_logits(model):
+    """The 128-token prompt, then the reference's own tokens fed one decode
+    step at a time: the logits after decode steps 1, 32, 64 and 128 against
+    the reference's (model_p128_d128_logits.npz), not only the tokens."""
+    fx = fixture("p128_d128_logits")
+    prompt, toks = fx["prompt"], fx["tokens"]
+    _forward_all(model, prompt)
+    worst = _logits_err(model.logits(), fx["prefill_logits"])
+    assert worst <= LOGIT_TOL
+    steps = [int(s) for s in fx["log_steps"]]
+    for i in range(1, max(steps) + 1):
+        model.forward([toks[i - 1]], len(prompt) + i - 1)
+        if i in steps:
+            err = _logits_err(model.logits(), fx["step_logits"][steps.index(i)])
+            print(f"decode step {i}: max abs logit diff {err:.3e}", flush=True)
+            worst = max(worst, err)
+            assert err <= LOGIT_TOL, (i, err)
+    print(f"p128_d128 decode-step logits: worst {worst:.3e}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def long_model(blob):
+    m = M.Model(blob, max_seq=2048)
+    yield m
+    m.close()
+
+
+def test_long_context_matches_reference(long_model):
+    """A 1,100-token prompt against the reference forward built with its own
+    2048-position cache (qwen3.c with -DQWEN3_MAX_SEQ=2048): the last prefill
+    row's logits, the logits after decode steps 1, 4 and 8 (the reference's
+    tokens fed), and the greedy tokens -- RoPE angles, the cache layout and
+    both attention kernels past position 1024 pinned to the reference."""
+    fx = fixture("long")
+    prompt, toks = fx["prompt"], fx["tokens"]
+    m = long_model
+    _forward_all(m, prompt)
+    err = _logits_err(m.logits(), fx["prefill_logits"])
+    print(f"1100-token prefill: max abs logit diff {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert m.argmax() == toks[0] or fx["margins"][0] < TIE_TOL
+    steps = [int(s) for s in fx["log_steps"]]
+    for i in range(1, max(steps) + 1):
+        m.forward([toks[i - 1]], len(prompt) + i - 1)
+        if i in steps:
+            err = _logits_err(m.logits(), fx["step_logits"][steps.index(i)])
+            print(f"decode step {i} (position {len(prompt) + i - 1}): max abs logit diff {err:.3e}", flush=True)
+            assert err <= LOGIT_TOL, (i, err)
+    got = m.generate(prompt, len(toks) - 1)
+    assert_tokens(got, fx, "long")
+
+
+def test_long_context_inside_a_batch(long_model):
+    """The same 1,100-token prompt as sequence 1 of a batch of three (the
+    others short): its greedy tokens equal the reference's, and its logits
+    after the eighth decode step equal the reference's step-8 logits."""
+    fx = fixture("long")
+    fb = fixture("batch")
+    lens = [int(v) for v in fb["prompt_lens"]]
+    short0 = fb["prompts"][:lens[0]]
+    short2 = fb["prompts"][lens[0]:lens[0] + lens[1]]
+    n_dec = len(fx["tokens"]) - 1
+    with M.Batch(long_model, 3, 1200) as b:
+        b.prefill(0, short0)
+        b.prefill(1, fx["prompt"])
+        b.prefill(2, short2)
+        out = b.decode(n_dec)
+        lb = b.logits()
+    j = _check_row(out[1], fx["tokens"], fx["margins"], "batch seq 1 (1100-token prompt)")
+    if j == len(fx["tokens"]):
+        steps = [int(s) for s in fx["log_steps"]]
+        err = _logits_err(lb[1], fx["step_logits"][steps.index(n_dec)])
+        print(f"batch seq 1, decode step {n_dec}: max abs logit diff {err:.3e}", flush=True)
+        assert err <= LOGIT_TOL
