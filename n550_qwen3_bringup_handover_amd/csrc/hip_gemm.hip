@@ -53,6 +53,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
 }
 #define BUF_OOB 0x80000000u      // an offset past every buffer below 2 GiB
+#define AUX_SC1 16               // buffer-op cache policy: agent scope, coherent across the XCDs' L2s
 
 // w.lo * x.lo + w.hi * x.hi + acc for two packed bf16 pairs (v_dot2_f32_bf16)
 __device__ __forceinline__ float bf16_dot2(uint32_t w, uint32_t x, float acc) {
@@ -1843,6 +1844,181 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// Narrow GEMM for M <= 64 and K-heavy shapes (o, down of a decode batch)
+// ---------------------------------------------------------------------------
+// blockIdx.y owns 32 columns of C (two 16-column MFMA tiles) and all 16 MT
+// rows, blockIdx.x a K slice of KSL = 128 * KPW (slice-major, so with a
+// multiple of 8 slices each XCD reads one slice of A).  Every thread issues
+// all of its loads at once: the block's slice of A first (from L2), then its
+// wave's weights (from HBM); the slice is rounded to bf16 (RNE) into LDS
+// (16-byte chunks XOR-swizzled by row) while the weights are in flight.  The
+// four waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
+// their partial tiles are added through LDS in wave order.  With one slice
+// the block writes C.  With several, each block writes its slice sums
+// [slice][M][N] with agent-scope (write-through) stores, waits for them, and
+// takes a ticket from its column block's counter; the block that draws the
+// last ticket reads every slice's sums (agent-scope loads), adds them in
+// slice order -- deterministic, whatever the arrival order -- writes C and
+// resets the counter to zero for the next call.  No block waits for another
+// and there is no second launch.  Loads past M and N read zeros at
+// out-of-range offsets.
+#define NARROW_COLS 32
+template <int MT, int KPW>
+__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
+                                                            unsigned *__restrict__ cnt,
+                                                            const float *__restrict__ a,
+                                                            const uint16_t *__restrict__ b, int M, int K, int N) {
+    constexpr int KSL = 128 * KPW, CH = KSL / 8;         // slice depth, 16-byte chunks per row
+    constexpr int NT = NARROW_COLS / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
+    static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
+    __shared__ __align__(16) u32x4 sa[ROWS * CH];
+    __shared__ __align__(16) float red[NW][ROWS][NARROW_COLS + 4];   // +4: conflict-free column writes
+    __shared__ unsigned last_s;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int k0 = blockIdx.x * KSL, ks = gridDim.x;
+    const int n0 = blockIdx.y * NARROW_COLS;
+    const size_t MN = (size_t)M * N;
+
+    // 1. every load at once: first the block's A slice (rows past M read
+    //    zeros; it comes from L2), then this wave's weights (rows
+    //    n0 + 16 nt + r16, k = k0 + 32 (KPW w + s) + 8 g; from HBM), so that the
+    //    slice is rounded into LDS while the weights are still in flight
+    constexpr int PER = ROWS * CH / NTHREADS;             // 32-byte pieces of A per thread
+    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PER + NT * KPW <= 63, "loads in flight");
+    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
+    u32x4 lo[PER], hi[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int q = tid + NTHREADS * i;
+        const int m = q / CH, ch = q % CH;
+        const uint32_t off = (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4);
+        lo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
+        hi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off + 16u : BUF_OOB, 0, 0);
+    }
+    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
+    u32x4 bq[NT][KPW];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+        const int n = n0 + 16 * nt + r16;
+        const uint32_t base = (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * g) * 2);
+#pragma unroll
+        for (int s = 0; s < KPW; s++)
+            bq[nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, n < N ? base + 64u * s : BUF_OOB, 0, 2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. A rounded to bf16 (RNE) into LDS
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int q = tid + NTHREADS * i;
+        const int m = q / CH, ch = q % CH;
+        u32x4 v;
+        v.x = pack_bf16x2(__uint_as_float(lo[i].x), __uint_as_float(lo[i].y));
+        v.y = pack_bf16x2(__uint_as_float(lo[i].z), __uint_as_float(lo[i].w));
+        v.z = pack_bf16x2(__uint_as_float(hi[i].x), __uint_as_float(hi[i].y));
+        v.w = pack_bf16x2(__uint_as_float(hi[i].z), __uint_as_float(hi[i].w));
+        sa[m * CH + (ch ^ (m & 15))] = v;
+    }
+    __syncthreads();
+
+    // 3. MFMA over this wave's steps: A fragment rows 16 mt + r16, chunk 4 (KPW w + s) + g
+    f32x4 acc[NT][MT];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KPW; s++) {
+        bf16x8 af[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int m = 16 * mt + r16;
+            af[mt] = __builtin_bit_cast(bf16x8, sa[m * CH + ((4 * (KPW * w + s) + g) ^ (m & 15))]);
+        }
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], __builtin_bit_cast(bf16x8, bq[nt][s]),
+                                                                      acc[nt][mt], 0, 0, 0);
+    }
+
+    // 4. wave partials -> LDS: lane holds rows 16 mt + 4 g + r, column 16 nt + r16
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[w][16 * mt + 4 * g + r][16 * nt + r16] = acc[nt][mt][r];
+    __syncthreads();
+
+    // 5. quads of 4 columns, q = tid + NTHREADS i: row q / 8, columns 4 (q % 8) .. +3,
+    //    summed over the waves in order; N % 4 == 0, so a quad is wholly in or out
+    constexpr int NQ = ROWS * NARROW_COLS / 4, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
+    static_assert(NQ % NTHREADS == 0 || NQ < NTHREADS, "quads per thread");
+    f32x4 v[QPT];
+    uint32_t coff[QPT];                                   // byte offset of the quad in C, or BUF_OOB
+#pragma unroll
+    for (int i = 0; i < QPT; i++) {
+        const bool live = tid + NTHREADS * i < NQ;        // MT = 1: half of the threads
+        const int q = live ? tid + NTHREADS * i : 0;
+        const int m = q >> 3, cq = 4 * (q & 7), n = n0 + cq;
+        f32x4 t = *reinterpret_cast<const f32x4 *>(&red[0][m][cq]);
+#pragma unroll
+        for (int ww = 1; ww < NW; ww++) t += *reinterpret_cast<const f32x4 *>(&red[ww][m][cq]);
+        v[i] = t;
+        coff[i] = (live && m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
+    }
+    const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, MN * 4);
+    if (ks == 1) {
+#pragma unroll
+        for (int i = 0; i < QPT; i++)
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rc, coff[i], 0, 0);
+        return;
+    }
+    // 6. slice sums out (write-through, agent scope), then a ticket; the last
+    //    block adds the slices
+    const __amdgpu_buffer_rsrc_t rp = xl_rsrc(part, (size_t)ks * MN * 4);
+    const uint32_t sl_bytes = (uint32_t)(MN * 4);
+#pragma unroll
+    for (int i = 0; i < QPT; i++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rp,
+                                               coff[i] == BUF_OOB ? BUF_OOB : coff[i] + blockIdx.x * sl_bytes, 0,
+                                               AUX_SC1);
+    __builtin_amdgcn_s_waitcnt(0);                        // this thread's sums have landed
+    __syncthreads();                                      // ... and every thread's
+    if (tid == 0)
+        last_s = __hip_atomic_fetch_add(cnt + blockIdx.y, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)ks - 1u;
+    __syncthreads();
+    if (!last_s) return;                                  // uniform over the block
+    f32x4 sum[QPT];
+#pragma unroll
+    for (int i = 0; i < QPT; i++)
+        sum[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, coff[i], 0, AUX_SC1));
+    for (int sl0 = 1; sl0 < ks; sl0 += 8) {               // 8 slices of every quad in flight, added in order
+        u32x4 t[QPT][8];
+#pragma unroll
+        for (int i = 0; i < QPT; i++)
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                t[i][u] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rp, (coff[i] == BUF_OOB || sl0 + u >= ks) ? BUF_OOB : coff[i] + (uint32_t)(sl0 + u) * sl_bytes,
+                    0, AUX_SC1);
+#pragma unroll
+        for (int i = 0; i < QPT; i++)
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (sl0 + u < ks) sum[i] += __builtin_bit_cast(f32x4, t[i][u]);
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; i++)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[i]), rc, coff[i], 0, 0);
+    if (tid == 0) __hip_atomic_store(cnt + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // host side of the shim
 // ---------------------------------------------------------------------------
 static int g_inited = 0;
@@ -1874,11 +2050,18 @@ static int g_cus = 256;            // compute units of the device (set at init)
 #define PART_INIT_BYTES ((size_t)32 << 20)
 static float *g_part = nullptr;    // split-K partial sums of the large-tile GEMM (grown on demand)
 static size_t g_part_bytes = 0;
+// tickets of the narrow kernel's K split, one per 32-column block: zero
+// between calls (each call's last block resets the ones it used)
+#define NARROW_CNT 2048
+static unsigned *g_cnt = nullptr;
 static const size_t ABF_INIT_ELEMS = (size_t)8192 * 3072;   // 48 MiB: M x K up to 8192 x 3072
 
 // the no-allocation entry point's workspace (see qh_gemm_noalloc)
 #define QH_SCRATCH_BYTES ((size_t)32 << 20)
 __device__ __align__(256) unsigned char scratch[QH_SCRATCH_BYTES];
+// its last NARROW_CNT words hold the narrow kernel's tickets (zeroed at init);
+// the rest is the bf16 copy of A or the slice sums
+#define QH_SCRATCH_WS_BYTES (QH_SCRATCH_BYTES - NARROW_CNT * sizeof(unsigned))
 #define QH_MAX_DEVICES 64
 static void *g_scratch_dev[QH_MAX_DEVICES];   // per device: its copy of `scratch`
 
@@ -1924,10 +2107,15 @@ extern "C" int qh_init(int device) {
     // (e.g. 4 slices x 1024 x 1024 fp32); grown outside graph capture if needed
     HCHECK(hipMalloc((void **)&g_part, PART_INIT_BYTES), QH_ENOMEM);
     g_part_bytes = PART_INIT_BYTES;
+    HCHECK(hipMalloc((void **)&g_cnt, NARROW_CNT * sizeof(unsigned)), QH_ENOMEM);
+    HCHECK(hipMemset(g_cnt, 0, NARROW_CNT * sizeof(unsigned)), QH_ERUNTIME);
     // the no-allocation entry point's workspace: this device's copy of the
     // file-scope array (device current here)
     if (device < QH_MAX_DEVICES && !g_scratch_dev[device])
         HCHECK(hipGetSymbolAddress(&g_scratch_dev[device], HIP_SYMBOL(scratch)), QH_ERUNTIME);
+    if (device < QH_MAX_DEVICES)
+        HCHECK(hipMemset((unsigned char *)g_scratch_dev[device] + QH_SCRATCH_WS_BYTES, 0,
+                         NARROW_CNT * sizeof(unsigned)), QH_ERUNTIME);
     g_device = device;
     {
         const int rc = qh_persist_init();
@@ -1953,6 +2141,8 @@ extern "C" void qh_shutdown(void) {
     (void)hipFree(g_part);
     g_part = nullptr;
     g_part_bytes = 0;
+    (void)hipFree(g_cnt);
+    g_cnt = nullptr;
     (void)hipFree(g_am_v);
     (void)hipFree(g_am_i);
     g_am_v = nullptr;
@@ -2071,14 +2261,17 @@ enum {
     PLAN_STREAM_KS8 = 21,
     // skinny M <= 64: A slice staged in LDS, K split over blocks (K % 64 == 0)
     PLAN_SKINNY = 22,
-    PLAN_COUNT = 23
+    // narrow M <= 64 (K % 128 == 0): 32-column blocks, K split over blocks and
+    // the slices added inside the same launch
+    PLAN_NARROW = 23,
+    PLAN_COUNT = 24
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
     "pipe32x64k128s4", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
-    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny"};
+    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
@@ -2089,6 +2282,12 @@ static inline int stream_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 static inline bool stream_fits(int M, int K, int N) {
     return M >= 1 && M <= 64 && K > 0 && K % 256 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
            (size_t)N * K * 2 < (1ull << 31);
+}
+// the narrow kernel's limits: M <= 64, whole 128-deep slices, whole quads of
+// columns, byte offsets below 2 GiB, a ticket per 32-column block
+static inline bool narrow_fits(int M, int K, int N) {
+    return M >= 1 && M <= 64 && K > 0 && K % 128 == 0 && N % 4 == 0 && (N + NARROW_COLS - 1) / NARROW_COLS <= NARROW_CNT &&
+           (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31);
 }
 // k steps of 32 per wave (KS must divide K/256, and the A fragments, 4*MT*KS
 // registers, must fit in 64): no K split while there are >= 128 tiles of 16
@@ -2128,11 +2327,22 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
-    // K-heavy, narrow shapes at M <= 64 (o and down of batched decode): the
-    // skinny kernel, A slices staged once per block and K split over blocks
-    // (measured on MI355X: 64x3072x1024 13.6 -> 10.1 us, 48x2048x1024
-    // 10.0 -> 8.9 us, 16x3072x1024 8.1 -> 6.4 us); at K = 1024 the slices'
-    // partial sums cost more than they save
+    // K-heavy, narrow shapes at 16 < M <= 64 (o and down of batched decode),
+    // and 16 < M <= 32 at K = 1024: the narrow kernel, K split over 32-column
+    // blocks and the slices added in the same launch (measured on MI355X,
+    // graph-replayed: 64x3072x1024 9.7 -> 7.7 us, 64x2048x1024 9.3 -> 7.4,
+    // 32x3072x1024 7.2 -> 6.1, 32x1024x2048 6.9 -> 5.6; at M <= 16 and N =
+    // 1024 the skinny kernel below is 0.2-0.3 us faster, at M = 48, 64 and
+    // K = 1024 the 32x64 tiles are 0.6-1.3 us faster)
+    if (!gated && narrow_fits(M, K, N) && M > 16 && N >= 512 &&
+        ((K >= 2048 && K <= 4096 && N <= 2048) || (M <= 32 && K >= 1024 && N <= 4096)))
+        return PLAN_NARROW;
+    if (!gated && narrow_fits(M, K, N) && K >= 2048 && K <= 4096 && N > 1024 && N <= 2048)
+        return PLAN_NARROW;   // M <= 16 (16x3072x2048: 7.7 -> 6.4 us)
+    // the rest of them at M <= 64: the skinny kernel, A slices staged once
+    // per block and K split over blocks, the slices added by a second launch
+    // (measured on MI355X: 16x3072x1024 8.1 -> 5.5 us against the tiles); at
+    // K = 1024 the slices' partial sums cost more than they save
     if (!gated && M <= 64 && K >= 2048 && K <= 4096 && K % 64 == 0 && N <= 2048 &&
         (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31))
         return PLAN_SKINNY;
@@ -2390,6 +2600,7 @@ struct Ws {
     float *part;
     size_t part_bytes;
     bool grow;
+    unsigned *cnt;     // NARROW_CNT zeroed tickets (narrow plan)
 };
 
 // A captured graph keeps the device addresses it was recorded with.  Each
@@ -2475,7 +2686,7 @@ static bool abf_ensure(Ws &ws, size_t n) {
     return true;
 }
 
-static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, true}; }
+static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, true, g_cnt}; }
 
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
@@ -2590,6 +2801,59 @@ static int launch_skinny(const Ws &ws, float *c, const float *a, const uint16_t 
     }
 }
 
+// its slice depth, 128 * kpw: the deepest slice that still gives every CU a
+// block, else the shallowest that divides K (kpw <= 6: the bf16 A slice of
+// 64 rows fits 96 KB of LDS)
+static int narrow_kpw(int K, int N) {
+    static const int opts[] = {6, 4, 3, 2, 1};
+    const long ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
+    int best = 0;
+    for (int kpw : opts) {
+        if (K % (128 * kpw)) continue;
+        best = kpw;
+        if (ncb * (K / (128 * kpw)) >= g_cus) return kpw;
+    }
+    return best;
+}
+static inline size_t narrow_part_bytes(int M, int K, int N) {
+    const int kpw = narrow_kpw(K, N);
+    const int ks = kpw > 0 ? K / (128 * kpw) : 0;
+    return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+}
+template <int MT, int KPW>
+static int launch_narrow_t(const Ws &ws, float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    const int ks = K / (128 * KPW), ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
+    float *part = nullptr;
+    if (ks > 1) {
+        if ((size_t)ks * M * N * sizeof(float) > ws.part_bytes || !ws.cnt) return QH_ETOOBIG;
+        part = use_part(ws);
+    }
+    hipLaunchKernelGGL((k_gemm_narrow<MT, KPW>), dim3((unsigned)ks, (unsigned)ncb), dim3(NTHREADS), 0, g_stream,
+                       c, part, ws.cnt, a, b, M, K, N);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+// narrow GEMM: sizes within narrow_fits, 16-byte aligned a and b, and the
+// slice sums within ws (checked by the caller)
+static int launch_narrow(const Ws &ws, float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    const int kpw = narrow_kpw(K, N);
+#define QH_NARROW_CASES(MT)                                                      \
+    switch (kpw) {                                                               \
+        case 1: return launch_narrow_t<MT, 1>(ws, c, a, b, M, K, N);             \
+        case 2: return launch_narrow_t<MT, 2>(ws, c, a, b, M, K, N);             \
+        case 3: return launch_narrow_t<MT, 3>(ws, c, a, b, M, K, N);             \
+        case 4: return launch_narrow_t<MT, 4>(ws, c, a, b, M, K, N);             \
+        case 6: return launch_narrow_t<MT, 6>(ws, c, a, b, M, K, N);             \
+        default: return QH_EINVAL;                                               \
+    }
+    switch (stream_mt(M)) {
+        case 1: QH_NARROW_CASES(1)
+        case 2: QH_NARROW_CASES(2)
+        default: QH_NARROW_CASES(4)
+    }
+#undef QH_NARROW_CASES
+}
+
 template <bool GATED>
 static int launch_stream(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N, int ks) {
@@ -2656,6 +2920,9 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
+        case PLAN_NARROW:
+            if constexpr (GATED) return QH_EINVAL;
+            else return launch_narrow(ws, c, a, b, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -2692,6 +2959,18 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
             plan = PLAN_T64x64;
         } else if (ks <= 0) {
             plan = PLAN_T64x64;
+        }
+    }
+    if (plan == PLAN_NARROW) {
+        // not gated; the slice sums need room in the workspace
+        if (gated || !narrow_fits(M, K, N) || narrow_kpw(K, N) <= 0) {
+            plan = PLAN_T64x64;
+        } else {
+            const size_t part = narrow_part_bytes(M, K, N);
+            if (part && (!ws.cnt || !part_ensure(ws, part))) {
+                if (strict) return -QH_ETOOBIG;
+                plan = PLAN_T64x64;
+            }
         }
     }
     if (is_stream_plan(plan)) {
@@ -2777,15 +3056,18 @@ extern "C" const char *qh_last_plan(void) { return k_plan_names[g_last_plan]; }
 // QH_ETOOBIG, and nothing is allocated or freed.  Host code reaches the array
 // only through the per-device address hipGetSymbolAddress returned at init
 // (g_scratch_dev), never through its name.  Every plan writes all of the
-// workspace it reads, so nothing needs clearing between calls; calls that
-// overlap on one GPU (another stream, another process's graph) race on it.
+// workspace it reads, except the narrow plan's tickets in the array's last
+// NARROW_CNT words: zeroed at init, and each call leaves the ones it used at
+// zero again, so nothing needs clearing between calls.  Calls that overlap on
+// one GPU (another stream, another process's graph) race on the array.
 extern "C" size_t qh_scratch_bytes(void) { return QH_SCRATCH_BYTES; }
 
 extern "C" int qh_gemm_noalloc(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
     if (!g_inited) return QH_ESTATE;
     void *s = g_scratch_dev[g_device];
     if (!s) return QH_ESTATE;
-    const Ws ws{(uint16_t *)s, QH_SCRATCH_BYTES / sizeof(uint16_t), (float *)s, QH_SCRATCH_BYTES, false};
+    const Ws ws{(uint16_t *)s, QH_SCRATCH_WS_BYTES / sizeof(uint16_t), (float *)s, QH_SCRATCH_WS_BYTES, false,
+                (unsigned *)((unsigned char *)s + QH_SCRATCH_WS_BYTES)};
     return gemm_common(ws, true, c, a, b, nullptr, M, K, N, false);
 }
 
@@ -2795,7 +3077,9 @@ extern "C" int qh_gemm_noalloc(float *c, const float *a, const uint16_t *b, int 
 // launch.  Taken where the automatic plan is the skinny kernel, and for
 // M <= 128, K >= 2048, N <= 2048, where the kernel in 64-row slabs ties or
 // beats the 32x64 tiles once the reduction launch is gone (measured at
-// M = 96 / 128: down 13.2 / 13.2 -> ~9 us, o 9.6 / 9.8 -> ~6.5 us).
+// M = 96 / 128: down 13.2 / 13.2 -> ~9 us, o 9.6 / 9.8 -> ~6.5 us) -- but
+// not where the automatic plan is the narrow kernel, which adds its slices
+// in the same launch.
 // Otherwise C is written and *ks = 0.  The partials last until the next call
 // that uses the workspace.
 extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M, int K, int N,
@@ -2805,8 +3089,9 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     *ks = 0;
     if (!g_inited) return QH_ESTATE;
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
-    const bool take = vec && !g_forced_plan &&
-                      (choose_plan(M, K, N, false, vec) == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
+    const int auto_plan = vec ? choose_plan(M, K, N, false, vec) : PLAN_SCALAR64;
+    const bool take = vec && !g_forced_plan && auto_plan != PLAN_NARROW &&
+                      (auto_plan == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
     Ws ws = lib_ws();
     if (take && M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
         (size_t)N * K * 2 < (1ull << 31)) {

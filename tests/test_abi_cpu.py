@@ -48,7 +48,8 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (64, H, V, False, "stream"),                                  # lm_head of a 64-sequence batch
     (32, H, V, False, "stream"),
     (4096, H, Q + 2 * KV, False, "xl256x256"), (8192, H, Q + 2 * KV, False, "xb256x256s1"),
-    (64, Q, H, False, "skinny"), (64, I, H, False, "skinny"),     # o, down at M = 64
+    (64, Q, H, False, "narrow"), (64, I, H, False, "narrow"),     # o, down at M = 64
+    (16, I, H, False, "skinny"), (32, H, Q, False, "narrow"),
     (64, H, Q + 2 * KV, False, "pipe32x64k128s4"), (64, H, I, True, "pipe32x64k128s4"),
     (512, H, Q + 2 * KV, False, "xl64x128"), (512, H, I, True, "xl128x128"),
     (512, H, Q, False, "pipe32x64k64s4"), (512, I, H, False, "pipe32x64k128s4"),

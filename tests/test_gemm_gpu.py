@@ -208,6 +208,46 @@ def test_skinny_kernel(M, K, N):
         assert np.array_equal(c.view(np.uint32), got.view(np.uint32))
 
 
+NARROW_SHAPES = [(64, 2048, 1024), (64, 3072, 1024), (48, 2048, 1024), (16, 3072, 1024), (1, 3072, 1024),
+                 (64, 4096, 2048), (64, 4096, 64), (7, 1152, 36), (33, 1024, 300), (64, 2048, 1000),
+                 (5, 128, 100), (64, 1024, 20000)]
+
+
+def test_narrow_kernel():
+    """The narrow kernel (32-column blocks, K split over blocks, slices added
+    in slice order by the last block of each column block to take a ticket):
+    1 to 32 slices, partial row tiles (M = 1 .. 64) and partial column blocks
+    (N % 32 != 0), one slice only (K = 128).  Device buffers refilled with NaN
+    before every call, so an output left unwritten fails; every shape is run
+    three times, interleaved with the others (each call must leave its
+    tickets at zero for the next), and the repeats are bit-identical."""
+    cases = []
+    for M, K, N in NARROW_SHAPES:
+        a, b = inputs(M, K, N, 4500 + M + K + N)
+        cases.append((M, K, N, a, b, abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(b),
+                      abi.DeviceBuffer(4 * M * N)))
+    L = runtime.lib()
+    outs = {}
+    abi.force_plan(abi.PLANS["narrow"])
+    try:
+        for rep in range(3):
+            for M, K, N, a, b, ad, bd, cd in cases:
+                print(f"narrow {M}x{K}x{N} rep {rep}", flush=True)
+                cd.upload(np.full(M * N, np.nan, np.float32))
+                runtime.check(L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                                   ctypes.c_void_p(bd.ptr), M, K, N), "gemm_dev")
+                assert abi.last_plan() == "narrow", (M, K, N, abi.last_plan())
+                outs.setdefault((M, K, N), []).append(cd.download(np.float32, M * N))
+    finally:
+        abi.force_plan(0)
+    for M, K, N, a, b, *_ in cases:
+        got = outs[(M, K, N)]
+        numerics.compare(got[0], a, b, M, K, N, rows=numerics.pick_rows(M, 40),
+                         cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+        for g in got[1:]:
+            assert np.array_equal(got[0].view(np.uint32), g.view(np.uint32)), (M, K, N)
+
+
 @pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe", "xl", "stream", "skinny")) or p == "gemv"])
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
                                    (40, 2048, 300), (16, 1024, 3072)])

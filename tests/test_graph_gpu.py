@@ -15,10 +15,12 @@ pytestmark = pytest.mark.gpu
 
 def test_graph_replay_matches_eager():
     L = runtime.init()
-    # (64, 2048 | 3072, 1024): the skinny split-K kernel and its slice reduction
+    # (64, 2048 | 3072, 1024): the narrow kernel, slices added in-launch by
+    # ticket (the tickets must be back at zero for every replay);
+    # (16, 3072, 1024): the skinny split-K kernel and its slice reduction
     shapes = [(1, 1024, 4096, False), (1, 2048, 1024, False), (1, 1024, 3072, True),
               (1, 3072, 1024, False), (64, 1024, 2048, False), (5, 40, 17, False), (2, 0, 8, False),
-              (64, 2048, 1024, False), (64, 3072, 1024, False)]
+              (64, 2048, 1024, False), (64, 3072, 1024, False), (16, 3072, 1024, False)]
     bufs = []
     for i, (M, K, N, gated) in enumerate(shapes):
         a = oracle.f32_bf16_normal(max(M * K, 1), 40 + i)

@@ -4,8 +4,9 @@ qwen3_hip_gemm_dev, through the C ABI.
 It has no counterpart in the reference: it is qwen3_hip_gemm_dev with the
 library's growable workspace replaced by a fixed device array, for callers
 that cannot allocate.  The shapes below reach every plan that uses workspace
-(the skinny and stream kernels' K-slice sums, the xb plans' bf16 copy of A)
-and one that does not (the M = 1 GEMV).  Results must equal the allocating
+(the narrow, skinny and stream kernels' K-slice sums, the narrow kernel's
+tickets, the xb plans' bf16 copy of A) and one that does not (the M = 1
+GEMV).  Results must equal the allocating
 entry point's bit for bit (same plan, same kernels) and pass the oracle
 comparison; each pair of calls is made twice in a row, the second time with a
 smaller input, so a stale workspace would show.
@@ -41,14 +42,16 @@ def run(L, fn, a, b, M, K, N):
 
 # (first call, second smaller call): plan family each pair reaches
 PAIRS = [
-    ((64, 3072, 1024), (48, 2048, 1024)),      # skinny, K split: slice sums in scratch
+    ((64, 3072, 1024), (48, 2048, 1024)),      # narrow: slice sums and tickets in scratch
+    ((16, 3072, 1024), (16, 2048, 1024)),      # skinny, K split: slice sums in scratch
     ((16, 1024, 1024), (8, 1024, 512)),        # stream, K split: slice sums in scratch
     ((8192, 1024, 4096), (8192, 512, 4096)),   # xb256x256s1: bf16 copy of A in scratch
     ((1, 1024, 3072), (1, 1024, 1024)),        # gemv: no workspace
 ]
 
 
-PLAN_OF = {PAIRS[0][0]: "skinny", PAIRS[1][0]: "stream", PAIRS[2][0]: "xb256x256s1", PAIRS[3][0]: "gemv"}
+PLAN_OF = {PAIRS[0][0]: "narrow", PAIRS[1][0]: "skinny", PAIRS[2][0]: "stream", PAIRS[3][0]: "xb256x256s1",
+           PAIRS[4][0]: "gemv"}
 
 
 @pytest.mark.parametrize("first,second", PAIRS)
