@@ -1846,38 +1846,45 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // ---------------------------------------------------------------------------
 // Narrow GEMM for M <= 64 and K-heavy shapes (o, down of a decode batch)
 // ---------------------------------------------------------------------------
-// blockIdx.y owns 32 columns of C (two 16-column MFMA tiles) and all 16 MT
-// rows, blockIdx.x a K slice of KSL = 128 * KPW (slice-major, so with a
-// multiple of 8 slices each XCD reads one slice of A).  Every thread issues
-// all of its loads at once: the block's slice of A first (from L2), then its
-// wave's weights (from HBM); the slice is rounded to bf16 (RNE) into LDS
-// (16-byte chunks XOR-swizzled by row) while the weights are in flight.  The
-// four waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
-// their partial tiles are added through LDS in wave order.  With one slice
-// the block writes C.  With several, each block writes its slice sums
-// [slice][M][N] with agent-scope (write-through) stores, waits for them, and
-// takes a ticket from its column block's counter; the block that draws the
-// last ticket reads every slice's sums (agent-scope loads), adds them in
-// slice order -- deterministic, whatever the arrival order -- writes C and
-// resets the counter to zero for the next call.  No block waits for another
-// and there is no second launch.  Loads past M and N read zeros at
-// out-of-range offsets.
+// blockIdx.y owns 32 columns of C (two 16-column MFMA tiles; with GATED the
+// same columns of both weights), blockIdx.z a slab of ROWS = 16 MT rows and
+// blockIdx.x a K slice of KSL = 128 * KPW (slice-major, so with a multiple
+// of 8 slices each XCD reads one slice of A).  Every thread issues all of its
+// loads at once: the block's slice of A first (from L2), then its wave's
+// weights (from HBM); the slice is rounded to bf16 (RNE) into LDS (16-byte
+// chunks XOR-swizzled by row) while the weights are in flight.  The four
+// waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
+// their partial tiles are added through LDS (reusing the A slice's space) in
+// wave order.  With one slice the block writes C (silu(gate) * up when
+// GATED).  With several, each block writes its slice sums [slice][j][M][N]
+// with agent-scope (write-through) stores, waits for them, and takes a ticket
+// from its tile's counter; the block that draws the last ticket reads every
+// slice's sums (agent-scope loads), adds them in slice order --
+// deterministic, whatever the arrival order -- writes C and resets the
+// counter to zero for the next call.  No block waits for another and there
+// is no second launch.  Loads past M and N read zeros at out-of-range
+// offsets.
 #define NARROW_COLS 32
-template <int MT, int KPW>
+#define NARROW_RSTRIDE (NARROW_COLS + 4)   // +4: conflict-free column writes, 16-byte aligned rows
+template <int MT, int KPW, bool GATED>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
                                                             unsigned *__restrict__ cnt,
                                                             const float *__restrict__ a,
-                                                            const uint16_t *__restrict__ b, int M, int K, int N) {
+                                                            const uint16_t *__restrict__ b,
+                                                            const uint16_t *__restrict__ b2, int M, int K, int N) {
+    constexpr int NJ = GATED ? 2 : 1;
     constexpr int KSL = 128 * KPW, CH = KSL / 8;         // slice depth, 16-byte chunks per row
     constexpr int NT = NARROW_COLS / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
+    constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * NARROW_RSTRIDE / 4;
     static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
-    __shared__ __align__(16) u32x4 sa[ROWS * CH];
-    __shared__ __align__(16) float red[NW][ROWS][NARROW_COLS + 4];   // +4: conflict-free column writes
+    __shared__ __align__(16) u32x4 smem[SA_U4 > RED_U4 ? SA_U4 : RED_U4];
+    u32x4 *const sa = smem;                               // the A slice, then
+    float *const red = reinterpret_cast<float *>(smem);   // [wave][j][row][RSTRIDE] wave partials
     __shared__ unsigned last_s;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.x * KSL, ks = gridDim.x;
-    const int n0 = blockIdx.y * NARROW_COLS;
+    const int n0 = blockIdx.y * NARROW_COLS, m0 = blockIdx.z * ROWS;
     const size_t MN = (size_t)M * N;
 
     // 1. every load at once: first the block's A slice (rows past M read
@@ -1885,26 +1892,30 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     //    n0 + 16 nt + r16, k = k0 + 32 (KPW w + s) + 8 g; from HBM), so that the
     //    slice is rounded into LDS while the weights are still in flight
     constexpr int PER = ROWS * CH / NTHREADS;             // 32-byte pieces of A per thread
-    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PER + NT * KPW <= 63, "loads in flight");
+    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PER + NJ * NT * KPW <= 64, "loads in flight");
     const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
     u32x4 lo[PER], hi[PER];
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int q = tid + NTHREADS * i;
-        const int m = q / CH, ch = q % CH;
+        const int m = m0 + q / CH, ch = q % CH;
         const uint32_t off = (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4);
         lo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
         hi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off + 16u : BUF_OOB, 0, 0);
     }
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
-    u32x4 bq[NT][KPW];
+    const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
+    u32x4 bq[NJ][NT][KPW];
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) {
         const int n = n0 + 16 * nt + r16;
         const uint32_t base = (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * g) * 2);
 #pragma unroll
-        for (int s = 0; s < KPW; s++)
-            bq[nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, n < N ? base + 64u * s : BUF_OOB, 0, 2);
+        for (int s = 0; s < KPW; s++) {
+            const uint32_t off = n < N ? base + 64u * s : BUF_OOB;
+            bq[0][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
+            if constexpr (GATED) bq[NJ - 1][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -1923,11 +1934,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     __syncthreads();
 
     // 3. MFMA over this wave's steps: A fragment rows 16 mt + r16, chunk 4 (KPW w + s) + g
-    f32x4 acc[NT][MT];
+    f32x4 acc[NJ][NT][MT];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[j][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KPW; s++) {
         bf16x8 af[MT];
@@ -1937,85 +1950,115 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
             af[mt] = __builtin_bit_cast(bf16x8, sa[m * CH + ((4 * (KPW * w + s) + g) ^ (m & 15))]);
         }
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++)
+        for (int j = 0; j < NJ; j++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], __builtin_bit_cast(bf16x8, bq[nt][s]),
-                                                                      acc[nt][mt], 0, 0, 0);
+            for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    acc[j][nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        af[mt], __builtin_bit_cast(bf16x8, bq[j][nt][s]), acc[j][nt][mt], 0, 0, 0);
     }
+    __syncthreads();                                      // every wave is done reading the A slice
 
     // 4. wave partials -> LDS: lane holds rows 16 mt + 4 g + r, column 16 nt + r16
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++)
+    for (int j = 0; j < NJ; j++)
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) red[w][16 * mt + 4 * g + r][16 * nt + r16] = acc[nt][mt][r];
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    red[((w * NJ + j) * ROWS + 16 * mt + 4 * g + r) * NARROW_RSTRIDE + 16 * nt + r16] =
+                        acc[j][nt][mt][r];
     __syncthreads();
 
-    // 5. quads of 4 columns, q = tid + NTHREADS i: row q / 8, columns 4 (q % 8) .. +3,
-    //    summed over the waves in order; N % 4 == 0, so a quad is wholly in or out
+    // 5. quads of 4 columns, q = tid + NTHREADS i: row m0 + q / 8, columns
+    //    4 (q % 8) .. +3, summed over the waves in order; N % 4 == 0, so a
+    //    quad is wholly in or out
     constexpr int NQ = ROWS * NARROW_COLS / 4, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
     static_assert(NQ % NTHREADS == 0 || NQ < NTHREADS, "quads per thread");
-    f32x4 v[QPT];
+    f32x4 v[NJ][QPT];
     uint32_t coff[QPT];                                   // byte offset of the quad in C, or BUF_OOB
 #pragma unroll
     for (int i = 0; i < QPT; i++) {
         const bool live = tid + NTHREADS * i < NQ;        // MT = 1: half of the threads
         const int q = live ? tid + NTHREADS * i : 0;
         const int m = q >> 3, cq = 4 * (q & 7), n = n0 + cq;
-        f32x4 t = *reinterpret_cast<const f32x4 *>(&red[0][m][cq]);
 #pragma unroll
-        for (int ww = 1; ww < NW; ww++) t += *reinterpret_cast<const f32x4 *>(&red[ww][m][cq]);
-        v[i] = t;
-        coff[i] = (live && m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
+        for (int j = 0; j < NJ; j++) {
+            f32x4 t = *reinterpret_cast<const f32x4 *>(&red[(j * ROWS + m) * NARROW_RSTRIDE + cq]);
+#pragma unroll
+            for (int ww = 1; ww < NW; ww++)
+                t += *reinterpret_cast<const f32x4 *>(&red[((ww * NJ + j) * ROWS + m) * NARROW_RSTRIDE + cq]);
+            v[j][i] = t;
+        }
+        coff[i] = (live && m0 + m < M && n < N) ? (uint32_t)(((size_t)(m0 + m) * N + n) * 4) : BUF_OOB;
     }
+    auto finish = [&](const f32x4 &x, const f32x4 &y) -> u32x4 {
+        if constexpr (GATED)
+            return __builtin_bit_cast(u32x4, f32x4{silu_mul(x[0], y[0]), silu_mul(x[1], y[1]),
+                                                   silu_mul(x[2], y[2]), silu_mul(x[3], y[3])});
+        else
+            return __builtin_bit_cast(u32x4, x);
+    };
     const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, MN * 4);
     if (ks == 1) {
 #pragma unroll
         for (int i = 0; i < QPT; i++)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rc, coff[i], 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b128(finish(v[0][i], v[NJ - 1][i]), rc, coff[i], 0, 0);
         return;
     }
     // 6. slice sums out (write-through, agent scope), then a ticket; the last
     //    block adds the slices
-    const __amdgpu_buffer_rsrc_t rp = xl_rsrc(part, (size_t)ks * MN * 4);
-    const uint32_t sl_bytes = (uint32_t)(MN * 4);
+    const __amdgpu_buffer_rsrc_t rp = xl_rsrc(part, (size_t)ks * NJ * MN * 4);
+    const uint32_t j_bytes = (uint32_t)(MN * 4), sl_bytes = NJ * j_bytes;
 #pragma unroll
     for (int i = 0; i < QPT; i++)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[i]), rp,
-                                               coff[i] == BUF_OOB ? BUF_OOB : coff[i] + blockIdx.x * sl_bytes, 0,
-                                               AUX_SC1);
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(u32x4, v[j][i]), rp,
+                coff[i] == BUF_OOB ? BUF_OOB : coff[i] + blockIdx.x * sl_bytes + j * j_bytes, 0, AUX_SC1);
     __builtin_amdgcn_s_waitcnt(0);                        // this thread's sums have landed
     __syncthreads();                                      // ... and every thread's
+    unsigned *const tick = cnt + blockIdx.z * gridDim.y + blockIdx.y;
     if (tid == 0)
-        last_s = __hip_atomic_fetch_add(cnt + blockIdx.y, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (unsigned)ks - 1u;
+        last_s = __hip_atomic_fetch_add(tick, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)ks - 1u;
     __syncthreads();
     if (!last_s) return;                                  // uniform over the block
-    f32x4 sum[QPT];
+    f32x4 sum[NJ][QPT];
 #pragma unroll
     for (int i = 0; i < QPT; i++)
-        sum[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, coff[i], 0, AUX_SC1));
+#pragma unroll
+        for (int j = 0; j < NJ; j++)
+            sum[j][i] = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rp, coff[i] == BUF_OOB ? BUF_OOB : coff[i] + j * j_bytes, 0, AUX_SC1));
     for (int sl0 = 1; sl0 < ks; sl0 += 8) {               // 8 slices of every quad in flight, added in order
-        u32x4 t[QPT][8];
+        u32x4 t[NJ][QPT][8];
 #pragma unroll
         for (int i = 0; i < QPT; i++)
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                t[i][u] = __builtin_amdgcn_raw_buffer_load_b128(
-                    rp, (coff[i] == BUF_OOB || sl0 + u >= ks) ? BUF_OOB : coff[i] + (uint32_t)(sl0 + u) * sl_bytes,
-                    0, AUX_SC1);
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    t[j][i][u] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rp, (coff[i] == BUF_OOB || sl0 + u >= ks)
+                                ? BUF_OOB : coff[i] + (uint32_t)(sl0 + u) * sl_bytes + j * j_bytes,
+                        0, AUX_SC1);
 #pragma unroll
         for (int i = 0; i < QPT; i++)
 #pragma unroll
-            for (int u = 0; u < 8; u++)
-                if (sl0 + u < ks) sum[i] += __builtin_bit_cast(f32x4, t[i][u]);
+            for (int j = 0; j < NJ; j++)
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (sl0 + u < ks) sum[j][i] += __builtin_bit_cast(f32x4, t[j][i][u]);
     }
 #pragma unroll
     for (int i = 0; i < QPT; i++)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[i]), rc, coff[i], 0, 0);
-    if (tid == 0) __hip_atomic_store(cnt + blockIdx.y, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_raw_buffer_store_b128(finish(sum[0][i], sum[NJ - 1][i]), rc, coff[i], 0, 0);
+    if (tid == 0) __hip_atomic_store(tick, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -2264,18 +2307,22 @@ enum {
     // narrow M <= 64 (K % 128 == 0): 32-column blocks, K split over blocks and
     // the slices added inside the same launch
     PLAN_NARROW = 23,
-    PLAN_COUNT = 24
+    PLAN_NARROW_R32 = 24,      // forced row slabs of 32 / 16
+    PLAN_NARROW_R16 = 25,
+    PLAN_COUNT = 26
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
     "pipe32x64k128s4", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
-    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow"};
+    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
+    "narrow-r16"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
 static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
+static inline bool is_narrow_plan(int p) { return p >= PLAN_NARROW && p <= PLAN_NARROW_R16; }
 static inline int stream_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // the stream kernel's limits: M <= 64, whole 256-deep block slices, byte
 // offsets below 2 GiB (its out-of-range marker), 16-byte aligned rows
@@ -2327,18 +2374,21 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
-    // K-heavy, narrow shapes at 16 < M <= 64 (o and down of batched decode),
-    // and 16 < M <= 32 at K = 1024: the narrow kernel, K split over 32-column
-    // blocks and the slices added in the same launch (measured on MI355X,
-    // graph-replayed: 64x3072x1024 9.7 -> 7.7 us, 64x2048x1024 9.3 -> 7.4,
-    // 32x3072x1024 7.2 -> 6.1, 32x1024x2048 6.9 -> 5.6; at M <= 16 and N =
-    // 1024 the skinny kernel below is 0.2-0.3 us faster, at M = 48, 64 and
-    // K = 1024 the 32x64 tiles are 0.6-1.3 us faster)
-    if (!gated && narrow_fits(M, K, N) && M > 16 && N >= 512 &&
-        ((K >= 2048 && K <= 4096 && N <= 2048) || (M <= 32 && K >= 1024 && N <= 4096)))
+    // 16 < M <= 64, not gated (every projection of a decode batch but
+    // gate|up): the narrow kernel, 32-column blocks in row slabs with K split
+    // over blocks where that fills the chip, the slices added in the same
+    // launch (measured on MI355X, graph-replayed, M = 64: q|k|v 1024 -> 4096
+    // 6.3 -> 4.7 us, q 6.0 -> 4.4, k 6.0 -> 5.4, o 9.7 -> 6.2, down 9.7 ->
+    // 6.9, gate alone 6.0 -> 5.1; M = 32 and 48 alike).  Gated, its two weight
+    // streams make it slower than the 32x64 tiles (64x1024x3072: 7.8 against
+    // 6.3 us).
+    if (!gated && narrow_fits(M, K, N) && M > 16 && N >= 512 && N <= 4096 && K >= 1024 && K <= 4096)
         return PLAN_NARROW;
-    if (!gated && narrow_fits(M, K, N) && K >= 2048 && K <= 4096 && N > 1024 && N <= 2048)
-        return PLAN_NARROW;   // M <= 16 (16x3072x2048: 7.7 -> 6.4 us)
+    // and at M <= 16 where it beats the stream and skinny kernels below
+    // (16x1024x1024 5.6 -> 5.2 us, 16x3072x2048 7.7 -> 6.4)
+    if (!gated && narrow_fits(M, K, N) &&
+        ((K == 1024 && N >= 512 && N <= 1024) || (K >= 2048 && K <= 4096 && N > 1024 && N <= 2048)))
+        return PLAN_NARROW;
     // the rest of them at M <= 64: the skinny kernel, A slices staged once
     // per block and K split over blocks, the slices added by a second launch
     // (measured on MI355X: 16x3072x1024 8.1 -> 5.5 us against the tiles); at
@@ -2801,52 +2851,117 @@ static int launch_skinny(const Ws &ws, float *c, const float *a, const uint16_t 
     }
 }
 
-// its slice depth, 128 * kpw: the deepest slice that still gives every CU a
-// block, else the shallowest that divides K (kpw <= 6: the bf16 A slice of
-// 64 rows fits 96 KB of LDS)
-static int narrow_kpw(int K, int N) {
-    static const int opts[] = {6, 4, 3, 2, 1};
+// The narrow kernel's geometry: 16 mt rows per block in `slabs` row slabs,
+// K slices of 128 kpw (ks of them).  kpw is capped so that a thread's loads
+// in flight (2 mt kpw of A, 2 nj kpw of weights) stay within 64.  The forced
+// narrow-r32 / narrow-r16 plans fix row slabs of 32 / 16 and take the
+// deepest slice that still gives every CU a block.  The automatic plan
+// searches mt (from the rows M needs down to 16) and kpw for the grid that
+// fills the most CUs in one round (one block per CU); among those it prefers
+// one slice (no slice sums at all), then the fewest bytes a block moves: its
+// A slice (fp32), its weights, and twice the slice sums its last block reads
+// (they sit on the critical path).  Measured on MI355X, M = 64, graph-
+// replayed: 64x1024x4096 6.1 us (32x64 tiles) -> 4.9 (32-row slabs, one
+// slice), 64x1024x2048 6.0 -> 4.2 (16-row slabs), 64x2048x1024 7.4 (64 rows,
+// 8 slices) -> 6.2 (32 rows, 4 slices), 64x3072x1024 7.9 -> 6.9.
+struct NarrowGeom {
+    int mt, slabs, kpw, ks;
+};
+static inline int narrow_kmax(int mt, bool gated) {
+    const int lim = 64 / (2 * mt + 2 * (gated ? 2 : 1));
+    return lim >= 8 ? 8 : lim >= 6 ? 6 : lim >= 4 ? 4 : lim >= 3 ? 3 : lim >= 2 ? 2 : 1;
+}
+static NarrowGeom narrow_geom(int plan, int M, int K, int N, bool gated) {
+    static const int opts[] = {8, 6, 4, 3, 2, 1};
+    const int nj = gated ? 2 : 1;
     const long ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
-    int best = 0;
-    for (int kpw : opts) {
-        if (K % (128 * kpw)) continue;
-        best = kpw;
-        if (ncb * (K / (128 * kpw)) >= g_cus) return kpw;
+    const int auto_mt = stream_mt(M);
+    NarrowGeom best{0, 0, 0, 0};
+    if (plan != PLAN_NARROW) {
+        NarrowGeom g{plan == PLAN_NARROW_R16 ? 1 : (auto_mt < 2 ? auto_mt : 2), 0, 0, 0};
+        g.slabs = (M + 16 * g.mt - 1) / (16 * g.mt);
+        const long tiles = ncb * g.slabs;
+        for (int kpw : opts) {
+            if (kpw > narrow_kmax(g.mt, gated) || K % (128 * kpw)) continue;
+            g.kpw = kpw;
+            if (tiles * (K / (128 * kpw)) >= g_cus) break;
+        }
+        g.ks = g.kpw ? K / (128 * g.kpw) : 0;
+        if (tiles > NARROW_CNT) g.kpw = g.ks = 0;          // a ticket per tile
+        return g;
+    }
+    long best_blocks = 0, best_cost = 0;
+    for (int mt = auto_mt; mt >= 1; mt /= 2) {
+        const int slabs = (M + 16 * mt - 1) / (16 * mt);
+        const long tiles = ncb * slabs;
+        if (tiles > NARROW_CNT) continue;
+        for (int kpw : opts) {
+            if (kpw > narrow_kmax(mt, gated) || K % (128 * kpw)) continue;
+            const int ks = K / (128 * kpw);
+            const long blocks = tiles * ks;
+            const long ksl = 128L * kpw, rows = 16L * mt;
+            const long cost = rows * ksl * 4 + nj * NARROW_COLS * ksl * 2 +
+                              (ks > 1 ? 2L * ks * rows * NARROW_COLS * 4 * nj : 0);
+            // one round: blocks <= CUs, else (nothing fits) the fewest blocks
+            const bool fits = blocks <= g_cus, best_fits = best_blocks <= g_cus;
+            bool take;
+            if (!best.kpw) take = true;
+            else if (fits != best_fits) take = fits;
+            else if (!fits) take = blocks < best_blocks;
+            else if (blocks != best_blocks) take = blocks > best_blocks;
+            else if ((ks == 1) != (best.ks == 1)) take = ks == 1;
+            else take = cost < best_cost;
+            if (take) {
+                best = NarrowGeom{mt, slabs, kpw, ks};
+                best_blocks = blocks;
+                best_cost = cost;
+            }
+        }
     }
     return best;
 }
-static inline size_t narrow_part_bytes(int M, int K, int N) {
-    const int kpw = narrow_kpw(K, N);
-    const int ks = kpw > 0 ? K / (128 * kpw) : 0;
-    return ks > 1 ? (size_t)ks * M * N * sizeof(float) : 0;
+static inline size_t narrow_part_bytes(const NarrowGeom &g, int M, int N, bool gated) {
+    return g.ks > 1 ? (size_t)g.ks * (gated ? 2 : 1) * M * N * sizeof(float) : 0;
 }
-template <int MT, int KPW>
-static int launch_narrow_t(const Ws &ws, float *c, const float *a, const uint16_t *b, int M, int K, int N) {
-    const int ks = K / (128 * KPW), ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
-    float *part = nullptr;
-    if (ks > 1) {
-        if ((size_t)ks * M * N * sizeof(float) > ws.part_bytes || !ws.cnt) return QH_ETOOBIG;
-        part = use_part(ws);
+// the instantiated (mt, kpw, gated) combinations: loads in flight within 64
+template <int MT, int KPW, bool GATED>
+constexpr bool narrow_ok() { return 2 * MT * KPW + 2 * (GATED ? 2 : 1) * KPW <= 64; }
+
+template <int MT, int KPW, bool GATED>
+static int launch_narrow_t(const Ws &ws, const NarrowGeom &g, float *c, const float *a, const uint16_t *b,
+                           const uint16_t *b2, int M, int K, int N) {
+    if constexpr (!narrow_ok<MT, KPW, GATED>()) {
+        return QH_EINVAL;
+    } else {
+        const int ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
+        float *part = nullptr;
+        if (g.ks > 1) {
+            if (narrow_part_bytes(g, M, N, GATED) > ws.part_bytes || !ws.cnt) return QH_ETOOBIG;
+            part = use_part(ws);
+        }
+        hipLaunchKernelGGL((k_gemm_narrow<MT, KPW, GATED>), dim3((unsigned)g.ks, (unsigned)ncb, (unsigned)g.slabs),
+                           dim3(NTHREADS), 0, g_stream, c, part, ws.cnt, a, b, b2, M, K, N);
+        HCHECK(hipGetLastError(), QH_ELAUNCH);
+        return QH_OK;
     }
-    hipLaunchKernelGGL((k_gemm_narrow<MT, KPW>), dim3((unsigned)ks, (unsigned)ncb), dim3(NTHREADS), 0, g_stream,
-                       c, part, ws.cnt, a, b, M, K, N);
-    HCHECK(hipGetLastError(), QH_ELAUNCH);
-    return QH_OK;
 }
-// narrow GEMM: sizes within narrow_fits, 16-byte aligned a and b, and the
-// slice sums within ws (checked by the caller)
-static int launch_narrow(const Ws &ws, float *c, const float *a, const uint16_t *b, int M, int K, int N) {
-    const int kpw = narrow_kpw(K, N);
-#define QH_NARROW_CASES(MT)                                                      \
-    switch (kpw) {                                                               \
-        case 1: return launch_narrow_t<MT, 1>(ws, c, a, b, M, K, N);             \
-        case 2: return launch_narrow_t<MT, 2>(ws, c, a, b, M, K, N);             \
-        case 3: return launch_narrow_t<MT, 3>(ws, c, a, b, M, K, N);             \
-        case 4: return launch_narrow_t<MT, 4>(ws, c, a, b, M, K, N);             \
-        case 6: return launch_narrow_t<MT, 6>(ws, c, a, b, M, K, N);             \
-        default: return QH_EINVAL;                                               \
+// narrow GEMM for plan p: sizes within narrow_fits, 16-byte aligned a, b, b2
+// and the slice sums within ws (checked by the caller)
+template <bool GATED>
+static int launch_narrow(const Ws &ws, int p, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+                         int M, int K, int N) {
+    const NarrowGeom g = narrow_geom(p, M, K, N, GATED);
+#define QH_NARROW_CASES(MT)                                                                  \
+    switch (g.kpw) {                                                                         \
+        case 1: return launch_narrow_t<MT, 1, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        case 2: return launch_narrow_t<MT, 2, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        case 3: return launch_narrow_t<MT, 3, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        case 4: return launch_narrow_t<MT, 4, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        case 6: return launch_narrow_t<MT, 6, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        case 8: return launch_narrow_t<MT, 8, GATED>(ws, g, c, a, b, b2, M, K, N);           \
+        default: return QH_EINVAL;                                                           \
     }
-    switch (stream_mt(M)) {
+    switch (g.mt) {
         case 1: QH_NARROW_CASES(1)
         case 2: QH_NARROW_CASES(2)
         default: QH_NARROW_CASES(4)
@@ -2920,9 +3035,8 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
-        case PLAN_NARROW:
-            if constexpr (GATED) return QH_EINVAL;
-            else return launch_narrow(ws, c, a, b, M, K, N);
+        case PLAN_NARROW: case PLAN_NARROW_R32: case PLAN_NARROW_R16:
+            return launch_narrow<GATED>(ws, plan, c, a, b, b2, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -2961,12 +3075,13 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
             plan = PLAN_T64x64;
         }
     }
-    if (plan == PLAN_NARROW) {
-        // not gated; the slice sums need room in the workspace
-        if (gated || !narrow_fits(M, K, N) || narrow_kpw(K, N) <= 0) {
+    if (is_narrow_plan(plan)) {
+        // the slice sums need room in the workspace
+        const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(plan, M, K, N, gated) : NarrowGeom{0, 0, 0, 0};
+        if (g.kpw <= 0) {
             plan = PLAN_T64x64;
         } else {
-            const size_t part = narrow_part_bytes(M, K, N);
+            const size_t part = narrow_part_bytes(g, M, N, gated);
             if (part && (!ws.cnt || !part_ensure(ws, part))) {
                 if (strict) return -QH_ETOOBIG;
                 plan = PLAN_T64x64;

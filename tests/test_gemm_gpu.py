@@ -213,42 +213,64 @@ NARROW_SHAPES = [(64, 2048, 1024), (64, 3072, 1024), (48, 2048, 1024), (16, 3072
                  (5, 128, 100), (64, 1024, 20000)]
 
 
-def test_narrow_kernel():
-    """The narrow kernel (32-column blocks, K split over blocks, slices added
-    in slice order by the last block of each column block to take a ticket):
-    1 to 32 slices, partial row tiles (M = 1 .. 64) and partial column blocks
+@pytest.mark.parametrize("plan", ["narrow", "narrow-r32", "narrow-r16"])
+@pytest.mark.parametrize("gated", [False, True], ids=["plain", "gated"])
+def test_narrow_kernel(plan, gated):
+    """The narrow kernel (32-column blocks in row slabs, K split over blocks,
+    slices added in slice order by the last block of each tile to take a
+    ticket), plain and gated (silu(gate) * up): 1 to 32 slices, one to four
+    row slabs, partial row tiles (M = 1 .. 64) and partial column blocks
     (N % 32 != 0), one slice only (K = 128).  Device buffers refilled with NaN
     before every call, so an output left unwritten fails; every shape is run
     three times, interleaved with the others (each call must leave its
     tickets at zero for the next), and the repeats are bit-identical."""
+    nb = 2 if gated else 1
     cases = []
     for M, K, N in NARROW_SHAPES:
-        a, b = inputs(M, K, N, 4500 + M + K + N)
+        if gated and N * K > 4096 * 2048:
+            continue
+        a = oracle.f32_bf16_normal(M * K, 4500 + M + K + N, 1.0)
+        b = oracle.bf16_normal(nb * N * K, 4501 + M + K + N, 0.02)
         cases.append((M, K, N, a, b, abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(b),
                       abi.DeviceBuffer(4 * M * N)))
     L = runtime.lib()
     outs = {}
-    abi.force_plan(abi.PLANS["narrow"])
+    abi.force_plan(abi.PLANS[plan])
     try:
         for rep in range(3):
             for M, K, N, a, b, ad, bd, cd in cases:
-                print(f"narrow {M}x{K}x{N} rep {rep}", flush=True)
+                print(f"{plan} gated={gated} {M}x{K}x{N} rep {rep}", flush=True)
                 cd.upload(np.full(M * N, np.nan, np.float32))
-                runtime.check(L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
-                                                   ctypes.c_void_p(bd.ptr), M, K, N), "gemm_dev")
-                assert abi.last_plan() == "narrow", (M, K, N, abi.last_plan())
+                if gated:
+                    rc = L.qwen3_hip_gemm_gate_up_silu_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                                           ctypes.c_void_p(bd.ptr),
+                                                           ctypes.c_void_p(bd.ptr + 2 * N * K), M, K, N)
+                else:
+                    rc = L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                              ctypes.c_void_p(bd.ptr), M, K, N)
+                runtime.check(rc, "gemm")
+                rows = 16 if plan == "narrow-r16" else 32 if plan == "narrow-r32" or M <= 32 else 64
+                tiles = -(-N // 32) * -(-M // rows)
+                # more tiles than the library's 2048 tickets: the 64x64 tiles instead
+                want = plan if tiles <= 2048 else "mfma64x64"
+                assert abi.last_plan() == want, (M, K, N, abi.last_plan())
                 outs.setdefault((M, K, N), []).append(cd.download(np.float32, M * N))
     finally:
         abi.force_plan(0)
     for M, K, N, a, b, *_ in cases:
         got = outs[(M, K, N)]
-        numerics.compare(got[0], a, b, M, K, N, rows=numerics.pick_rows(M, 40),
-                         cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+        rows = numerics.pick_rows(M, 40)
+        cols = None if N <= 4200 else numerics.pick_rows(N, 600)
+        if gated:
+            numerics.compare_gated(got[0], a, b[:N * K], b[N * K:], M, K, N, rows=rows)
+        else:
+            numerics.compare(got[0], a, b, M, K, N, rows=rows, cols=cols)
         for g in got[1:]:
             assert np.array_equal(got[0].view(np.uint32), g.view(np.uint32)), (M, K, N)
 
 
-@pytest.mark.parametrize("plan", [p for p in ALL_PLANS if p.startswith(("ring", "pipe", "xl", "stream", "skinny")) or p == "gemv"])
+@pytest.mark.parametrize("plan", [p for p in ALL_PLANS
+                                  if p.startswith(("ring", "pipe", "xl", "stream", "skinny", "narrow")) or p == "gemv"])
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
                                    (40, 2048, 300), (16, 1024, 3072)])
 def test_every_kernel_variant_gated(plan, M, K, N):
