@@ -2062,6 +2062,165 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Wide GEMM for M <= 64 and very wide N (the tied lm_head of a decode batch)
+// ---------------------------------------------------------------------------
+// One block per CU, four independent waves.  The block's 16 MT rows of A sit
+// in LDS as bf16 for the whole launch (RNE; 16-byte chunks XOR-swizzled by
+// row); each wave walks its own 32-column tiles (tile t = wave + j * waves)
+// over the whole of K, in chunks of 64 k.  A chunk's weights -- 32 rows x
+// 128 bytes -- are read with every load instruction covering 8 rows x 128
+// contiguous bytes (the MFMA fragment order, 16 rows x 64 bytes per
+// instruction, streams about 15% slower from HBM), passed through the wave's
+// own 4 KB of LDS, and read back as 16x16x32 MFMA fragments.  WIDE_D chunks
+// are in flight per wave; no block or wave waits for another.  Loads past N
+// read zeros at out-of-range offsets; rows past M are zeros in LDS.
+#define WIDE_KC 64            // k per chunk
+#define WIDE_D 4              // chunks in flight per wave (K / WIDE_KC must be a multiple)
+#define WIDE_A_BYTES (128 * 1024)
+#define WIDE_B_U4 (32 * WIDE_KC / 8)   // 16-byte chunks of one wave's staged weights
+__device__ __forceinline__ int wide_key(int row) { return (row ^ (row >> 3)) & 7; }
+
+template <int MT, int NCH>
+__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c, const float *__restrict__ a,
+                                                          const uint16_t *__restrict__ b, int M, int N,
+                                                          int ntiles) {
+    extern __shared__ __align__(16) u32x4 wide_lds[];
+    constexpr int ROWS = 16 * MT, NW = NTHREADS / WAVE, K = NCH * WIDE_KC, CHA = K / 8;
+    static_assert(NCH % WIDE_D == 0 && CHA % 16 == 0 && ROWS * CHA * 16 <= WIDE_A_BYTES, "wide geometry");
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    u32x4 *const sa = wide_lds;                            // [ROWS][CHA] A, swizzled
+    u32x4 *const sb = wide_lds + ROWS * CHA + w * WIDE_B_U4;   // this wave's staged chunk
+    const int gw = blockIdx.x * NW + w, nwaves = gridDim.x * NW;
+    const int my_tiles = gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0;
+    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
+
+    // the loads of chunk kc of tile number ti (of this wave): instruction i
+    // covers rows 32 t + 8 i + lane / 8, bytes 128 kc + 16 (lane % 8)
+    // (32-bit offsets, N * K * 2 < 2^31; computed without branches so that
+    // every load is issued where it stands)
+    auto issue = [&](u32x4 (&dst)[4], int ti, int kc) {
+        const int t = gw + ti * nwaves;
+        const bool live = ti < my_tiles;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = 32 * t + 8 * i + (lane >> 3);
+            const uint32_t off = ((uint32_t)n * K + WIDE_KC * kc + 8 * (lane & 7)) * 2u;
+            dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (live && n < N) ? off : BUF_OOB, 0, 2);
+        }
+    };
+    u32x4 ring[WIDE_D][4];
+#pragma unroll
+    for (int d = 0; d < WIDE_D; d++) issue(ring[d], 0, d);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // A -> LDS once: rows past M read zeros
+    {
+        const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
+        constexpr int TOTAL = ROWS * CHA;
+#pragma unroll 1
+        for (int q0 = 0; q0 < TOTAL; q0 += 8 * NTHREADS) {
+            u32x4 lo[8], hi[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int q = q0 + tid + NTHREADS * i;
+                const int m = q / CHA, ch = q % CHA;
+                const bool ok = q < TOTAL && m < M;
+                const uint32_t off = (uint32_t)(((size_t)m * K + 8 * ch) * 4);
+                lo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off : BUF_OOB, 0, 0);
+                hi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off + 16u : BUF_OOB, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int q = q0 + tid + NTHREADS * i;
+                const int m = q / CHA, ch = q % CHA;
+                u32x4 v;
+                v.x = pack_bf16x2(__uint_as_float(lo[i].x), __uint_as_float(lo[i].y));
+                v.y = pack_bf16x2(__uint_as_float(lo[i].z), __uint_as_float(lo[i].w));
+                v.z = pack_bf16x2(__uint_as_float(hi[i].x), __uint_as_float(hi[i].y));
+                v.w = pack_bf16x2(__uint_as_float(hi[i].z), __uint_as_float(hi[i].w));
+                if (q < TOTAL) sa[m * CHA + (ch ^ (m & 15))] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    // one iteration per tile, its NCH chunks unrolled: chunk kc always uses
+    // ring slot kc % WIDE_D, and the accumulators live inside the iteration
+    for (int ti = 0; ti < my_tiles; ti++) {
+        f32x4 acc[2][MT];
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < NCH; kc++) {
+            const int d = kc % WIDE_D;
+            // stage this chunk: row 8 i + lane / 8, chunk lane % 8 (swizzled)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int row = 8 * i + (lane >> 3);
+                sb[row * 8 + ((lane & 7) ^ wide_key(row))] = ring[d][i];
+            }
+            // refill the slot WIDE_D chunks ahead (into the next tile near the end)
+            if (kc + WIDE_D < NCH) issue(ring[d], ti, kc + WIDE_D);
+            else issue(ring[d], ti + 1, kc + WIDE_D - NCH);
+            __builtin_amdgcn_sched_barrier(0);            // keep the ring's order of issue
+            // two k-steps of 32: A rows 16 mt + r16, B rows 16 nt + r16, chunk 4 s + g
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                const int ka = 4 * (WIDE_KC / 32 * kc + s) + g;         // chunk of A's row
+                bf16x8 af[MT], bfr[2];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const int m = 16 * mt + r16;
+                    af[mt] = __builtin_bit_cast(bf16x8, sa[m * CHA + (ka ^ (m & 15))]);
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++) {
+                    const int row = 16 * nt + r16;
+                    bfr[nt] = __builtin_bit_cast(bf16x8, sb[row * 8 + ((4 * s + g) ^ wide_key(row))]);
+                }
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[nt][mt], 0, 0, 0);
+            }
+        }
+        // The tile out through the wave's staging space, 32 rows at a time, so
+        // that every store instruction writes 8 rows x 128 contiguous bytes
+        // (4-byte stores straight from the MFMA layout, 4 rows x 64 bytes per
+        // instruction, write back at well under half the speed).  Lane holds
+        // rows 16 mt + 4 g + r, column 16 nt + r16; LDS row-major [32][32]
+        // fp32 with the 16-byte chunk XOR-swizzled by row.
+        const int t = gw + ti * nwaves;
+        float *const sc = reinterpret_cast<float *>(sb);
+        const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, (size_t)M * N * 4);
+#pragma unroll
+        for (int h = 0; h < (MT + 1) / 2; h++) {
+#pragma unroll
+            for (int mh = 0; mh < 2 && 2 * h + mh < MT; mh++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int row = 16 * mh + 4 * g + r, col = 16 * nt + r16;
+                        sc[row * 32 + ((((col >> 2) ^ (row & 7)) << 2) | (col & 3))] = acc[nt][2 * h + mh][r];
+                    }
+#pragma unroll
+            for (int i = 0; i < (MT >= 2 ? 4 : 2); i++) {
+                const int row = 8 * i + (lane >> 3), cq = lane & 7;
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sc[row * 32 + ((cq ^ (row & 7)) << 2)]);
+                const int m = 32 * h + row, n = 32 * t + 4 * cq;
+                const uint32_t off = (m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 0);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side of the shim
 // ---------------------------------------------------------------------------
 static int g_inited = 0;
@@ -2309,7 +2468,10 @@ enum {
     PLAN_NARROW = 23,
     PLAN_NARROW_R32 = 24,      // forced row slabs of 32 / 16
     PLAN_NARROW_R16 = 25,
-    PLAN_COUNT = 26
+    // wide M <= 64 (K % 512 == 0, A within 128 KB of LDS as bf16): A resident
+    // in LDS, each wave streaming its own 32-column tiles
+    PLAN_WIDE = 26,
+    PLAN_COUNT = 27
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2317,7 +2479,7 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
     "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
-    "narrow-r16"};
+    "narrow-r16", "wide"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
@@ -2335,6 +2497,14 @@ static inline bool stream_fits(int M, int K, int N) {
 static inline bool narrow_fits(int M, int K, int N) {
     return M >= 1 && M <= 64 && K > 0 && K % 128 == 0 && N % 4 == 0 && (N + NARROW_COLS - 1) / NARROW_COLS <= NARROW_CNT &&
            (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31);
+}
+// the wide kernel's limits: M <= 64, K = 512 or 1024 (whole groups of
+// WIDE_D chunks, instantiated depths), whole quads of columns, the bf16 rows
+// of A within WIDE_A_BYTES, byte offsets below 2 GiB
+static inline bool wide_fits(int M, int K, int N) {
+    return M >= 1 && M <= 64 && N > 0 && N % 4 == 0 && (K == 512 || K == 1024) && (size_t)M * N * 4 < (1ull << 31) &&
+           (size_t)16 * stream_mt(M) * K * 2 <= WIDE_A_BYTES && (size_t)M * K * 4 < (1ull << 31) &&
+           (size_t)N * K * 2 < (1ull << 31);
 }
 // k steps of 32 per wave (KS must divide K/256, and the A fragments, 4*MT*KS
 // registers, must fit in 64): no K split while there are >= 128 tiles of 16
@@ -2396,16 +2566,21 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!gated && M <= 64 && K >= 2048 && K <= 4096 && K % 64 == 0 && N <= 2048 &&
         (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31))
         return PLAN_SKINNY;
+    // the tied lm_head of a decode batch (N very wide, K = 512 or 1024): the
+    // wide kernel, A resident in LDS and every wave streaming its own tiles
+    // (measured on MI355X, graph-replayed, 64 / 48 / 32 / 16 / 8 x 1024 x
+    // 151936: 65.6 / 62.7 / 58.5 / 53.2 / 50.5 us against 79.0 / 72.2 / 66.9
+    // / 60.1 / 55.9 on the weight-streaming kernel; at M = 64 it moves 311 MB
+    // of weights in and 39 MB of C out, 5.3 TB/s of mixed traffic)
+    if (!gated && N >= 32768 && wide_fits(M, K, N)) return PLAN_WIDE;
     // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
     // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
     // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
     // stay on the tiles, which hold both weight rows of a block in one pass
     if (!gated && stream_fits(M, K, N) && (M <= 16 || (M <= 32 && N <= 2048))) return PLAN_STREAM;
-    // and for every M <= 64 when N is very wide (the tied lm_head of a decode
-    // batch; measured on MI355X, 64 / 48 / 32 x 1024 x 151936: 76-79 / 70-73 /
-    // 62-63 us against 81-84 / 74-75 / 68-70 on the 64- and 32-row tiles; a
-    // kernel staging A once per CU, each wave streaming its own weight tiles
-    // with no barrier, measured 77-83 us at M = 64 and was not kept)
+    // and for every M <= 64 when N is very wide and the wide kernel does not
+    // fit (measured on MI355X, 64 / 48 / 32 x 1024 x 151936: 76-79 / 70-73 /
+    // 62-63 us against 81-84 / 74-75 / 68-70 on the 64- and 32-row tiles)
     if (!gated && stream_fits(M, K, N) && N >= 32768) return PLAN_STREAM;
     const int bno = gated ? 2 : 1;   // gated tiles produce half as many output columns
     auto blocks = [&](int bm, int bn) {
@@ -2969,6 +3144,35 @@ static int launch_narrow(const Ws &ws, int p, float *c, const float *a, const ui
 #undef QH_NARROW_CASES
 }
 
+// wide GEMM: sizes within wide_fits, 16-byte aligned a and b (checked by the caller)
+template <int MT, int NCH>
+static int launch_wide_t(float *c, const float *a, const uint16_t *b, int M, int N) {
+    const int nw = NTHREADS / WAVE;
+    const size_t lds = (size_t)16 * MT * NCH * WIDE_KC * 2 + (size_t)nw * WIDE_B_U4 * 16;
+    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
+    if (!attr_set) {
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds),
+               QH_ELAUNCH);
+        attr_set = true;
+    }
+    const int ntiles = (N + 31) / 32;
+    int blocks = (ntiles + nw - 1) / nw;
+    if (blocks > g_cus) blocks = g_cus;
+    hipLaunchKernelGGL((k_gemm_wide<MT, NCH>), dim3((unsigned)blocks), dim3(NTHREADS), lds, g_stream, c, a, b, M, N,
+                       ntiles);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    const int mt = stream_mt(M);
+    if (K == 1024) return mt == 1 ? launch_wide_t<1, 16>(c, a, b, M, N) : mt == 2 ? launch_wide_t<2, 16>(c, a, b, M, N)
+                                                                                 : launch_wide_t<4, 16>(c, a, b, M, N);
+    if (K == 512) return mt == 1 ? launch_wide_t<1, 8>(c, a, b, M, N) : mt == 2 ? launch_wide_t<2, 8>(c, a, b, M, N)
+                                                                               : launch_wide_t<4, 8>(c, a, b, M, N);
+    return QH_EINVAL;
+}
+
 template <bool GATED>
 static int launch_stream(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N, int ks) {
@@ -3037,6 +3241,9 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
         case PLAN_NARROW: case PLAN_NARROW_R32: case PLAN_NARROW_R16:
             return launch_narrow<GATED>(ws, plan, c, a, b, b2, M, K, N);
+        case PLAN_WIDE:
+            if constexpr (GATED) return QH_EINVAL;
+            else return launch_wide(c, a, b, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -3075,6 +3282,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
             plan = PLAN_T64x64;
         }
     }
+    if (plan == PLAN_WIDE && (gated || !wide_fits(M, K, N))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
         const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(plan, M, K, N, gated) : NarrowGeom{0, 0, 0, 0};

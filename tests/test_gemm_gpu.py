@@ -114,7 +114,7 @@ def test_batched_m64(name, K, N):
     M = 64
     a, b = inputs(M, K, N, 0x03550000 + 16 * 5 + sid(name))
     if name == "lm_head":
-        assert abi.plan(M, K, N) == "stream"      # the weight-streaming kernel for very wide N
+        assert abi.plan(M, K, N) == "wide"        # A resident in LDS, waves streaming their own tiles
     c = run_gemm(a, b, M, K, N, row=(name == "lm_head"))
     cols = None if N <= 4096 else np.unique(np.concatenate(
         [np.arange(256), np.linspace(0, N - 1, 2048).astype(int), np.arange(N - 256, N)]))
@@ -267,6 +267,34 @@ def test_narrow_kernel(plan, gated):
             numerics.compare(got[0], a, b, M, K, N, rows=rows, cols=cols)
         for g in got[1:]:
             assert np.array_equal(got[0].view(np.uint32), g.view(np.uint32)), (M, K, N)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 1024, 151936), (48, 1024, 40000), (33, 1024, 1000), (16, 1024, 76),
+                                   (5, 512, 4100), (64, 512, 32), (1, 1024, 9000), (64, 1024, 36)])
+def test_wide_kernel(M, K, N):
+    """The wide kernel (A resident in LDS, each wave streaming its own
+    32-column tiles through LDS): the tied lm_head of a 64-sequence batch,
+    partial row tiles, N not a multiple of 32 or smaller than one tile per
+    wave, both instantiated depths (K = 512, 1024); repeated calls are
+    bit-identical."""
+    a, b = inputs(M, K, N, 4700 + M + K + N)
+    ad, bd, cd = abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(b), abi.DeviceBuffer(4 * M * N)
+    L = runtime.lib()
+    outs = []
+    abi.force_plan(abi.PLANS["wide"])
+    try:
+        for rep in range(2):
+            print(f"wide {M}x{K}x{N} rep {rep}", flush=True)
+            cd.upload(np.full(M * N, np.nan, np.float32))
+            runtime.check(L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                               ctypes.c_void_p(bd.ptr), M, K, N), "gemm_dev")
+            assert abi.last_plan() == "wide"
+            outs.append(cd.download(np.float32, M * N))
+    finally:
+        abi.force_plan(0)
+    numerics.compare(outs[0], a, b, M, K, N, rows=numerics.pick_rows(M, 40),
+                     cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
 @pytest.mark.parametrize("plan", [p for p in ALL_PLANS
