@@ -91,23 +91,28 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 // ---------------------------------------------------------------------------
 // GEMV: M <= 4
 // ---------------------------------------------------------------------------
+// One halving step per template level, so that every index below is a
+// constant (a loop over a run-time `half` would index v dynamically).
+template <int HALF, int MASK>
+__device__ __forceinline__ void wave_halving_steps(float *v, int lane) {
+    if constexpr (HALF >= 1) {
+        const bool hi = (lane & MASK) != 0;
+#pragma unroll
+        for (int i = 0; i < HALF; i++) {
+            const float send = hi ? v[i] : v[i + HALF];
+            const float keep = hi ? v[i + HALF] : v[i];
+            v[i] = keep + __shfl_xor(send, MASK);
+        }
+        wave_halving_steps<HALF / 2, MASK / 2>(v, lane);
+    }
+}
 // After this, lane l holds the 64-lane total of value index l >> (6 - log2 V).
 // Each halving step trades half of the values with the partner lane, so a
 // lane ends up owning one value after log2(V) exchanges instead of V*6.
 template <int V>
 __device__ __forceinline__ float wave_transpose_reduce(float (&v)[V], int lane) {
     static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of 2 <= 64");
-#pragma unroll
-    for (int s = 0, half = V / 2; half >= 1; s++, half /= 2) {
-        const int mask = 32 >> s;
-        const bool hi = (lane & mask) != 0;
-#pragma unroll
-        for (int i = 0; i < half; i++) {
-            float send = hi ? v[i] : v[i + half];
-            float keep = hi ? v[i + half] : v[i];
-            v[i] = keep + __shfl_xor(send, mask);
-        }
-    }
+    wave_halving_steps<V / 2, 32>(v, lane);
     constexpr int L = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
     float x = v[0];
 #pragma unroll
@@ -196,6 +201,96 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
     if ((lane & ((64 >> LV) - 1)) == 0) {
         const int m = idx / ROWS, r = idx % ROWS;
         if (m < MR && row0 + r < N) c[(size_t)m * N + row0 + r] = tot;
+    }
+}
+
+// GEMV-shaped GEMM for 5 <= M <= MR (8 or 16) and K <= 512 * CPL: every
+// weight row is read once, with each load instruction covering 1 KB of one
+// row (lane l owns the 16-byte chunks l, l + 64, ... of every row), and the
+// M rows of A are applied to it from registers with v_dot2_f32_bf16.  The
+// block's 256 threads first load A once between them (fp32, from L2) and
+// round it to bf16 into LDS, then every wave issues its ROWS * CPL weight
+// loads, and A is passed to the lanes while the weights are in flight: a
+// launch costs one HBM round trip.  The ROWS * MR sums of a wave are reduced
+// across its lanes by halving exchanges, one value per lane at the end.
+// Rows of A past M are zeros; weight rows past N read zeros and are not
+// stored.  Dynamic LDS: MR * K * 2 bytes.
+template <int MR, int ROWS, int CPL>
+__global__ __launch_bounds__(NTHREADS) void k_gemv_m(float *__restrict__ c, const float *__restrict__ a,
+                                                    const uint16_t *__restrict__ b, int M, int K, int N) {
+    extern __shared__ u32x4 sa_m[];                   // [MR][K / 8] bf16 chunks
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch = K >> 3;
+    const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
+
+    // 1. A -> registers (fp32, from L2): MR rows of nch chunks over the block
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * K * 4);
+    constexpr int AQ = (MR * 128 * CPL + NTHREADS - 1) / NTHREADS;   // chunks per thread at K = 512 CPL
+    u32x4 alo[AQ], ahi[AQ];
+#pragma unroll
+    for (int i = 0; i < AQ; i++) {
+        const int q = tid + NTHREADS * i;
+        const int m = q / nch, ch = q - m * nch;
+        const bool ok = q < MR * nch && m < M;
+        const uint32_t off = ((uint32_t)m * K + 8 * ch) * 4u;   // M * K * 4 < 2^31
+        alo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off : BUF_OOB, 0, 0);
+        ahi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off + 16u : BUF_OOB, 0, 0);
+    }
+    // 2. this wave's weights: rows row0 + r, chunks lane + 64 j (non-temporal)
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
+    u32x4 bw[ROWS][CPL];
+#pragma unroll
+    for (int r = 0; r < ROWS; r++)
+#pragma unroll
+        for (int j = 0; j < CPL; j++) {
+            const int ch = lane + WAVE * j;
+            const bool ok = row0 + r < N && ch < nch;
+            const uint32_t off = ((uint32_t)(row0 + r) * K + 8 * ch) * 2u;   // N * K * 2 < 2^31
+            bw[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? off : BUF_OOB, 0, 2);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. A rounded to bf16 (RNE) into LDS while the weights are in flight
+#pragma unroll
+    for (int i = 0; i < AQ; i++) {
+        const int q = tid + NTHREADS * i;
+        u32x4 v;
+        v.x = pack_bf16x2(__uint_as_float(alo[i].x), __uint_as_float(alo[i].y));
+        v.y = pack_bf16x2(__uint_as_float(alo[i].z), __uint_as_float(alo[i].w));
+        v.z = pack_bf16x2(__uint_as_float(ahi[i].x), __uint_as_float(ahi[i].y));
+        v.w = pack_bf16x2(__uint_as_float(ahi[i].z), __uint_as_float(ahi[i].w));
+        if (q < MR * nch) sa_m[q] = v;
+    }
+    __syncthreads();
+    // 4. sums: acc[r * MR + m] over this lane's chunks
+    constexpr int V = pow2_ceil<ROWS * MR>::v;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; j++) {
+        // chunks past K: the weights read zeros, so any A chunk will do
+        const int ch = min(lane + WAVE * j, nch - 1);
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const u32x4 x = sa_m[m * nch + ch];
+#pragma unroll
+            for (int r = 0; r < ROWS; r++) {
+                float t = acc[r * MR + m];
+                t = bf16_dot2(bw[r][j].x, x.x, t);
+                t = bf16_dot2(bw[r][j].y, x.y, t);
+                t = bf16_dot2(bw[r][j].z, x.z, t);
+                t = bf16_dot2(bw[r][j].w, x.w, t);
+                acc[r * MR + m] = t;
+            }
+        }
+    }
+    // 5. reduce over the lanes; value index r * MR + m ends in lane group idx
+    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
+    const float tot = wave_transpose_reduce<V>(acc, lane);
+    const int idx = lane >> (6 - LV);
+    if ((lane & ((64 >> LV) - 1)) == 0 && idx < ROWS * MR) {
+        const int r = idx / MR, m = idx % MR;
+        if (m < M && row0 + r < N) c[(size_t)m * N + row0 + r] = tot;
     }
 }
 
@@ -2471,7 +2566,9 @@ enum {
     // wide M <= 64 (K % 512 == 0, A within 128 KB of LDS as bf16): A resident
     // in LDS, each wave streaming its own 32-column tiles
     PLAN_WIDE = 26,
-    PLAN_COUNT = 27
+    // 5 <= M <= 16, K <= 1024: every weight row read once, dot2 with A from registers
+    PLAN_GEMV16 = 27,
+    PLAN_COUNT = 28
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2479,7 +2576,7 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
     "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
-    "narrow-r16", "wide"};
+    "narrow-r16", "wide", "gemv16"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
@@ -2504,6 +2601,12 @@ static inline bool narrow_fits(int M, int K, int N) {
 static inline bool wide_fits(int M, int K, int N) {
     return M >= 1 && M <= 64 && N > 0 && N % 4 == 0 && (K == 512 || K == 1024) && (size_t)M * N * 4 < (1ull << 31) &&
            (size_t)16 * stream_mt(M) * K * 2 <= WIDE_A_BYTES && (size_t)M * K * 4 < (1ull << 31) &&
+           (size_t)N * K * 2 < (1ull << 31);
+}
+// the GEMV-shaped kernel for M <= 16: K <= 1024 (two chunks per lane),
+// byte offsets below 2 GiB
+static inline bool gemv16_fits(int M, int K, int N) {
+    return M >= 1 && M <= 16 && N > 0 && K > 0 && K % 8 == 0 && K <= 1024 && (size_t)M * K * 4 < (1ull << 31) &&
            (size_t)N * K * 2 < (1ull << 31);
 }
 // k steps of 32 per wave (KS must divide K/256, and the A fragments, 4*MT*KS
@@ -2555,10 +2658,8 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!gated && narrow_fits(M, K, N) && M > 16 && N >= 512 && N <= 4096 && K >= 1024 && K <= 4096)
         return PLAN_NARROW;
     // and at M <= 16 where it beats the stream and skinny kernels below
-    // (16x1024x1024 5.6 -> 5.2 us, 16x3072x2048 7.7 -> 6.4)
-    if (!gated && narrow_fits(M, K, N) &&
-        ((K == 1024 && N >= 512 && N <= 1024) || (K >= 2048 && K <= 4096 && N > 1024 && N <= 2048)))
-        return PLAN_NARROW;
+    // (16x3072x2048 7.7 -> 6.4 us)
+    if (!gated && narrow_fits(M, K, N) && K >= 2048 && K <= 4096 && N > 1024 && N <= 2048) return PLAN_NARROW;
     // the rest of them at M <= 64: the skinny kernel, A slices staged once
     // per block and K split over blocks, the slices added by a second launch
     // (measured on MI355X: 16x3072x1024 8.1 -> 5.5 us against the tiles); at
@@ -2573,6 +2674,14 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // / 60.1 / 55.9 on the weight-streaming kernel; at M = 64 it moves 311 MB
     // of weights in and 39 MB of C out, 5.3 TB/s of mixed traffic)
     if (!gated && N >= 32768 && wide_fits(M, K, N)) return PLAN_WIDE;
+    // 5 <= M <= 8 (and up to 16 at N <= 1024), K <= 1024: the GEMV-shaped
+    // kernel, each weight row read once in 1 KB pieces and dot2 against A
+    // held in registers (measured on MI355X, graph-replayed: 8 x 1024 x
+    // {1024, 2048, 3072, 4096} 3.0 / 3.4 / 4.0 / 4.2 us against 5.2 / 4.5 /
+    // 4.5 / 4.5 on the narrow and weight-streaming kernels; 16 x 1024 x 1024
+    // 4.8 against 5.2).  At M = 16 and N >= 2048 its 16 sums per weight pair
+    // make it VALU-bound (16 x 1024 x 3072: 6.7 against 5.2 us).
+    if (!gated && gemv16_fits(M, K, N) && M >= 5 && N <= 4096 && (M <= 8 || N <= 1024)) return PLAN_GEMV16;
     // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
     // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
     // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
@@ -3173,6 +3282,37 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
     return QH_EINVAL;
 }
 
+template <int MR, int ROWS, int CPL>
+static int launch_gemv_m_t(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    const int per_block = (NTHREADS / WAVE) * ROWS;
+    const unsigned grid = (unsigned)((N + per_block - 1) / per_block);
+    hipLaunchKernelGGL((k_gemv_m<MR, ROWS, CPL>), dim3(grid), dim3(NTHREADS), (size_t)MR * K * 2, g_stream, c, a, b,
+                       M, K, N);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+// sizes within gemv16_fits, 16-byte aligned a and b (checked by the caller);
+// rows per wave: 4 (2 at M > 8, the sums' registers), halved while that
+// leaves fewer blocks than CUs
+static int launch_gemv16(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    int rows = M <= 8 ? 4 : 2;
+    while (rows > 1 && (long)N / ((NTHREADS / WAVE) * rows) < g_cus) rows /= 2;
+    const int key = (M <= 8 ? 100 : 200) + (K <= 512 ? 10 : 20) + rows;
+    switch (key) {
+        case 111: return launch_gemv_m_t<8, 1, 1>(c, a, b, M, K, N);
+        case 112: return launch_gemv_m_t<8, 2, 1>(c, a, b, M, K, N);
+        case 114: return launch_gemv_m_t<8, 4, 1>(c, a, b, M, K, N);
+        case 121: return launch_gemv_m_t<8, 1, 2>(c, a, b, M, K, N);
+        case 122: return launch_gemv_m_t<8, 2, 2>(c, a, b, M, K, N);
+        case 124: return launch_gemv_m_t<8, 4, 2>(c, a, b, M, K, N);
+        case 211: return launch_gemv_m_t<16, 1, 1>(c, a, b, M, K, N);
+        case 212: return launch_gemv_m_t<16, 2, 1>(c, a, b, M, K, N);
+        case 221: return launch_gemv_m_t<16, 1, 2>(c, a, b, M, K, N);
+        case 222: return launch_gemv_m_t<16, 2, 2>(c, a, b, M, K, N);
+        default: return QH_EINVAL;
+    }
+}
+
 template <bool GATED>
 static int launch_stream(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N, int ks) {
@@ -3244,6 +3384,9 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_WIDE:
             if constexpr (GATED) return QH_EINVAL;
             else return launch_wide(c, a, b, M, K, N);
+        case PLAN_GEMV16:
+            if constexpr (GATED) return QH_EINVAL;
+            else return launch_gemv16(c, a, b, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -3283,6 +3426,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
         }
     }
     if (plan == PLAN_WIDE && (gated || !wide_fits(M, K, N))) plan = PLAN_T64x64;
+    if (plan == PLAN_GEMV16 && (gated || !gemv16_fits(M, K, N))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
         const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(plan, M, K, N, gated) : NarrowGeom{0, 0, 0, 0};

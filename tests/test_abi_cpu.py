@@ -50,8 +50,9 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (4096, H, Q + 2 * KV, False, "xl256x256"), (8192, H, Q + 2 * KV, False, "xb256x256s1"),
     (64, Q, H, False, "narrow"), (64, I, H, False, "narrow"),     # o, down at M = 64
     (16, I, H, False, "skinny"), (32, H, Q, False, "narrow"),
+    (8, H, I, False, "gemv16"), (16, H, H, False, "gemv16"),
     (64, H, Q + 2 * KV, False, "narrow"), (64, H, I, True, "pipe32x64k128s4"),   # q|k|v, gate|up
-    (64, H, Q, False, "narrow"), (16, H, H, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
+    (64, H, Q, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
     (512, H, Q + 2 * KV, False, "xl64x128"), (512, H, I, True, "xl128x128"),
     (512, H, Q, False, "pipe32x64k64s4"), (512, I, H, False, "pipe32x64k128s4"),
     (8, 33, 128, False, "mfma64x64-scalar"),                      # K % 8 != 0: element-wise loads

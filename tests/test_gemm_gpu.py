@@ -297,6 +297,33 @@ def test_wide_kernel(M, K, N):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(16, 1024, 3072), (16, 1024, 1024), (9, 1024, 4096), (8, 1024, 3072),
+                                   (5, 512, 1000), (13, 520, 77), (16, 1024, 151936), (12, 8, 5)])
+def test_gemv16_kernel(M, K, N):
+    """The GEMV-shaped kernel for M <= 16 (each weight row read once, dot2
+    against A from registers): both row counts (8, 16), K of one and two
+    chunks per lane and a ragged one, N not a multiple of the rows per block,
+    the lm_head width; repeated calls are bit-identical."""
+    a, b = inputs(M, K, N, 4900 + M + K + N)
+    ad, bd, cd = abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(b), abi.DeviceBuffer(4 * M * N)
+    L = runtime.lib()
+    outs = []
+    abi.force_plan(abi.PLANS["gemv16"])
+    try:
+        for rep in range(2):
+            print(f"gemv16 {M}x{K}x{N} rep {rep}", flush=True)
+            cd.upload(np.full(M * N, np.nan, np.float32))
+            runtime.check(L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                               ctypes.c_void_p(bd.ptr), M, K, N), "gemm_dev")
+            assert abi.last_plan() == "gemv16"
+            outs.append(cd.download(np.float32, M * N))
+    finally:
+        abi.force_plan(0)
+    numerics.compare(outs[0], a, b, M, K, N, rows=numerics.pick_rows(M, 40),
+                     cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("plan", [p for p in ALL_PLANS
                                   if p.startswith(("ring", "pipe", "xl", "stream", "skinny", "narrow")) or p == "gemv"])
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
