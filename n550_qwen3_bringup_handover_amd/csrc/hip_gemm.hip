@@ -2568,7 +2568,9 @@ enum {
     PLAN_WIDE = 26,
     // 5 <= M <= 16, K <= 1024: every weight row read once, dot2 with A from registers
     PLAN_GEMV16 = 27,
-    PLAN_COUNT = 28
+    // large-tile kernel on 64 x 64 tiles, BK 64 (not gated): two blocks per CU
+    PLAN_X64x64 = 28,
+    PLAN_COUNT = 29
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2576,9 +2578,9 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
     "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
-    "narrow-r16", "wide", "gemv16"};
+    "narrow-r16", "wide", "gemv16", "xl64x64"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
-static inline bool is_xl_plan(int p) { return p >= PLAN_X128x128 && p <= PLAN_XB256x256s1; }
+static inline bool is_xl_plan(int p) { return (p >= PLAN_X128x128 && p <= PLAN_XB256x256s1) || p == PLAN_X64x64; }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
 static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
 static inline bool is_narrow_plan(int p) { return p >= PLAN_NARROW && p <= PLAN_NARROW_R16; }
@@ -2707,6 +2709,12 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // all 256 CUs, gate|up from M = 2048 with A rounded to bf16 by one pass
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
+        // 64 x 64 tiles (two blocks per CU) where they make one or two rounds
+        // at K = 1024 (measured on MI355X: 512x1024x2048 9.3 -> 8.6 us,
+        // 512x1024x4096 12.8 -> 12.3, 1024x1024x2048 12.4 -> 11.8,
+        // 1024x1024x1024 8.5 -> 8.0; at 512x1024x1024 they lose, 7.7 vs 6.6)
+        if (!gated && M >= 512 && M <= 1024 && K <= 1024 && blocks(64, 64) >= 256 && blocks(64, 64) <= 512)
+            return PLAN_X64x64;
         if (M >= 1024) {
             // Fewer than 256 tiles of 128x128 (measured on MI355X, every plan at
             // M = 1024 and 2048 on the Qwen3-0.6B shapes): the 32x64 tiles while
@@ -3378,6 +3386,7 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
+        case PLAN_X64x64:   return launch_xl<64, 64, 64, false>(c, a, b, b2, M, K, N);   // not gated
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
         case PLAN_NARROW: case PLAN_NARROW_R32: case PLAN_NARROW_R16:
             return launch_narrow<GATED>(ws, plan, c, a, b, b2, M, K, N);
@@ -3406,6 +3415,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     if (!vec) plan = PLAN_SCALAR64;   // forced plans still need vector-safe inputs
     if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
     if (is_pipe_plan(plan) && (K % pipe_bk(plan)) != 0) plan = PLAN_T64x64;   // whole k stages
+    if (plan == PLAN_X64x64 && gated) plan = PLAN_T64x64;            // its wave tile holds one B block
     if (is_xl_plan(plan) && ((K % xl_bk(plan)) != 0 ||           // xl copies whole k stages and
                              (size_t)M * K * 4 >= (1ull << 32) ||   // addresses with 32-bit offsets
                              (size_t)N * K * 2 >= (1ull << 32)))
