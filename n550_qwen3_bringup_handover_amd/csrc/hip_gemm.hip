@@ -208,28 +208,29 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
 // weight row is read once, with each load instruction covering 1 KB of one
 // row (lane l owns the 16-byte chunks l, l + 64, ... of every row), and the
 // M rows of A are applied to it from registers with v_dot2_f32_bf16.  The
-// block's 256 threads first load A once between them (fp32, from L2) and
+// block's NWV waves first load A once between them (fp32, from L2) and
 // round it to bf16 into LDS, then every wave issues its ROWS * CPL weight
 // loads, and A is passed to the lanes while the weights are in flight: a
 // launch costs one HBM round trip.  The ROWS * MR sums of a wave are reduced
 // across its lanes by halving exchanges, one value per lane at the end.
 // Rows of A past M are zeros; weight rows past N read zeros and are not
 // stored.  Dynamic LDS: MR * K * 2 bytes.
-template <int MR, int ROWS, int CPL>
-__global__ __launch_bounds__(NTHREADS) void k_gemv_m(float *__restrict__ c, const float *__restrict__ a,
-                                                    const uint16_t *__restrict__ b, int M, int K, int N) {
+template <int MR, int ROWS, int CPL, int NWV>
+__global__ __launch_bounds__(NWV * WAVE) void k_gemv_m(float *__restrict__ c, const float *__restrict__ a,
+                                                      const uint16_t *__restrict__ b, int M, int K, int N) {
+    constexpr int NT = NWV * WAVE;                    // threads per block
     extern __shared__ u32x4 sa_m[];                   // [MR][K / 8] bf16 chunks
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch = K >> 3;
-    const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
+    const int row0 = (blockIdx.x * NWV + wave) * ROWS;
 
     // 1. A -> registers (fp32, from L2): MR rows of nch chunks over the block
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * K * 4);
-    constexpr int AQ = (MR * 128 * CPL + NTHREADS - 1) / NTHREADS;   // chunks per thread at K = 512 CPL
+    constexpr int AQ = (MR * WAVE * CPL + NT - 1) / NT;  // chunks per thread at K = 512 CPL
     u32x4 alo[AQ], ahi[AQ];
 #pragma unroll
     for (int i = 0; i < AQ; i++) {
-        const int q = tid + NTHREADS * i;
+        const int q = tid + NT * i;
         const int m = q / nch, ch = q - m * nch;
         const bool ok = q < MR * nch && m < M;
         const uint32_t off = ((uint32_t)m * K + 8 * ch) * 4u;   // M * K * 4 < 2^31
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv_m(float *__restrict__ c, cons
     // 3. A rounded to bf16 (RNE) into LDS while the weights are in flight
 #pragma unroll
     for (int i = 0; i < AQ; i++) {
-        const int q = tid + NTHREADS * i;
+        const int q = tid + NT * i;
         u32x4 v;
         v.x = pack_bf16x2(__uint_as_float(alo[i].x), __uint_as_float(alo[i].y));
         v.y = pack_bf16x2(__uint_as_float(alo[i].z), __uint_as_float(alo[i].w));
@@ -2676,14 +2677,14 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // / 60.1 / 55.9 on the weight-streaming kernel; at M = 64 it moves 311 MB
     // of weights in and 39 MB of C out, 5.3 TB/s of mixed traffic)
     if (!gated && N >= 32768 && wide_fits(M, K, N)) return PLAN_WIDE;
-    // 5 <= M <= 8 (and up to 16 at N <= 1024), K <= 1024: the GEMV-shaped
-    // kernel, each weight row read once in 1 KB pieces and dot2 against A
-    // held in registers (measured on MI355X, graph-replayed: 8 x 1024 x
-    // {1024, 2048, 3072, 4096} 3.0 / 3.4 / 4.0 / 4.2 us against 5.2 / 4.5 /
-    // 4.5 / 4.5 on the narrow and weight-streaming kernels; 16 x 1024 x 1024
-    // 4.8 against 5.2).  At M = 16 and N >= 2048 its 16 sums per weight pair
-    // make it VALU-bound (16 x 1024 x 3072: 6.7 against 5.2 us).
-    if (!gated && gemv16_fits(M, K, N) && M >= 5 && N <= 4096 && (M <= 8 || N <= 1024)) return PLAN_GEMV16;
+    // 5 <= M <= 16, K <= 1024 (config 1's gate_proj and the K = 1024
+    // projections of small decode batches): the GEMV-shaped kernel, each
+    // weight row read once in 1 KB pieces and dot2 against A held in
+    // registers (measured on MI355X, graph-replayed: 16 x 1024 x {1024, 2048,
+    // 3072, 4096} 3.5 / 3.7 / 4.8 / 4.9 us against 5.2 / 5.1 / 5.2 / 5.2 on
+    // the narrow and weight-streaming kernels; 8 x 1024 x the same N 2.7 /
+    // 2.9 / 3.3 / 3.5 against 5.2 / 4.5 / 4.5 / 4.5)
+    if (!gated && gemv16_fits(M, K, N) && M >= 5 && N <= 4096) return PLAN_GEMV16;
     // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
     // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
     // 16x1024x3072 5.7 vs 6.5 us, 16x3072x1024 7.7 vs 13.5 us); gated shapes
@@ -3290,33 +3291,37 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
     return QH_EINVAL;
 }
 
-template <int MR, int ROWS, int CPL>
+template <int MR, int ROWS, int CPL, int NWV>
 static int launch_gemv_m_t(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
-    const int per_block = (NTHREADS / WAVE) * ROWS;
+    const int per_block = NWV * ROWS;
     const unsigned grid = (unsigned)((N + per_block - 1) / per_block);
-    hipLaunchKernelGGL((k_gemv_m<MR, ROWS, CPL>), dim3(grid), dim3(NTHREADS), (size_t)MR * K * 2, g_stream, c, a, b,
-                       M, K, N);
+    hipLaunchKernelGGL((k_gemv_m<MR, ROWS, CPL, NWV>), dim3(grid), dim3(NWV * WAVE), (size_t)MR * K * 2, g_stream, c,
+                       a, b, M, K, N);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
-// sizes within gemv16_fits, 16-byte aligned a and b (checked by the caller);
-// rows per wave: 4 (2 at M > 8, the sums' registers), halved while that
-// leaves fewer blocks than CUs
+// sizes within gemv16_fits, 16-byte aligned a and b (checked by the caller).
+// 8 waves per block share one staged copy of A (its L2 reads, 2-4 KB per
+// row of A per block, are the kernel's main cost after the weights); rows per
+// wave: 4 at M <= 8, else 2, halved while that leaves fewer than 192 blocks
+// (measured on MI355X, 16 x 1024 x {3072, 2048, 1024}: 4.9 / 3.8 / 3.5 us
+// with 8 waves against 5.4 / 4.5 / 3.6 with 4 and 5.0 / 4.8 / 4.6 with 16)
 static int launch_gemv16(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    constexpr int NWV = 8;
     int rows = M <= 8 ? 4 : 2;
-    while (rows > 1 && (long)N / ((NTHREADS / WAVE) * rows) < g_cus) rows /= 2;
+    while (rows > 1 && (long)N / (NWV * rows) < 192) rows /= 2;
     const int key = (M <= 8 ? 100 : 200) + (K <= 512 ? 10 : 20) + rows;
     switch (key) {
-        case 111: return launch_gemv_m_t<8, 1, 1>(c, a, b, M, K, N);
-        case 112: return launch_gemv_m_t<8, 2, 1>(c, a, b, M, K, N);
-        case 114: return launch_gemv_m_t<8, 4, 1>(c, a, b, M, K, N);
-        case 121: return launch_gemv_m_t<8, 1, 2>(c, a, b, M, K, N);
-        case 122: return launch_gemv_m_t<8, 2, 2>(c, a, b, M, K, N);
-        case 124: return launch_gemv_m_t<8, 4, 2>(c, a, b, M, K, N);
-        case 211: return launch_gemv_m_t<16, 1, 1>(c, a, b, M, K, N);
-        case 212: return launch_gemv_m_t<16, 2, 1>(c, a, b, M, K, N);
-        case 221: return launch_gemv_m_t<16, 1, 2>(c, a, b, M, K, N);
-        case 222: return launch_gemv_m_t<16, 2, 2>(c, a, b, M, K, N);
+        case 111: return launch_gemv_m_t<8, 1, 1, NWV>(c, a, b, M, K, N);
+        case 112: return launch_gemv_m_t<8, 2, 1, NWV>(c, a, b, M, K, N);
+        case 114: return launch_gemv_m_t<8, 4, 1, NWV>(c, a, b, M, K, N);
+        case 121: return launch_gemv_m_t<8, 1, 2, NWV>(c, a, b, M, K, N);
+        case 122: return launch_gemv_m_t<8, 2, 2, NWV>(c, a, b, M, K, N);
+        case 124: return launch_gemv_m_t<8, 4, 2, NWV>(c, a, b, M, K, N);
+        case 211: return launch_gemv_m_t<16, 1, 1, NWV>(c, a, b, M, K, N);
+        case 212: return launch_gemv_m_t<16, 2, 1, NWV>(c, a, b, M, K, N);
+        case 221: return launch_gemv_m_t<16, 1, 2, NWV>(c, a, b, M, K, N);
+        case 222: return launch_gemv_m_t<16, 2, 2, NWV>(c, a, b, M, K, N);
         default: return QH_EINVAL;
     }
 }

@@ -44,7 +44,7 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
 
 @pytest.mark.parametrize("M,K,N,gated,plan", [
     (1, H, Q + 2 * KV, False, "gemv"), (1, Q, H, False, "gemv"), (1, H, V, False, "gemv"),
-    (16, H, I, False, "stream"),                                  # gate_proj at M = 16
+    (16, H, I, False, "gemv16"),                                  # gate_proj at M = 16
     (64, H, V, False, "wide"),                                    # lm_head of a 64-sequence batch
     (32, H, V, False, "wide"), (8, H, V, False, "wide"), (64, 2048, V, False, "stream"),
     (4096, H, Q + 2 * KV, False, "xl256x256"), (8192, H, Q + 2 * KV, False, "xb256x256s1"),
