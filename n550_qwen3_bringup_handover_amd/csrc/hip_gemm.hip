@@ -1168,7 +1168,7 @@ struct XlCfg {
     static constexpr int MFMAS = TM * TN * (BK / 16);           // per wave per stage
     static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
     static_assert(BK == 32 || BK == 64, "k stage");
-    static_assert(SETS == 1 || SETS == 2, "register sets");
+    static_assert(SETS >= 1 && SETS <= 3, "register sets");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
     static_assert(A_LOADS >= 1 && B_LOADS >= 1, "loads per lane");
     static_assert(!GATED || BNO % B_ROWS_PER_LOAD == 0, "a load never mixes Wg and Wu rows");
@@ -1326,7 +1326,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     u32x4 breg[SETS][X::B_LOADS];
     // SET: register set (and, for store and compute, LDS slot), compile-time
     auto load = [&](int step, auto SET) {
-        constexpr int set = SETS == 1 ? 0 : decltype(SET)::value;
+        constexpr int set = SETS == 1 ? 0 : decltype(SET)::value % SETS;
         const int ka = (kofs + step * BK) * (ABF16 ? 2 : 4), kb = (kofs + step * BK) * 2;   // scalar byte offsets
 #pragma unroll
         for (int i = 0; i < X::A_LOADS; i++)
@@ -1337,9 +1337,10 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
             breg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(up ? rb2 : rb, boffs[i], kb, 0);
         }
     };
-    auto store = [&](auto SLOT) {
+    // RSET: the register set that holds the stage (SETS = 3: not the slot)
+    auto store = [&](auto SLOT, auto RSET) {
         constexpr int slot = decltype(SLOT)::value;
-        constexpr int set = SETS == 1 ? 0 : slot;
+        constexpr int set = SETS == 1 ? 0 : SETS == 2 ? slot : decltype(RSET)::value % SETS;
         unsigned char *as = slot ? sa1 : sa0;
         unsigned char *bs = slot ? sb1 : sb0;
 #pragma unroll
@@ -1399,13 +1400,18 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
 
     // prologue: stage 0 stored, stage 1 (and with two sets stage 1 too)
     // in flight
-    if constexpr (SETS == 2) {
+    if constexpr (SETS == 3) {
         load(0, IC<0>{});
         if (nk > 1) load(1, IC<1>{});
-        store(IC<0>{});
+        if (nk > 2) load(2, IC<2>{});
+        store(IC<0>{}, IC<0>{});
+    } else if constexpr (SETS == 2) {
+        load(0, IC<0>{});
+        if (nk > 1) load(1, IC<1>{});
+        store(IC<0>{}, IC<0>{});
     } else {
         load(0, IC<0>{});
-        store(IC<0>{});
+        store(IC<0>{}, IC<0>{});
         if (nk > 1) load(1, IC<0>{});
     }
     __syncthreads();
@@ -1418,9 +1424,9 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
         if constexpr (SETS == 2) {
             load(it + 2, IC<set>{});
             compute(IC<set>{});
-            store(IC<set ^ 1>{});
+            store(IC<set ^ 1>{}, IC<set ^ 1>{});
         } else {
-            store(IC<set ^ 1>{});
+            store(IC<set ^ 1>{}, IC<0>{});
             load(it + 2, IC<0>{});
             compute(IC<set>{});
         }
@@ -1432,23 +1438,61 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
         if constexpr (SETS == 2) {
             if (it + 2 < nk) load(it + 2, IC<set>{});
             compute(IC<set>{});
-            if (it + 1 < nk) store(IC<set ^ 1>{});
+            if (it + 1 < nk) store(IC<set ^ 1>{}, IC<set ^ 1>{});
         } else {
-            if (it + 1 < nk) store(IC<set ^ 1>{});
+            if (it + 1 < nk) store(IC<set ^ 1>{}, IC<0>{});
             if (it + 2 < nk) load(it + 2, IC<0>{});
             compute(IC<set>{});
         }
         __syncthreads();
     };
+    // three register sets (SETS = 3): stage it + 3 is loaded while stage it
+    // is computed, so three stages are in flight; R = it mod 6 fixes the LDS
+    // slot (R & 1) and the register sets (R mod 3 loaded, R + 1 mod 3 stored)
+    auto steady3 = [&](int it, auto R) {
+        constexpr int r = decltype(R)::value;
+        load(it + 3, IC<r % 3>{});
+        compute(IC<r & 1>{});
+        store(IC<(r + 1) & 1>{}, IC<(r + 1) % 3>{});
+        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS, false>::run();
+        __syncthreads();
+    };
+    auto tail3 = [&](int it, auto R) {
+        constexpr int r = decltype(R)::value;
+        if (it + 3 < nk) load(it + 3, IC<r % 3>{});
+        compute(IC<r & 1>{});
+        if (it + 1 < nk) store(IC<(r + 1) & 1>{}, IC<(r + 1) % 3>{});
+        __syncthreads();
+    };
     int it = 0;
-    for (; it + 3 < nk; it += 2) {
-        steady(it, IC<0>{});
-        steady(it + 1, IC<1>{});
+    if constexpr (SETS == 3) {
+        for (; it + 8 < nk; it += 6) {
+            steady3(it, IC<0>{});
+            steady3(it + 1, IC<1>{});
+            steady3(it + 2, IC<2>{});
+            steady3(it + 3, IC<3>{});
+            steady3(it + 4, IC<4>{});
+            steady3(it + 5, IC<5>{});
+        }
+        // at most 8 stages left, it a multiple of 6
+        tail3(it, IC<0>{});
+        if (it + 1 < nk) tail3(it + 1, IC<1>{});
+        if (it + 2 < nk) tail3(it + 2, IC<2>{});
+        if (it + 3 < nk) tail3(it + 3, IC<3>{});
+        if (it + 4 < nk) tail3(it + 4, IC<4>{});
+        if (it + 5 < nk) tail3(it + 5, IC<5>{});
+        if (it + 6 < nk) tail3(it + 6, IC<0>{});
+        if (it + 7 < nk) tail3(it + 7, IC<1>{});
+    } else {
+        for (; it + 3 < nk; it += 2) {
+            steady(it, IC<0>{});
+            steady(it + 1, IC<1>{});
+        }
+        // 1 to 3 stages left, it even
+        tail(it, IC<0>{});
+        if (it + 1 < nk) tail(it + 1, IC<1>{});
+        if (it + 2 < nk) tail(it + 2, IC<0>{});
     }
-    // 1 to 3 stages left, it even
-    tail(it, IC<0>{});
-    if (it + 1 < nk) tail(it + 1, IC<1>{});
-    if (it + 2 < nk) tail(it + 2, IC<0>{});
 
     // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
     // column lane%32
@@ -2569,8 +2613,9 @@ enum {
     PLAN_WIDE = 26,
     // 5 <= M <= 16, K <= 1024: every weight row read once, dot2 with A from registers
     PLAN_GEMV16 = 27,
-    // large-tile kernel on 64 x 64 tiles, BK 64 (not gated): two blocks per CU
-    PLAN_X64x64 = 28,
+    // large-tile kernel on 64 x 64 tiles, BK 64, three register sets (three
+    // stages in flight; not gated): two blocks per CU
+    PLAN_X64x64s3 = 28,
     PLAN_COUNT = 29
 };
 static const char *k_plan_names[PLAN_COUNT] = {
@@ -2579,9 +2624,11 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
     "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
-    "narrow-r16", "wide", "gemv16", "xl64x64"};
+    "narrow-r16", "wide", "gemv16", "xl64x64s3"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
-static inline bool is_xl_plan(int p) { return (p >= PLAN_X128x128 && p <= PLAN_XB256x256s1) || p == PLAN_X64x64; }
+static inline bool is_xl_plan(int p) {
+    return (p >= PLAN_X128x128 && p <= PLAN_XB256x256s1) || p == PLAN_X64x64s3;
+}
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
 static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
 static inline bool is_narrow_plan(int p) { return p >= PLAN_NARROW && p <= PLAN_NARROW_R16; }
@@ -2710,12 +2757,17 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // all 256 CUs, gate|up from M = 2048 with A rounded to bf16 by one pass
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
-        // 64 x 64 tiles (two blocks per CU) where they make one or two rounds
-        // at K = 1024 (measured on MI355X: 512x1024x2048 9.3 -> 8.6 us,
-        // 512x1024x4096 12.8 -> 12.3, 1024x1024x2048 12.4 -> 11.8,
-        // 1024x1024x1024 8.5 -> 8.0; at 512x1024x1024 they lose, 7.7 vs 6.6)
+        // 64 x 64 tiles (two blocks per CU, three stages in flight) where they
+        // make one or two rounds at K = 1024 (measured on MI355X: 512x1024x2048
+        // 9.3 -> 8.2 us, 512x1024x4096 12.8 -> 12.2, 1024x1024x2048 12.4 -> 11.5,
+        // 1024x1024x1024 8.5 -> 8.0; at 512x1024x1024 they lose, 7.6 vs 6.6)
         if (!gated && M >= 512 && M <= 1024 && K <= 1024 && blocks(64, 64) >= 256 && blocks(64, 64) <= 512)
-            return PLAN_X64x64;
+            return PLAN_X64x64s3;
+        // and for the K-heavy narrow shapes (o, down) at M = 1024 .. 2048, where
+        // the third stage in flight pays (1024x2048x1024 15.8 -> 13.9 us,
+        // 1024x3072x1024 21.6 -> 18.7, 2048x3072x1024 30.4 -> 28.4)
+        if (!gated && M >= 1024 && M <= 2048 && K >= 2048 && N <= 1024 && blocks(64, 64) >= 256)
+            return PLAN_X64x64s3;
         if (M >= 1024) {
             // Fewer than 256 tiles of 128x128 (measured on MI355X, every plan at
             // M = 1024 and 2048 on the Qwen3-0.6B shapes): the 32x64 tiles while
@@ -3391,7 +3443,7 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_X128x128: return launch_xl<128, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X256x256: return launch_xl<256, 256, 32, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
-        case PLAN_X64x64:   return launch_xl<64, 64, 64, false>(c, a, b, b2, M, K, N);   // not gated
+        case PLAN_X64x64s3: return launch_xl<64, 64, 64, false, false, 3>(c, a, b, b2, M, K, N);   // not gated
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
         case PLAN_NARROW: case PLAN_NARROW_R32: case PLAN_NARROW_R16:
             return launch_narrow<GATED>(ws, plan, c, a, b, b2, M, K, N);
@@ -3420,7 +3472,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     if (!vec) plan = PLAN_SCALAR64;   // forced plans still need vector-safe inputs
     if (plan == PLAN_GEMV && (M > 4 || (size_t)M * K * 4 > 64 * 1024)) plan = PLAN_T64x64;
     if (is_pipe_plan(plan) && (K % pipe_bk(plan)) != 0) plan = PLAN_T64x64;   // whole k stages
-    if (plan == PLAN_X64x64 && gated) plan = PLAN_T64x64;            // its wave tile holds one B block
+    if (plan == PLAN_X64x64s3 && gated) plan = PLAN_T64x64;   // one B block per wave tile
     if (is_xl_plan(plan) && ((K % xl_bk(plan)) != 0 ||           // xl copies whole k stages and
                              (size_t)M * K * 4 >= (1ull << 32) ||   // addresses with 32-bit offsets
                              (size_t)N * K * 2 >= (1ull << 32)))

@@ -53,9 +53,10 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (8, H, I, False, "gemv16"), (16, H, H, False, "gemv16"),
     (64, H, Q + 2 * KV, False, "narrow"), (64, H, I, True, "pipe32x64k128s4"),   # q|k|v, gate|up
     (64, H, Q, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
-    (512, H, Q + 2 * KV, False, "xl64x64"), (512, H, I, True, "xl128x128"),
-    (512, H, Q, False, "xl64x64"), (512, I, H, False, "pipe32x64k128s4"), (512, H, KV, False, "pipe32x64k128s4"),
-    (1024, H, KV, False, "xl64x64"), (2048, H, KV, False, "xl64x128"),
+    (512, H, Q + 2 * KV, False, "xl64x64s3"), (512, H, I, True, "xl128x128"),
+    (512, H, Q, False, "xl64x64s3"), (512, I, H, False, "pipe32x64k128s4"), (512, H, KV, False, "pipe32x64k128s4"),
+    (1024, H, KV, False, "xl64x64s3"), (2048, H, KV, False, "xl64x128"),
+    (1024, I, H, False, "xl64x64s3"), (2048, Q, H, False, "xl64x64s3"), (4096, I, H, False, "xl128x128"),
     (8, 33, 128, False, "mfma64x64-scalar"),                      # K % 8 != 0: element-wise loads
 ])
 def test_automatic_plan_table(M, K, N, gated, plan):
