@@ -1249,8 +1249,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
-                                                        int M, int K, int N, TileMap map,
-                                                        float *__restrict__ part, int kslice) {
+                                                        int M, int K, int N, TileMap map) {
     using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
     constexpr int CPR = X::CPR;
     __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
@@ -1266,10 +1265,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * X::BNO;
-    // split K: blockIdx.y owns k range [kslice*y, kslice*(y+1)); with part set
-    // the raw fp32 sums go to part[y][j][M][N] (j: gate, up for GATED)
-    const int nk = kslice / BK;
-    const int kofs = blockIdx.y * kslice;
+    const int nk = K / BK;
 
     const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * (ABF16 ? 2 : 4));
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
@@ -1327,7 +1323,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     // SET: register set (and, for store and compute, LDS slot), compile-time
     auto load = [&](int step, auto SET) {
         constexpr int set = SETS == 1 ? 0 : decltype(SET)::value % SETS;
-        const int ka = (kofs + step * BK) * (ABF16 ? 2 : 4), kb = (kofs + step * BK) * 2;   // scalar byte offsets
+        const int ka = step * BK * (ABF16 ? 2 : 4), kb = step * BK * 2;   // scalar byte offsets
 #pragma unroll
         for (int i = 0; i < X::A_LOADS; i++)
             areg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoffs[i], ka, 0);
@@ -1496,32 +1492,6 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
 
     // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
     // column lane%32
-    if (part) {                                  // uniform: one K slice's raw sums
-        constexpr int NJ = GATED ? 2 : 1;
-        constexpr int TNO = X::TN / NJ;
-        const size_t MN = (size_t)M * N;
-        float *pp = part + (size_t)blockIdx.y * NJ * MN;
-#pragma unroll
-        for (int i = 0; i < X::TM; i++) {
-            const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
-#pragma unroll
-            for (int j = 0; j < TNO; j++) {
-                // the columns of the direct epilogue below
-                const int col = n0 + (GATED ? wn * (X::BNO / 2) : wn * X::WTN) + 32 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int row = rbase + 8 * (v >> 2) + (v & 3);
-                        if (row < M) {
-                            pp[(size_t)row * N + col] = acc[i][j][v];
-                            if constexpr (GATED) pp[MN + (size_t)row * N + col] = acc[i][j + TNO][v];
-                        }
-                    }
-                }
-            }
-        }
-        return;
-    }
 #pragma unroll
     for (int i = 0; i < X::TM; i++) {
         const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
@@ -2390,7 +2360,7 @@ static uint16_t *g_abf = nullptr;
 static size_t g_abf_elems = 0;
 static int g_cus = 256;            // compute units of the device (set at init)
 #define PART_INIT_BYTES ((size_t)32 << 20)
-static float *g_part = nullptr;    // split-K partial sums of the large-tile GEMM (grown on demand)
+static float *g_part = nullptr;    // K-slice sums of the skinny, stream and narrow kernels (grown on demand)
 static size_t g_part_bytes = 0;
 // tickets of the narrow kernel's K split, one per 32-column block: zero
 // between calls (each call's last block resets the ones it used)
@@ -2606,32 +2576,30 @@ enum {
     // narrow M <= 64 (K % 128 == 0): 32-column blocks, K split over blocks and
     // the slices added inside the same launch
     PLAN_NARROW = 23,
-    PLAN_NARROW_R32 = 24,      // forced row slabs of 32 / 16
-    PLAN_NARROW_R16 = 25,
     // wide M <= 64 (K % 512 == 0, A within 128 KB of LDS as bf16): A resident
     // in LDS, each wave streaming its own 32-column tiles
-    PLAN_WIDE = 26,
+    PLAN_WIDE = 24,
     // 5 <= M <= 16, K <= 1024: every weight row read once, dot2 with A from registers
-    PLAN_GEMV16 = 27,
+    PLAN_GEMV16 = 25,
     // large-tile kernel on 64 x 64 tiles, BK 64, three register sets (three
     // stages in flight; not gated): two blocks per CU
-    PLAN_X64x64s3 = 28,
-    PLAN_COUNT = 29
+    PLAN_X64x64s3 = 26,
+    PLAN_COUNT = 27
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
     "pipe32x64k128s4", "pipe32x64k64s4", "pipe64x64k64s3",
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
-    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "narrow-r32",
-    "narrow-r16", "wide", "gemv16", "xl64x64s3"};
+    "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "wide",
+    "gemv16", "xl64x64s3"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) {
     return (p >= PLAN_X128x128 && p <= PLAN_XB256x256s1) || p == PLAN_X64x64s3;
 }
 static inline bool is_xb_plan(int p) { return p >= PLAN_XB256x256k32 && p <= PLAN_XB256x256s1; }
 static inline bool is_stream_plan(int p) { return p >= PLAN_STREAM && p <= PLAN_STREAM_KS8; }
-static inline bool is_narrow_plan(int p) { return p >= PLAN_NARROW && p <= PLAN_NARROW_R16; }
+static inline bool is_narrow_plan(int p) { return p == PLAN_NARROW; }
 static inline int stream_mt(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : 4; }
 // the stream kernel's limits: M <= 64, whole 256-deep block slices, byte
 // offsets below 2 GiB (its out-of-range marker), 16-byte aligned rows
@@ -3093,7 +3061,7 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
     hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, 1), dim3(NTHREADS), 0,
-                       g_stream, c, a, b, b2, M, K, N, map, (float *)nullptr, K);
+                       g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
@@ -3198,10 +3166,8 @@ static int launch_skinny(const Ws &ws, float *c, const float *a, const uint16_t 
 
 // The narrow kernel's geometry: 16 mt rows per block in `slabs` row slabs,
 // K slices of 128 kpw (ks of them).  kpw is capped so that a thread's loads
-// in flight (2 mt kpw of A, 2 nj kpw of weights) stay within 64.  The forced
-// narrow-r32 / narrow-r16 plans fix row slabs of 32 / 16 and take the
-// deepest slice that still gives every CU a block.  The automatic plan
-// searches mt (from the rows M needs down to 16) and kpw for the grid that
+// in flight (2 mt kpw of A, 2 nj kpw of weights) stay within 64.  The search
+// runs over mt (from the rows M needs down to 16) and kpw for the grid that
 // fills the most CUs in one round (one block per CU); among those it prefers
 // one slice (no slice sums at all), then the fewest bytes a block moves: its
 // A slice (fp32), its weights, and twice the slice sums its last block reads
@@ -3216,25 +3182,12 @@ static inline int narrow_kmax(int mt, bool gated) {
     const int lim = 64 / (2 * mt + 2 * (gated ? 2 : 1));
     return lim >= 8 ? 8 : lim >= 6 ? 6 : lim >= 4 ? 4 : lim >= 3 ? 3 : lim >= 2 ? 2 : 1;
 }
-static NarrowGeom narrow_geom(int plan, int M, int K, int N, bool gated) {
+static NarrowGeom narrow_geom(int M, int K, int N, bool gated) {
     static const int opts[] = {8, 6, 4, 3, 2, 1};
     const int nj = gated ? 2 : 1;
     const long ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
     const int auto_mt = stream_mt(M);
     NarrowGeom best{0, 0, 0, 0};
-    if (plan != PLAN_NARROW) {
-        NarrowGeom g{plan == PLAN_NARROW_R16 ? 1 : (auto_mt < 2 ? auto_mt : 2), 0, 0, 0};
-        g.slabs = (M + 16 * g.mt - 1) / (16 * g.mt);
-        const long tiles = ncb * g.slabs;
-        for (int kpw : opts) {
-            if (kpw > narrow_kmax(g.mt, gated) || K % (128 * kpw)) continue;
-            g.kpw = kpw;
-            if (tiles * (K / (128 * kpw)) >= g_cus) break;
-        }
-        g.ks = g.kpw ? K / (128 * g.kpw) : 0;
-        if (tiles > NARROW_CNT) g.kpw = g.ks = 0;          // a ticket per tile
-        return g;
-    }
     long best_blocks = 0, best_cost = 0;
     for (int mt = auto_mt; mt >= 1; mt /= 2) {
         const int slabs = (M + 16 * mt - 1) / (16 * mt);
@@ -3293,9 +3246,9 @@ static int launch_narrow_t(const Ws &ws, const NarrowGeom &g, float *c, const fl
 // narrow GEMM for plan p: sizes within narrow_fits, 16-byte aligned a, b, b2
 // and the slice sums within ws (checked by the caller)
 template <bool GATED>
-static int launch_narrow(const Ws &ws, int p, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
+static int launch_narrow(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N) {
-    const NarrowGeom g = narrow_geom(p, M, K, N, GATED);
+    const NarrowGeom g = narrow_geom(M, K, N, GATED);
 #define QH_NARROW_CASES(MT)                                                                  \
     switch (g.kpw) {                                                                         \
         case 1: return launch_narrow_t<MT, 1, GATED>(ws, g, c, a, b, b2, M, K, N);           \
@@ -3445,8 +3398,8 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_X64x128:  return launch_xl<64, 128, 64, GATED>(c, a, b, b2, M, K, N);
         case PLAN_X64x64s3: return launch_xl<64, 64, 64, false, false, 3>(c, a, b, b2, M, K, N);   // not gated
         case PLAN_SKINNY: return launch_skinny<GATED>(ws, c, a, b, b2, M, K, N);
-        case PLAN_NARROW: case PLAN_NARROW_R32: case PLAN_NARROW_R16:
-            return launch_narrow<GATED>(ws, plan, c, a, b, b2, M, K, N);
+        case PLAN_NARROW:
+            return launch_narrow<GATED>(ws, c, a, b, b2, M, K, N);
         case PLAN_WIDE:
             if constexpr (GATED) return QH_EINVAL;
             else return launch_wide(c, a, b, M, K, N);
@@ -3496,7 +3449,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     if (plan == PLAN_GEMV16 && (gated || !gemv16_fits(M, K, N))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
-        const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(plan, M, K, N, gated) : NarrowGeom{0, 0, 0, 0};
+        const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(M, K, N, gated) : NarrowGeom{0, 0, 0, 0};
         if (g.kpw <= 0) {
             plan = PLAN_T64x64;
         } else {
