@@ -338,6 +338,51 @@ def test_every_kernel_variant_gated(plan, M, K, N):
     numerics.compare_gated(h, x, wg, wu, M, K, N, rows=numerics.pick_rows(M, 24))
 
 
+def _random_cases(n, seed):
+    """seeded random (plan, M, K, N, gated) cases over the plan table, sized so
+    the oracle checks each in well under a second"""
+    rng = np.random.default_rng(seed)
+    plans = [p for p in ALL_PLANS]
+    cases = []
+    while len(cases) < n:
+        plan = plans[int(rng.integers(len(plans)))]
+        M = int(rng.choice([int(rng.integers(1, 17)), int(rng.integers(17, 65)), int(rng.integers(65, 600))]))
+        K = int(rng.choice([8, 64, 128, 512, 1024, 2048, 3072])) + 8 * int(rng.integers(0, 3)) * int(rng.integers(0, 2))
+        N = int(rng.choice([int(rng.integers(1, 65)), int(rng.integers(65, 3000)), 4 * int(rng.integers(1, 1200))]))
+        gated = bool(rng.integers(0, 4) == 0)
+        if M * N * K * (2 if gated else 1) > 60_000_000:
+            continue
+        cases.append((plan, M, K, N, gated))
+    return cases
+
+
+@pytest.mark.parametrize("case", _random_cases(200, 2026), ids=lambda c: "-".join(map(str, c)))
+def test_random_shapes_forced_plans(case):
+    """Seeded random shapes on random forced plans (a plan whose conditions
+    fail falls back to a tiled kernel), plain and gated: every output against
+    the oracle, and the plan that ran reported by qwen3_hip_last_plan."""
+    plan, M, K, N, gated = case
+    nb = 2 if gated else 1
+    a = oracle.f32_bf16_normal(M * K, 5000 + M + K + N, 1.0)
+    b = oracle.bf16_normal(nb * N * K, 5001 + M + K + N, 0.02)
+    c = np.full(M * N, np.nan, np.float32)
+    abi.force_plan(abi.PLANS[plan])
+    try:
+        if gated:
+            abi.gemm_gate_up_silu(c, a, b[:N * K], b[N * K:], M, K, N)
+        else:
+            abi.gemm(c, a, b, M, K, N)
+        ran = abi.last_plan()
+    finally:
+        abi.force_plan(0)
+    assert ran in abi.PLANS, ran
+    rows = numerics.pick_rows(M, 24)
+    if gated:
+        numerics.compare_gated(c, a, b[:N * K], b[N * K:], M, K, N, rows=rows)
+    else:
+        numerics.compare(c, a, b, M, K, N, rows=rows)
+
+
 def test_non_bf16_activations_are_rounded_rne():
     """fp32 activations that are not bf16-representable: the GPU rounds them
     RNE like the AME/hwsim kernels, so the result matches the oracle on the
