@@ -108,3 +108,50 @@ def test_graph_survives_workspace_growth():
             runtime.check(L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
     finally:
         abi.force_plan(0)
+
+
+def test_narrow_ticket_chain_in_a_graph():
+    """Fifty back-to-back calls of the narrow kernel (K split over blocks, the
+    slices added in-launch by the last block of each tile to take a ticket)
+    on shapes with 2 to 24 slices and one to four row slabs, captured into
+    one graph and replayed five times: every output of every replay equals
+    the eager result bit for bit, so every call found its tickets at zero and
+    left them there."""
+    L = runtime.init()
+    shapes = [(64, 3072, 1024), (48, 2048, 1024), (33, 1024, 300), (64, 4096, 64), (64, 2048, 1000),
+              (17, 3072, 512), (64, 1024, 4096), (40, 2048, 2048), (64, 3072, 2048), (20, 1024, 4096)]
+    calls = [shapes[i % len(shapes)] for i in range(50)]
+    bufs = []
+    for i, (M, K, N) in enumerate(calls):
+        a = oracle.f32_bf16_normal(M * K, 700 + i)
+        w = oracle.bf16_normal(N * K, 800 + i, 0.02)
+        bufs.append((abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(w), abi.DeviceBuffer(4 * M * N)))
+    abi.force_plan(abi.PLANS["narrow"])
+    try:
+        def issue():
+            for (M, K, N), (ad, wd, cd) in zip(calls, bufs):
+                abi.gemm_dev(cd.ptr, ad.ptr, wd.ptr, M, K, N)
+
+        def outputs():
+            abi.sync()
+            return [cd.download(np.float32, M * N) for (M, K, N), (_, _, cd) in zip(calls, bufs)]
+
+        issue()
+        assert abi.last_plan() == "narrow"
+        eager = outputs()
+        runtime.check(L.qwen3_hip_capture_begin(), "capture_begin")
+        issue()
+        gid = ctypes.c_int(-1)
+        runtime.check(L.qwen3_hip_capture_end(ctypes.byref(gid)), "capture_end")
+    finally:
+        abi.force_plan(0)
+    try:
+        for rep in range(5):
+            for _, _, cd in bufs:
+                cd.upload(np.full(cd.nbytes // 4, np.nan, np.float32))
+            runtime.check(L.qwen3_hip_graph_launch(gid.value), "graph_launch")
+            got = outputs()
+            for i, (e, g) in enumerate(zip(eager, got)):
+                assert np.array_equal(e.view(np.uint32), g.view(np.uint32)), (rep, i, calls[i])
+    finally:
+        runtime.check(L.qwen3_hip_graph_destroy(gid.value), "graph_destroy")
