@@ -179,7 +179,7 @@ PLANS = {"auto": 0, "gemv": 1, "mfma128x128": 2, "mfma64x128": 3, "mfma64x64": 4
          "xl128x128": 11, "xl256x256": 12, "xl64x128": 13,
          "xb256x256k32": 14, "xb128x128": 15, "xb256x256s1": 16,
          "stream": 17, "stream-ks1": 18, "stream-ks2": 19, "stream-ks4": 20, "stream-ks8": 21,
-         "skinny": 22, "narrow": 23, "wide": 24, "gemv16": 25, "xl64x64s3": 26}
+         "skinny": 22, "narrow": 23, "wide": 24, "gemv16": 25, "xl64x64s3": 26, "m16": 27}
 
 
 def last_plan():

@@ -2331,6 +2331,107 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
 }
 
 // ---------------------------------------------------------------------------
+// 16-row GEMM for M <= 16 (small decode batches)
+// ---------------------------------------------------------------------------
+// blockIdx.x owns 16 columns of C (16 rows of B); the block's NWV waves split
+// K = KT (wave w: k range [w KW, (w + 1) KW)), each computing a 16 x 16 tile
+// with v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand =
+// weights), and the NWV tiles are added through LDS in wave order.  Each lane
+// issues all of its loads at once: its share of the wave's weights, 16 rows x
+// KW, each load instruction covering 8 rows x 128 contiguous bytes (the
+// fragment order itself, 16 rows x 64 bytes per instruction, streams from HBM
+// more slowly), then its A fragments (fp32, from L2, rows past M reading
+// zeros), rounded to bf16 (RNE) on arrival.  The weights pass through the
+// wave's own LDS rows (16-byte chunks XOR-swizzled by row) and are read back
+// as fragments by the same wave, so a wave-scope fence, not a block barrier,
+// orders those writes and reads.  Lane (r, g) = (lane % 16, lane / 16)
+// holds k = 32s + 8g .. 32s + 8g + 7 of step s for row r of both operands.
+// Rows of B past N read zeros and their columns of C are not stored.
+template <int NWV, int KT, int CT>
+__global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, const float *__restrict__ a,
+                                                        const uint16_t *__restrict__ b, int M, int N) {
+    constexpr int KW = KT / NWV, CHW = KW / 8, STEPS = KW / 32, NBL = 16 * CHW / WAVE;
+    constexpr int SW = CHW >= 16 ? 15 : CHW - 1;           // swizzle mask: within the row's chunks
+    static_assert(KW * NWV == KT && CHW % 8 == 0 && NBL * WAVE == 16 * CHW && NWV * WAVE >= 256 * CT, "k split");
+    extern __shared__ __align__(16) u32x4 m16_lds[];       // [NWV][CT][16][CHW] weights, then [NWV][CT][16][17] fp32
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16 * CT;
+    u32x4 *const sb = m16_lds + w * CT * 16 * CHW;
+    float *const red = reinterpret_cast<float *>(m16_lds + NWV * CT * 16 * CHW);
+
+    // weights: load i of tile t covers rows 16 t + 8 (i % 2) + lane / 8, chunks 8 (i / 2) + lane % 8
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * KT * 2);
+    u32x4 bw[CT][NBL];
+#pragma unroll
+    for (int t = 0; t < CT; t++)
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
+            const int n = n0 + 16 * t + row;
+            const uint32_t off = n < N ? ((uint32_t)n * KT + w * KW + 8 * ch) * 2u : BUF_OOB;
+            bw[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+        }
+    // A fragments of this wave's k range
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * KT * 4);
+    const uint32_t aoff = r16 < M ? ((uint32_t)r16 * KT + w * KW + 8 * g) * 4u : BUF_OOB;
+    u32x4 alo[STEPS], ahi[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        alo[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 128 * s, 0, 0);
+        ahi[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 128 * s + 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 af[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        u32x4 p;
+        p.x = pack_bf16x2(__uint_as_float(alo[s].x), __uint_as_float(alo[s].y));
+        p.y = pack_bf16x2(__uint_as_float(alo[s].z), __uint_as_float(alo[s].w));
+        p.z = pack_bf16x2(__uint_as_float(ahi[s].x), __uint_as_float(ahi[s].y));
+        p.w = pack_bf16x2(__uint_as_float(ahi[s].z), __uint_as_float(ahi[s].w));
+        af[s] = __builtin_bit_cast(bf16x8, p);
+    }
+#pragma unroll
+    for (int t = 0; t < CT; t++)
+#pragma unroll
+        for (int i = 0; i < NBL; i++) {
+            const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
+            sb[(16 * t + row) * CHW + (ch ^ (row & SW))] = bw[t][i];
+        }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    f32x4 acc[CT];
+#pragma unroll
+    for (int t = 0; t < CT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+        const int ch = 4 * s + g;
+#pragma unroll
+        for (int t = 0; t < CT; t++) {
+            const bf16x8 bf = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + (ch ^ (r16 & SW))]);
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s], bf, acc[t], 0, 0, 0);
+        }
+    }
+    // lane (r, g) holds rows 4g .. 4g + 3 of C, column 16 t + r of the block's
+#pragma unroll
+    for (int t = 0; t < CT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[((w * CT + t) * 16 + 4 * g + r) * 17 + r16] = acc[t][r];
+    __syncthreads();
+    if (threadIdx.x < 256 * CT) {
+        const int t = threadIdx.x >> 8, m = (threadIdx.x >> 4) & 15, col = threadIdx.x & 15;
+        float sum = red[(t * 16 + m) * 17 + col];
+#pragma unroll
+        for (int v = 1; v < NWV; v++) sum += red[((v * CT + t) * 16 + m) * 17 + col];
+        const int n = n0 + 16 * t + col;
+        if (m < M && n < N) c[(size_t)m * N + n] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host side of the shim
 // ---------------------------------------------------------------------------
 static int g_inited = 0;
@@ -2584,7 +2685,10 @@ enum {
     // large-tile kernel on 64 x 64 tiles, BK 64, three register sets (three
     // stages in flight; not gated): two blocks per CU
     PLAN_X64x64s3 = 26,
-    PLAN_COUNT = 27
+    // M <= 16, K = 1024, 2048 or 3072: 16-column blocks, K split over the
+    // block's waves, v_mfma_f32_16x16x32_bf16 (not gated)
+    PLAN_M16 = 27,
+    PLAN_COUNT = 28
 };
 static const char *k_plan_names[PLAN_COUNT] = {
     "auto", "gemv", "mfma128x128", "mfma64x128", "mfma64x64", "mfma32x128", "mfma16x64", "mfma64x64-scalar",
@@ -2592,7 +2696,7 @@ static const char *k_plan_names[PLAN_COUNT] = {
     "xl128x128", "xl256x256", "xl64x128",
     "xb256x256k32", "xb128x128", "xb256x256s1",
     "stream", "stream-ks1", "stream-ks2", "stream-ks4", "stream-ks8", "skinny", "narrow", "wide",
-    "gemv16", "xl64x64s3"};
+    "gemv16", "xl64x64s3", "m16"};
 static inline bool is_pipe_plan(int p) { return p >= PLAN_P32x64k128s4 && p <= PLAN_P64x64k64s3; }
 static inline bool is_xl_plan(int p) {
     return (p >= PLAN_X128x128 && p <= PLAN_XB256x256s1) || p == PLAN_X64x64s3;
@@ -2607,6 +2711,17 @@ static inline bool stream_fits(int M, int K, int N) {
     return M >= 1 && M <= 64 && K > 0 && K % 256 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
            (size_t)N * K * 2 < (1ull << 31);
 }
+// the 16-row kernel's limits: M <= 16, K one of its instantiations, byte
+// offsets below 2 GiB
+static inline bool m16_fits(int M, int K, int N) {
+    return M >= 1 && M <= 16 && (K == 1024 || K == 2048 || K == 3072) && N >= 1 &&
+           (size_t)N * K * 2 < (1ull << 31);
+}
+// the 16-row kernel's column tiles per block: two once one-tile blocks would
+// outnumber the CUs (halves the blocks' re-reads of A; measured on MI355X,
+// graph-replayed, 16 x 1024 x 8192 / 16384: 5.8 / 10.1 -> 4.5 / 7.7 us, and
+// 16 x 1024 x 4096: 3.8 -> 4.0 us the other way)
+static inline int m16_ct(int K, int N) { return K <= 2048 && (N + 15) / 16 > g_cus ? 2 : 1; }
 // the narrow kernel's limits: M <= 64, whole 128-deep slices, whole quads of
 // columns, byte offsets below 2 GiB, a ticket per 32-column block
 static inline bool narrow_fits(int M, int K, int N) {
@@ -2664,6 +2779,17 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
+    // 2 <= M <= 16 (config 1's gate_proj, small decode batches): the 16-row
+    // kernel, 16 or 32 columns per block and K split over its waves, where
+    // measured faster (MI355X, graph-replayed per call: 16 x 1024 x 3072 /
+    // 4096 / 8192 3.7 / 3.8 / 4.5 us against 4.8 / 5.0 / 5.9 on the GEMV-shaped
+    // and weight-streaming kernels; 4 x 1024 x 3072 2.7 against 3.5 on the
+    // GEMV; 8 x 2048 x 1024 4.2 against 5.3 on the skinny kernel; at K = 3072
+    // and M > 8 its blocks' re-reads of A make it slower than the skinny one)
+    if (!gated && M >= 2 && m16_fits(M, K, N) &&
+        ((K == 1024 && N <= 16384) ||
+         (K == 2048 && M > 4 && N <= 2048) || (K == 3072 && M > 4 && M <= 8 && N <= 1024)))
+        return PLAN_M16;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
     // 16 < M <= 64, not gated (every projection of a decode batch but
     // gate|up): the narrow kernel, 32-column blocks in row slabs with K split
@@ -2692,13 +2818,12 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // / 60.1 / 55.9 on the weight-streaming kernel; at M = 64 it moves 311 MB
     // of weights in and 39 MB of C out, 5.3 TB/s of mixed traffic)
     if (!gated && N >= 32768 && wide_fits(M, K, N)) return PLAN_WIDE;
-    // 5 <= M <= 16, K <= 1024 (config 1's gate_proj and the K = 1024
-    // projections of small decode batches): the GEMV-shaped kernel, each
-    // weight row read once in 1 KB pieces and dot2 against A held in
-    // registers (measured on MI355X, graph-replayed: 16 x 1024 x {1024, 2048,
-    // 3072, 4096} 3.5 / 3.7 / 4.8 / 4.9 us against 5.2 / 5.1 / 5.2 / 5.2 on
-    // the narrow and weight-streaming kernels; 8 x 1024 x the same N 2.7 /
-    // 2.9 / 3.3 / 3.5 against 5.2 / 4.5 / 4.5 / 4.5)
+    // 5 <= M <= 16, K < 1024 (K = 1024 takes the 16-row kernel above): the
+    // GEMV-shaped kernel, each weight row read once in 1 KB pieces and dot2
+    // against A held in registers (measured on MI355X, graph-replayed, at K =
+    // 1024 before the 16-row kernel: 16 x 1024 x {1024, 2048, 3072, 4096}
+    // 3.5 / 3.7 / 4.8 / 4.9 us against 5.2 / 5.1 / 5.2 / 5.2 on the narrow and
+    // weight-streaming kernels)
     if (!gated && gemv16_fits(M, K, N) && M >= 5 && N <= 4096) return PLAN_GEMV16;
     // the weight-streaming kernel for 5 <= M <= 16, and up to M = 32 where
     // N <= 2048 leaves the 32x64 tiles few blocks (measured on MI355X, e.g.
@@ -3296,6 +3421,34 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
     return QH_EINVAL;
 }
 
+template <int NWV, int KT, int CT>
+static int launch_m16_t(float *c, const float *a, const uint16_t *b, int M, int N) {
+    const size_t lds = (size_t)CT * 16 * KT * 2 + (size_t)NWV * CT * 16 * 17 * 4;   // weights, then the wave tiles
+    static bool attr = false;              // dynamic LDS above 64 KB must be opted into
+    if (!attr) {
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_m16<NWV, KT, CT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds),
+               QH_ELAUNCH);
+        attr = true;
+    }
+    hipLaunchKernelGGL((k_gemm_m16<NWV, KT, CT>), dim3((unsigned)((N + 16 * CT - 1) / (16 * CT))), dim3(NWV * WAVE),
+                       lds, g_stream, c, a, b, M, N);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+// sizes within m16_fits, 16-byte aligned a and b (checked by the caller)
+static int launch_m16(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
+    const int ct = m16_ct(K, N);
+    switch (K * 10 + ct) {
+        case 10241: return launch_m16_t<8, 1024, 1>(c, a, b, M, N);
+        case 10242: return launch_m16_t<8, 1024, 2>(c, a, b, M, N);
+        case 20481: return launch_m16_t<8, 2048, 1>(c, a, b, M, N);
+        case 20482: return launch_m16_t<8, 2048, 2>(c, a, b, M, N);
+        case 30721: return launch_m16_t<8, 3072, 1>(c, a, b, M, N);
+        default: return QH_EINVAL;
+    }
+}
+
 template <int MR, int ROWS, int CPL, int NWV>
 static int launch_gemv_m_t(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
     const int per_block = NWV * ROWS;
@@ -3406,6 +3559,9 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_GEMV16:
             if constexpr (GATED) return QH_EINVAL;
             else return launch_gemv16(c, a, b, M, K, N);
+        case PLAN_M16:
+            if constexpr (GATED) return QH_EINVAL;
+            else return launch_m16(c, a, b, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -3447,6 +3603,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     }
     if (plan == PLAN_WIDE && (gated || !wide_fits(M, K, N))) plan = PLAN_T64x64;
     if (plan == PLAN_GEMV16 && (gated || !gemv16_fits(M, K, N))) plan = PLAN_T64x64;
+    if (plan == PLAN_M16 && (gated || !m16_fits(M, K, N))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
         const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(M, K, N, gated) : NarrowGeom{0, 0, 0, 0};

@@ -44,13 +44,15 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
 
 @pytest.mark.parametrize("M,K,N,gated,plan", [
     (1, H, Q + 2 * KV, False, "gemv"), (1, Q, H, False, "gemv"), (1, H, V, False, "gemv"),
-    (16, H, I, False, "gemv16"),                                  # gate_proj at M = 16
+    (16, H, I, False, "m16"),                                     # gate_proj at M = 16
     (64, H, V, False, "wide"),                                    # lm_head of a 64-sequence batch
     (32, H, V, False, "wide"), (8, H, V, False, "wide"), (64, 2048, V, False, "stream"),
     (4096, H, Q + 2 * KV, False, "xl256x256"), (8192, H, Q + 2 * KV, False, "xb256x256s1"),
     (64, Q, H, False, "narrow"), (64, I, H, False, "narrow"),     # o, down at M = 64
     (16, I, H, False, "skinny"), (32, H, Q, False, "narrow"),
-    (8, H, I, False, "gemv16"), (16, H, H, False, "gemv16"),
+    (8, H, I, False, "m16"), (16, H, H, False, "m16"), (4, H, I, False, "m16"), (2, H, Q, False, "m16"),
+    (8, Q, H, False, "m16"), (8, I, H, False, "m16"), (12, I, H, False, "skinny"), (16, H, 16384, False, "m16"),
+    (4, Q, H, False, "gemv"), (16, H, 32768, False, "wide"), (16, H, I, True, "pipe32x64k128s4"),
     (64, H, Q + 2 * KV, False, "narrow"), (64, H, I, True, "pipe32x64k128s4"),   # q|k|v, gate|up
     (64, H, Q, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
     (512, H, Q + 2 * KV, False, "xl64x64s3"), (512, H, I, True, "xl128x128"),

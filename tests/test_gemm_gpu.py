@@ -321,6 +321,34 @@ def test_gemv16_kernel(M, K, N):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(16, 1024, 3072), (16, 1024, 16384), (1, 1024, 48), (3, 1024, 1000),
+                                   (7, 2048, 2052), (16, 2048, 8200), (8, 3072, 1024), (16, 3072, 520),
+                                   (12, 1024, 151936)])
+def test_m16_kernel(M, K, N):
+    """The 16-row MFMA kernel for M <= 16: each K it is built for, one and two
+    16-column tiles per block (two once the blocks would outnumber the CUs),
+    M of 1 and 16 and between, N not a multiple of 16, the lm_head width;
+    repeated calls are bit-identical."""
+    a, b = inputs(M, K, N, 5300 + M + K + N)
+    ad, bd, cd = abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(b), abi.DeviceBuffer(4 * M * N)
+    L = runtime.lib()
+    outs = []
+    abi.force_plan(abi.PLANS["m16"])
+    try:
+        for rep in range(2):
+            print(f"m16 {M}x{K}x{N} rep {rep}", flush=True)
+            cd.upload(np.full(M * N, np.nan, np.float32))
+            runtime.check(L.qwen3_hip_gemm_dev(ctypes.c_void_p(cd.ptr), ctypes.c_void_p(ad.ptr),
+                                               ctypes.c_void_p(bd.ptr), M, K, N), "gemm_dev")
+            assert abi.last_plan() == "m16"
+            outs.append(cd.download(np.float32, M * N))
+    finally:
+        abi.force_plan(0)
+    numerics.compare(outs[0], a, b, M, K, N, rows=numerics.pick_rows(M, 40),
+                     cols=None if N <= 4200 else numerics.pick_rows(N, 600))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("plan", [p for p in ALL_PLANS
                                   if p.startswith(("ring", "pipe", "xl", "stream", "skinny", "narrow")) or p == "gemv"])
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
