@@ -2722,10 +2722,11 @@ static inline bool m16_fits(int M, int K, int N) {
 // graph-replayed, 16 x 1024 x 8192 / 16384: 5.8 / 10.1 -> 4.5 / 7.7 us, and
 // 16 x 1024 x 4096: 3.8 -> 4.0 us the other way)
 static inline int m16_ct(int K, int N) { return K <= 2048 && (N + 15) / 16 > g_cus ? 2 : 1; }
-// the narrow kernel's limits: M <= 64, whole 128-deep slices, whole quads of
-// columns, byte offsets below 2 GiB, a ticket per 32-column block
+// the narrow kernel's limits: M <= 256, whole 128-deep slices, whole quads
+// of columns, byte offsets below 2 GiB; its geometry search also keeps the
+// tiles (row slab x 32 columns, a ticket each) within NARROW_CNT
 static inline bool narrow_fits(int M, int K, int N) {
-    return M >= 1 && M <= 64 && K > 0 && K % 128 == 0 && N % 4 == 0 && (N + NARROW_COLS - 1) / NARROW_COLS <= NARROW_CNT &&
+    return M >= 1 && M <= 256 && K > 0 && K % 128 == 0 && N % 4 == 0 && (N + NARROW_COLS - 1) / NARROW_COLS <= NARROW_CNT &&
            (size_t)M * K * 4 < (1ull << 31) && (size_t)N * K * 2 < (1ull << 31);
 }
 // the wide kernel's limits: M <= 64, K = 512 or 1024 (whole groups of
@@ -2799,11 +2800,22 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // 6.9, gate alone 6.0 -> 5.1; M = 32 and 48 alike).  Gated, its two weight
     // streams make it slower than the 32x64 tiles (64x1024x3072: 7.8 against
     // 6.3 us).
-    if (!gated && narrow_fits(M, K, N) && M > 16 && N >= 512 && N <= 4096 && K >= 1024 && K <= 4096)
+    if (!gated && narrow_fits(M, K, N) && M > 16 && M <= 64 && N >= 512 && N <= 4096 && K >= 1024 && K <= 4096)
         return PLAN_NARROW;
     // and at M <= 16 where it beats the stream and skinny kernels below
     // (16x3072x2048 7.7 -> 6.4 us)
-    if (!gated && narrow_fits(M, K, N) && K >= 2048 && K <= 4096 && N > 1024 && N <= 2048) return PLAN_NARROW;
+    if (!gated && narrow_fits(M, K, N) && M <= 16 && K >= 2048 && K <= 4096 && N > 1024 && N <= 2048)
+        return PLAN_NARROW;
+    // 64 < M <= 256 (prefill chunks through the drop-in call, one projection
+    // at a time), where its slabs beat the 32x64 tiles: N <= 1024 up to 128
+    // rows, and N <= 2048 at K = 1024; K = 1024, N <= 1024 up to 256 rows
+    // (measured on MI355X, graph-replayed, M = 128: k/v 1024 -> 1024 6.2 ->
+    // 4.1 us, q 1024 -> 2048 6.3 -> 4.9, o 2048 -> 1024 9.8 -> 7.2, down 3072
+    // -> 1024 13.3 -> 8.8; M = 256 k/v 6.2 -> 4.8; slower at N = 4096, at K =
+    // 2048 with N = 2048, and above 128 rows at K >= 2048)
+    if (!gated && narrow_fits(M, K, N) && M > 64 && K >= 1024 && K <= 3072 &&
+        ((M <= 128 && (N <= 1024 || (K == 1024 && N <= 2048))) || (K == 1024 && N <= 1024)))
+        return PLAN_NARROW;
     // the rest of them at M <= 64: the skinny kernel, A slices staged once
     // per block and K split over blocks, the slices added by a second launch
     // (measured on MI355X: 16x3072x1024 8.1 -> 5.5 us against the tiles); at
@@ -3331,6 +3343,11 @@ static NarrowGeom narrow_geom(int M, int K, int N, bool gated) {
             if (!best.kpw) take = true;
             else if (fits != best_fits) take = fits;
             else if (!fits) take = blocks < best_blocks;
+            // above 64 rows, one slice (no slice sums, no tickets) once it
+            // gives at least half the CUs a block (measured on MI355X, 96 x
+            // 1024 x 1024: 6.4 us on 256 blocks of 4 slices, 4.0 on 192 of one)
+            else if (M > 64 && (ks == 1 && 2 * blocks >= g_cus) != (best.ks == 1 && 2 * best_blocks >= g_cus))
+                take = ks == 1 && 2 * blocks >= g_cus;
             else if (blocks != best_blocks) take = blocks > best_blocks;
             else if ((ks == 1) != (best.ks == 1)) take = ks == 1;
             else take = cost < best_cost;
@@ -3722,8 +3739,8 @@ extern "C" int qh_gemm_noalloc(float *c, const float *a, const uint16_t *b, int 
 // M <= 128, K >= 2048, N <= 2048, where the kernel in 64-row slabs ties or
 // beats the 32x64 tiles once the reduction launch is gone (measured at
 // M = 96 / 128: down 13.2 / 13.2 -> ~9 us, o 9.6 / 9.8 -> ~6.5 us) -- but
-// not where the automatic plan is the narrow kernel, which adds its slices
-// in the same launch.
+// not where the automatic plan is the narrow kernel at M <= 64, which adds
+// its slices in the same launch.
 // Otherwise C is written and *ks = 0.  The partials last until the next call
 // that uses the workspace.
 extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M, int K, int N,
@@ -3734,7 +3751,7 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     if (!g_inited) return QH_ESTATE;
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
     const int auto_plan = vec ? choose_plan(M, K, N, false, vec) : PLAN_SCALAR64;
-    const bool take = vec && !g_forced_plan && auto_plan != PLAN_NARROW &&
+    const bool take = vec && !g_forced_plan && (auto_plan != PLAN_NARROW || M > 64) &&
                       (auto_plan == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
     Ws ws = lib_ws();
     if (take && M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&

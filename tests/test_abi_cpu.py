@@ -53,6 +53,9 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (8, H, I, False, "m16"), (16, H, H, False, "m16"), (4, H, I, False, "m16"), (2, H, Q, False, "m16"),
     (8, Q, H, False, "m16"), (8, I, H, False, "m16"), (12, I, H, False, "skinny"), (16, H, 16384, False, "m16"),
     (4, Q, H, False, "gemv"), (16, H, 32768, False, "wide"), (16, H, I, True, "pipe32x64k128s4"),
+    (128, H, KV, False, "narrow"), (128, H, Q, False, "narrow"), (128, Q, H, False, "narrow"),   # M = 128 prefill
+    (128, I, H, False, "narrow"), (256, H, KV, False, "narrow"), (256, Q, H, False, "pipe32x64k128s4"),
+    (128, H, I, True, "pipe32x64k64s4"), (160, H, Q, False, "pipe32x64k128s4"),
     (64, H, Q + 2 * KV, False, "narrow"), (64, H, I, True, "pipe32x64k128s4"),   # q|k|v, gate|up
     (64, H, Q, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
     (512, H, Q + 2 * KV, False, "xl64x64s3"), (512, H, I, True, "xl128x128"),

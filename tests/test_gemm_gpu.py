@@ -210,7 +210,8 @@ def test_skinny_kernel(M, K, N):
 
 NARROW_SHAPES = [(64, 2048, 1024), (64, 3072, 1024), (48, 2048, 1024), (16, 3072, 1024), (1, 3072, 1024),
                  (64, 4096, 2048), (64, 4096, 64), (7, 1152, 36), (33, 1024, 300), (64, 2048, 1000),
-                 (5, 128, 100), (64, 1024, 20000)]
+                 (5, 128, 100), (64, 1024, 20000), (128, 1024, 1024), (96, 3072, 1024), (256, 1024, 1000),
+                 (200, 2048, 520)]
 
 
 @pytest.mark.parametrize("gated", [False, True], ids=["plain", "gated"])
@@ -218,8 +219,8 @@ def test_narrow_kernel(gated):
     """The narrow kernel (32-column blocks in row slabs, K split over blocks,
     slices added in slice order by the last block of each tile to take a
     ticket), plain and gated (silu(gate) * up), on the geometry it chooses
-    per shape: 1 to 32 slices, one to four row slabs (16-, 32- and 64-row
-    slabs), partial row tiles (M = 1 .. 64) and partial column blocks
+    per shape: 1 to 32 slices, one to sixteen row slabs (16-, 32- and 64-row
+    slabs), partial row tiles (M = 1 .. 256) and partial column blocks
     (N % 32 != 0), one slice only (K = 128).  Device buffers refilled with NaN
     before every call, so an output left unwritten fails; every shape is run
     three times, interleaved with the others (each call must leave its
