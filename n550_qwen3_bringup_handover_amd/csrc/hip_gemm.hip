@@ -1124,10 +1124,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile MFMA GEMM: 32x32x16 bf16 MFMA, 2 x 2 waves, two stages in flight
+// Large-tile MFMA GEMM: 32x32x16 bf16 MFMA, 2 x 2 waves (2 x 4 on 256 x 256
+// tiles), two stages in flight
 // ---------------------------------------------------------------------------
 // Block tile BM x BN, k stages of BK (32 or 64).  Each wave owns a
-// (BM/2) x (BN/2) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
+// (BM/2) x (BN/WNW) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
+// 256 x 256 tiles run eight waves (two per SIMD, 128 x 64 each): with one
+// wave per SIMD the MFMA pipe idles whenever that wave waits (measured on
+// MI355X, graph-replayed: 4096 x 1024 x 4096 45.2 -> 43.3 us, gated 4096 x
+// 1024 x 3072 84.8 -> 72.4 us, 8192 x 1024 x 4096 bf16 A 88.2 -> 83.9 us).
 // Operands move global -> registers -> LDS with 16-byte buffer loads (a
 // fixed 32-bit offset per lane and load, the stage's k offset in a scalar
 // register): A as fp32, rounded to bf16 (RNE) on the way into LDS; B as
@@ -1153,18 +1158,21 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 // Requires K % BK == 0, 16-byte aligned a, b, b2, and fewer than 2^32 bytes
 // in A and in each weight matrix.  Rows >= M and columns >= N are clamped for
 // loading and never stored.
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
+// threads of a large-tile block: eight waves on 256 x 256 tiles, else four
+constexpr int xl_threads(int bm, int bn) { return bm == 256 && bn == 256 ? 512 : 256; }
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WNW = xl_threads(BM, BN) / 128>
 struct XlCfg {
+    static constexpr int NT = 2 * WNW * 64;                      // threads: 2 x WNW waves
     static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
-    static constexpr int WTM = BM / 2, WTN = BN / 2;            // wave tile
+    static constexpr int WTM = BM / 2, WTN = BN / WNW;          // wave tile
     static constexpr int TM = WTM / 32, TN = WTN / 32;          // 32x32 blocks per wave
     static constexpr int BNO = GATED ? BN / 2 : BN;             // output columns per block
     static constexpr int A_SLOT = BM * BK * 2, B_SLOT = BN * BK * 2;
     static constexpr int LDS = 2 * (A_SLOT + B_SLOT);
     static constexpr int A_CPR = ABF16 ? CPR : BK / 4;          // 16-byte A chunks per row
-    static constexpr int A_LOADS = BM * A_CPR / NTHREADS;       // 16-byte A loads per lane
-    static constexpr int B_LOADS = BN * CPR / NTHREADS;         // 16-byte bf16 loads per lane
-    static constexpr int B_ROWS_PER_LOAD = NTHREADS / CPR;
+    static constexpr int A_LOADS = BM * A_CPR / NT;             // 16-byte A loads per lane
+    static constexpr int B_LOADS = BN * CPR / NT;               // 16-byte bf16 loads per lane
+    static constexpr int B_ROWS_PER_LOAD = NT / CPR;
     static constexpr int MFMAS = TM * TN * (BK / 16);           // per wave per stage
     static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
     static_assert(BK == 32 || BK == 64, "k stage");
@@ -1183,13 +1191,13 @@ __device__ __forceinline__ int xl_swz(int r) {
 
 // B-tile row of 32-column block j of wave column wn (gated: the first TN/2
 // blocks are Wg rows, the rest the Wu rows of the same outputs)
-template <int BN, int TN, bool GATED>
+template <int BN, int TN, bool GATED, int WNW>
 __device__ __forceinline__ int xl_brow(int wn, int j) {
     if constexpr (!GATED) {
-        return wn * (BN / 2) + 32 * j;
+        return wn * (BN / WNW) + 32 * j;
     } else {
         constexpr int TNO = TN / 2;
-        const int base = wn * (BN / 4);
+        const int base = wn * (BN / (2 * WNW));
         return (j < TNO) ? base + 32 * j : BN / 2 + base + 32 * (j - TNO);
     }
 }
@@ -1245,7 +1253,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t 
 // loads stage it+2 into the freed registers (one stage of latency cover, for
 // tiles whose two register sets would not fit).
 template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS>
-__global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
+__global__ __launch_bounds__(xl_threads(BM, BN), BM * BN <= 128 * 128 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
@@ -1260,7 +1268,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / (X::NT / 128), wn = wave % (X::NT / 128);
     int tm, tn;
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
@@ -1277,7 +1285,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     int adst[X::A_LOADS];
 #pragma unroll
     for (int i = 0; i < X::A_LOADS; i++) {
-        const int q = i * NTHREADS + tid;
+        const int q = i * X::NT + tid;
         const int r = q / X::A_CPR, cq = q % X::A_CPR;
         const uint32_t row = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K;
         if constexpr (ABF16) {
@@ -1292,7 +1300,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     int bdst[X::B_LOADS];
 #pragma unroll
     for (int i = 0; i < X::B_LOADS; i++) {
-        const int q = i * NTHREADS + tid;
+        const int q = i * X::NT + tid;
         const int r = q / CPR, ch = q % CPR;
         int gn = n0 + r;
         if constexpr (GATED) {
@@ -1313,7 +1321,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
     }
 #pragma unroll
     for (int j = 0; j < X::TN; j++) {
-        const int r = xl_brow<BN, X::TN, GATED>(wn, j) + lrow;
+        const int r = xl_brow<BN, X::TN, GATED, X::NT / 128>(wn, j) + lrow;
         boff[j] = r * (BK * 2);
         bsw[j] = xl_swz<CPR>(r);
     }
@@ -1511,7 +1519,7 @@ __global__ __launch_bounds__(NTHREADS, BM * BN <= 128 * 128 ? 2 : 1) void k_gemm
             constexpr int TNO = X::TN / 2;
 #pragma unroll
             for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (X::BNO / 2) + 32 * j + lrow;
+                const int col = n0 + wn * (X::BNO / (X::NT / 128)) + 32 * j + lrow;
                 if (col < N) {
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
@@ -3197,7 +3205,7 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, 1), dim3(NTHREADS), 0,
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, 1), dim3(X::NT), 0,
                        g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
