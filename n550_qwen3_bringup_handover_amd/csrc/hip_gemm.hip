@@ -3747,8 +3747,10 @@ extern "C" int qh_gemm_noalloc(float *c, const float *a, const uint16_t *b, int 
 // M <= 128, K >= 2048, N <= 2048, where the kernel in 64-row slabs ties or
 // beats the 32x64 tiles once the reduction launch is gone (measured at
 // M = 96 / 128: down 13.2 / 13.2 -> ~9 us, o 9.6 / 9.8 -> ~6.5 us) -- but
-// not where the automatic plan is the narrow kernel at M <= 64, which adds
-// its slices in the same launch.
+// not where the automatic plan is the narrow kernel, which writes C itself
+// (at M = 128 its o and down, with the plain residual + RMSNorm after them,
+// beat the split sums and the norm that adds them: 128-token prefill 1.68
+// -> 1.65 ms, 2,014-token prefill 40.3 -> 39.5 ms).
 // Otherwise C is written and *ks = 0.  The partials last until the next call
 // that uses the workspace.
 extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M, int K, int N,
@@ -3759,7 +3761,7 @@ extern "C" int qh_gemm_split(float *c, const float *a, const uint16_t *b, int M,
     if (!g_inited) return QH_ESTATE;
     const bool vec = M > 0 && K > 0 && N > 0 && a && b && c && (K % 8) == 0 && aligned16(a) && aligned16(b);
     const int auto_plan = vec ? choose_plan(M, K, N, false, vec) : PLAN_SCALAR64;
-    const bool take = vec && !g_forced_plan && (auto_plan != PLAN_NARROW || M > 64) &&
+    const bool take = vec && !g_forced_plan && auto_plan != PLAN_NARROW &&
                       (auto_plan == PLAN_SKINNY || (M <= 128 && K >= 2048 && N <= 2048));
     Ws ws = lib_ws();
     if (take && M <= SKINNY_MMAX && K % 64 == 0 && (size_t)M * K * 4 < (1ull << 31) &&
