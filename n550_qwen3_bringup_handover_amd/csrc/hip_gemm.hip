@@ -1128,7 +1128,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 // tiles), two stages in flight
 // ---------------------------------------------------------------------------
 // Block tile BM x BN, k stages of BK (32 or 64).  Each wave owns a
-// (BM/2) x (BN/WNW) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
+// (BM/WMW) x (BN/WNW) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
 // 256 x 256 tiles run eight waves (two per SIMD, 128 x 64 each): with one
 // wave per SIMD the MFMA pipe idles whenever that wave waits (measured on
 // MI355X, graph-replayed: 4096 x 1024 x 4096 45.2 -> 43.3 us, gated 4096 x
@@ -1158,13 +1158,16 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c
 // Requires K % BK == 0, 16-byte aligned a, b, b2, and fewer than 2^32 bytes
 // in A and in each weight matrix.  Rows >= M and columns >= N are clamped for
 // loading and never stored.
-// threads of a large-tile block: eight waves on 256 x 256 tiles, else four
-constexpr int xl_threads(int bm, int bn) { return bm == 256 && bn == 256 ? 512 : 256; }
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WNW = xl_threads(BM, BN) / 128>
+// waves of a large-tile block along N: four on 256 x 256 tiles, else two;
+// along M (WMW): two, or four for gated 128 x 128 tiles when they do not
+// outnumber the CUs (a wave's gate and up columns stay together)
+constexpr int xl_wn(int bm, int bn) { return bm == 256 && bn == 256 ? 4 : 2; }
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WMW = 2>
 struct XlCfg {
-    static constexpr int NT = 2 * WNW * 64;                      // threads: 2 x WNW waves
+    static constexpr int WNW = xl_wn(BM, BN);
+    static constexpr int NT = 64 * WMW * WNW;                   // threads
     static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
-    static constexpr int WTM = BM / 2, WTN = BN / WNW;          // wave tile
+    static constexpr int WTM = BM / WMW, WTN = BN / WNW;        // wave tile
     static constexpr int TM = WTM / 32, TN = WTN / 32;          // 32x32 blocks per wave
     static constexpr int BNO = GATED ? BN / 2 : BN;             // output columns per block
     static constexpr int A_SLOT = BM * BK * 2, B_SLOT = BN * BK * 2;
@@ -1252,13 +1255,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t 
 // SETS = 1: one register set; each stage stores stage it+1 first and then
 // loads stage it+2 into the freed registers (one stage of latency cover, for
 // tiles whose two register sets would not fit).
-template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS>
-__global__ __launch_bounds__(xl_threads(BM, BN), BM * BN <= 128 * 128 ? 2 : 1) void k_gemm_xl(float *__restrict__ c,
+template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS, int WMW>
+__global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 ? 1 : (BM * BN <= 128 * 128 ? 2 : 1)) void k_gemm_xl(float *__restrict__ c,
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
                                                         int M, int K, int N, TileMap map) {
-    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS>;
+    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS, WMW>;
     constexpr int CPR = X::CPR;
     __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
     __shared__ __align__(16) unsigned char sa1[X::A_SLOT];
@@ -1268,7 +1271,7 @@ __global__ __launch_bounds__(xl_threads(BM, BN), BM * BN <= 128 * 128 ? 2 : 1) v
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / (X::NT / 128), wn = wave % (X::NT / 128);
+    const int wm = wave / X::WNW, wn = wave % X::WNW;
     int tm, tn;
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
@@ -1321,7 +1324,7 @@ __global__ __launch_bounds__(xl_threads(BM, BN), BM * BN <= 128 * 128 ? 2 : 1) v
     }
 #pragma unroll
     for (int j = 0; j < X::TN; j++) {
-        const int r = xl_brow<BN, X::TN, GATED, X::NT / 128>(wn, j) + lrow;
+        const int r = xl_brow<BN, X::TN, GATED, X::WNW>(wn, j) + lrow;
         boff[j] = r * (BK * 2);
         bsw[j] = xl_swz<CPR>(r);
     }
@@ -1519,7 +1522,7 @@ __global__ __launch_bounds__(xl_threads(BM, BN), BM * BN <= 128 * 128 ? 2 : 1) v
             constexpr int TNO = X::TN / 2;
 #pragma unroll
             for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (X::BNO / (X::NT / 128)) + 32 * j + lrow;
+                const int col = n0 + wn * (X::BNO / X::WNW) + 32 * j + lrow;
                 if (col < N) {
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
@@ -3198,6 +3201,11 @@ static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, tru
 
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
+// Gated 128 x 128 tiles run eight waves (4 x 2, two per SIMD) when one round
+// of blocks covers them, else four per block and two blocks per CU
+// (measured on MI355X, graph-replayed, gate|up + SiLU 1024 -> 3072: M = 512
+// 18.0 -> 16.7 us, M = 256 15.8 -> 13.7-14.9 us; with more tiles than CUs
+// eight waves lose: M = 1024 26.4 -> 33.3 us)
 template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
                      int M, int K, int N) {
@@ -3205,7 +3213,16 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, X::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS>), dim3((unsigned)tiles, 1), dim3(X::NT), 0,
+    if constexpr (GATED && BM == 128 && BN == 128) {
+        if (tiles <= g_cus) {
+            hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 4>), dim3((unsigned)tiles, 1),
+                               dim3(XlCfg<BM, BN, BK, GATED, ABF16, SETS, 4>::NT), 0, g_stream, c, a, b, b2, M, K, N,
+                               map);
+            HCHECK(hipGetLastError(), QH_ELAUNCH);
+            return QH_OK;
+        }
+    }
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2>), dim3((unsigned)tiles, 1), dim3(X::NT), 0,
                        g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
