@@ -886,16 +886,17 @@ struct RingCfg {
     static constexpr int CA = BK / 4, CB = BK / 8;      // 16-byte chunks per A / B row
     static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 2;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int A_DMA = A_BYTES / 1024 / 4;   // 1 KB copies per wave per step
-    static constexpr int B_DMA = B_BYTES / 1024 / 4;
+    static constexpr int NW = WM * WN;                  // waves
+    static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB copies per wave per step
+    static constexpr int B_DMA = B_BYTES / 1024 / NW;
     static constexpr int LPS = A_DMA + B_DMA;           // copies per wave per step
     static constexpr int WTM = BM / WM, WTN = BN / WN;
     static constexpr int TM = WTM / 16, TN = WTN / 16;
     static constexpr int BNO = GATED ? BN / 2 : BN;
     static constexpr int LDS = STAGES * STAGE;
     static constexpr int vm(int k) { return k * LPS > 63 ? 63 : k * LPS; }
-    static_assert(WM * WN == 4, "4 waves");
-    static_assert(BM % 32 == 0 && BN % 64 == 0, "every wave issues the same number of copies");
+    static_assert(WM * WN == 4 || WM * WN == 8, "4 or 8 waves");
+    static_assert(A_DMA * NW * 1024 == A_BYTES && B_DMA * NW * 1024 == B_BYTES, "every wave issues the same number of copies");
     static_assert(A_DMA >= 1 && B_DMA >= 1, "copies per wave");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
     static_assert(STAGES >= 2 && (STAGES - 2) * LPS <= 63, "vmcnt range");
@@ -916,8 +917,13 @@ template <int V> struct IC { static constexpr int value = V; };
 // The copy into slot (it-1) % STAGES is safe after the barrier: every wave
 // consumed stage it-1 (its MFMAs ran) before reaching it.  LDS destinations
 // of the copies are wave-uniform and computed from a scalar wave index.
+// WM x WN waves: 2 x 2, or 2 x 4 (16 x 16 wave tiles, two waves per SIMD) for
+// the plain 32 x 64 tiles, whose one block per CU otherwise leaves a single
+// wave per SIMD (measured on MI355X, graph-replayed: 512 x {1024, 2048,
+// 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.75 / 10.6 / 14.5 us, 128 x 1024 x 4096
+// 6.7 -> 6.5 us).
 template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_pipe(float *__restrict__ c,
+__global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict__ c,
                                                           const float *__restrict__ a,
                                                           const uint16_t *__restrict__ b,
                                                           const uint16_t *__restrict__ b2,
@@ -3094,7 +3100,7 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
     if (tiles < 0) return QH_ETOOBIG;
     hipLaunchKernelGGL((k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK>), dim3((unsigned)tiles),
-                       dim3(NTHREADS), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
+                       dim3(64 * WM * WN), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
@@ -3578,7 +3584,7 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_T32x128:  return launch_tile<32, 128, 64, 2, 2, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_T16x64:   return launch_tile<16, 128, 64, 1, 4, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_SCALAR64: return launch_tile<64, 64, 64, 2, 2, GATED, false>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, 2, 4, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, GATED ? 2 : 4, 4, GATED, 128>(c, a, b, b2, M, K, N);
         case PLAN_P32x64k64s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P64x64k64s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256k32: case PLAN_XB128x128: case PLAN_XB256x256s1: {
