@@ -1168,10 +1168,11 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict
 // along M (WMW): two, or four for gated 128 x 128 tiles when they do not
 // outnumber the CUs (a wave's gate and up columns stay together)
 constexpr int xl_wn(int bm, int bn) { return bm == 256 && bn == 256 ? 4 : 2; }
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WMW = 2>
+template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WMW = 2, int KG = 1>
 struct XlCfg {
     static constexpr int WNW = xl_wn(BM, BN);
-    static constexpr int NT = 64 * WMW * WNW;                   // threads
+    static constexpr int NT = 64 * WMW * WNW * KG;              // threads: KG groups of WMW x WNW waves
+    static constexpr int KSG = BK / 16 / KG;                    // k-steps of a stage per wave group
     static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
     static constexpr int WTM = BM / WMW, WTN = BN / WNW;        // wave tile
     static constexpr int TM = WTM / 32, TN = WTN / 32;          // 32x32 blocks per wave
@@ -1182,9 +1183,10 @@ struct XlCfg {
     static constexpr int A_LOADS = BM * A_CPR / NT;             // 16-byte A loads per lane
     static constexpr int B_LOADS = BN * CPR / NT;               // 16-byte bf16 loads per lane
     static constexpr int B_ROWS_PER_LOAD = NT / CPR;
-    static constexpr int MFMAS = TM * TN * (BK / 16);           // per wave per stage
+    static constexpr int MFMAS = TM * TN * KSG;                 // per wave per stage
     static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
     static_assert(BK == 32 || BK == 64, "k stage");
+    static_assert((KG == 1 || KG == 2) && KSG * KG == BK / 16, "wave groups split a stage's k-steps");
     static_assert(SETS >= 1 && SETS <= 3, "register sets");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
     static_assert(A_LOADS >= 1 && B_LOADS >= 1, "loads per lane");
@@ -1261,13 +1263,13 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t 
 // SETS = 1: one register set; each stage stores stage it+1 first and then
 // loads stage it+2 into the freed registers (one stage of latency cover, for
 // tiles whose two register sets would not fit).
-template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS, int WMW>
-__global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 ? 1 : (BM * BN <= 128 * 128 ? 2 : 1)) void k_gemm_xl(float *__restrict__ c,
+template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS, int WMW, int KG>
+__global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN) * KG, WMW * xl_wn(BM, BN) * KG == 8 ? 1 : (BM * BN <= 128 * 128 ? 2 : 1)) void k_gemm_xl(float *__restrict__ c,
                                                         const void *__restrict__ a,
                                                         const uint16_t *__restrict__ b,
                                                         const uint16_t *__restrict__ b2,
                                                         int M, int K, int N, TileMap map) {
-    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS, WMW>;
+    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS, WMW, KG>;
     constexpr int CPR = X::CPR;
     __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
     __shared__ __align__(16) unsigned char sa1[X::A_SLOT];
@@ -1277,7 +1279,8 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / X::WNW, wn = wave % X::WNW;
+    const int kg = wave / (WMW * X::WNW), wq = wave % (WMW * X::WNW);   // k group, wave within it
+    const int wm = wq / X::WNW, wn = wq % X::WNW;
     int tm, tn;
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
@@ -1386,12 +1389,12 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 
     // while the MFMAs of k-step t run
     auto compute = [&](auto SET) {
         constexpr int set = decltype(SET)::value;
-        constexpr int KS = BK / 16;
+        constexpr int KS = X::KSG;                               // this group's k-steps: kg KS ..
         const unsigned char *as = set ? sa1 : sa0;
         const unsigned char *bs = set ? sb1 : sb0;
         bf16x8 fa[2][X::TM], fb[2][X::TN];
         auto read = [&](int t, int f) {
-            const int ch = 2 * t + lk;
+            const int ch = 2 * (kg * KS + t) + lk;
 #pragma unroll
             for (int i = 0; i < X::TM; i++)
                 fa[f][i] = *reinterpret_cast<const bf16x8 *>(as + aoff[i] + ((ch ^ asw[i]) << 4));
@@ -1443,7 +1446,7 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 
             load(it + 2, IC<0>{});
             compute(IC<set>{});
         }
-        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS, SETS == 1>::run();
+        XlSched<0, X::MFMAS, X::KSG, X::TM + X::TN, X::LOADS, SETS == 1>::run();
         __syncthreads();
     };
     auto tail = [&](int it, auto SET) {
@@ -1467,7 +1470,7 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 
         load(it + 3, IC<r % 3>{});
         compute(IC<r & 1>{});
         store(IC<(r + 1) & 1>{}, IC<(r + 1) % 3>{});
-        XlSched<0, X::MFMAS, BK / 16, X::TM + X::TN, X::LOADS, false>::run();
+        XlSched<0, X::MFMAS, X::KSG, X::TM + X::TN, X::LOADS, false>::run();
         __syncthreads();
     };
     auto tail3 = [&](int it, auto R) {
@@ -1505,6 +1508,28 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN), WMW * xl_wn(BM, BN) == 8 
         tail(it, IC<0>{});
         if (it + 1 < nk) tail(it + 1, IC<1>{});
         if (it + 2 < nk) tail(it + 2, IC<0>{});
+    }
+
+    // two wave groups: the second adds its sums into the first's through LDS
+    if constexpr (KG == 2) {
+        __shared__ float xred[(X::NT / 2) * X::TM * X::TN * 16];
+        __syncthreads();
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < X::TM; i++)
+#pragma unroll
+                for (int j = 0; j < X::TN; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) xred[(((wq * X::TM + i) * X::TN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < X::TM; i++)
+#pragma unroll
+            for (int j = 0; j < X::TN; j++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[i][j][v] += xred[(((wq * X::TM + i) * X::TN + j) * 16 + v) * 64 + lane];
     }
 
     // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
@@ -3207,11 +3232,16 @@ static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, tru
 
 // requires K % BK == 0, 16-byte aligned a, b, b2 and operands below 4 GiB
 // (checked by the caller)
-// Gated 128 x 128 tiles run eight waves (4 x 2, two per SIMD) when one round
-// of blocks covers them, else four per block and two blocks per CU
-// (measured on MI355X, graph-replayed, gate|up + SiLU 1024 -> 3072: M = 512
-// 18.0 -> 16.7 us, M = 256 15.8 -> 13.7-14.9 us; with more tiles than CUs
-// eight waves lose: M = 1024 26.4 -> 33.3 us)
+// When one round of blocks covers the tiles, a block with one wave per SIMD
+// leaves the MFMA pipe idle while that wave waits, so two layouts run eight
+// waves instead: gated 128 x 128 tiles as 4 x 2 waves, and 64 x 64 tiles as
+// two groups of 2 x 2 waves that split each stage's k-steps, the second
+// group adding its sums into the first's through LDS at the end (measured
+// on MI355X, graph-replayed: gate|up + SiLU 512 x 1024 -> 3072 18.0 -> 16.7
+// us, 256 rows 15.8 -> 13.7-14.9; 64 x 64 tiles 512 x 1024 x 2048 8.46 ->
+// 7.83 us, 1024 x 2048 x 1024 13.65 -> 12.7, 1024 x 1024 x 1024 8.2 -> 7.7,
+// 1024 x 3072 x 1024 18.7 -> 18.2).  With more tiles than CUs, two blocks
+// of four waves per CU stay faster (gated M = 1024 26.4 against 33.3 us).
 template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
                      int M, int K, int N) {
@@ -3221,14 +3251,23 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
     if (tiles < 0) return QH_ETOOBIG;
     if constexpr (GATED && BM == 128 && BN == 128) {
         if (tiles <= g_cus) {
-            hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 4>), dim3((unsigned)tiles, 1),
+            hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 4, 1>), dim3((unsigned)tiles, 1),
                                dim3(XlCfg<BM, BN, BK, GATED, ABF16, SETS, 4>::NT), 0, g_stream, c, a, b, b2, M, K, N,
                                map);
             HCHECK(hipGetLastError(), QH_ELAUNCH);
             return QH_OK;
         }
     }
-    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2>), dim3((unsigned)tiles, 1), dim3(X::NT), 0,
+    if constexpr (BM == 64 && BN == 64 && BK == 64 && !GATED) {
+        if (tiles <= g_cus) {
+            hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2, 2>), dim3((unsigned)tiles, 1),
+                               dim3(XlCfg<BM, BN, BK, GATED, ABF16, SETS, 2, 2>::NT), 0, g_stream, c, a, b, b2, M, K, N,
+                               map);
+            HCHECK(hipGetLastError(), QH_ELAUNCH);
+            return QH_OK;
+        }
+    }
+    hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2, 1>), dim3((unsigned)tiles, 1), dim3(X::NT), 0,
                        g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
