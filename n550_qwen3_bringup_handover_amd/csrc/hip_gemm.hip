@@ -3234,14 +3234,17 @@ static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, tru
 // (checked by the caller)
 // When one round of blocks covers the tiles, a block with one wave per SIMD
 // leaves the MFMA pipe idle while that wave waits, so two layouts run eight
-// waves instead: gated 128 x 128 tiles as 4 x 2 waves, and 64 x 64 tiles as
-// two groups of 2 x 2 waves that split each stage's k-steps, the second
-// group adding its sums into the first's through LDS at the end (measured
-// on MI355X, graph-replayed: gate|up + SiLU 512 x 1024 -> 3072 18.0 -> 16.7
-// us, 256 rows 15.8 -> 13.7-14.9; 64 x 64 tiles 512 x 1024 x 2048 8.46 ->
-// 7.83 us, 1024 x 2048 x 1024 13.65 -> 12.7, 1024 x 1024 x 1024 8.2 -> 7.7,
-// 1024 x 3072 x 1024 18.7 -> 18.2).  With more tiles than CUs, two blocks
-// of four waves per CU stay faster (gated M = 1024 26.4 against 33.3 us).
+// waves instead: gated 128 x 128 tiles as 4 x 2 waves, and the other tiles
+// up to 128 x 128 (BK = 64) as two groups of 2 x 2 waves that split each
+// stage's k-steps, the second group adding its sums into the first's
+// through LDS at the end (measured on MI355X, graph-replayed: gate|up + SiLU
+// 512 x 1024 -> 3072 18.0 -> 16.7 us, 256 rows 15.8 -> 13.7-14.9; 64 x 64
+// tiles 512 x 1024 x 2048 8.46 -> 7.83 us, 1024 x 2048 x 1024 13.65 ->
+// 12.7, 1024 x 1024 x 1024 8.2 -> 7.7; 128 x 128 tiles 4096 x {1024, 2048,
+// 3072} x 1024 19.2 / 32 / 44 -> 17.8 / 27 / 37.8, 2048 x 1024 x 2048 18.9
+// -> 17.6; 64 x 128 tiles 2048 x 1024 x 1024 12.8 -> 11.3).  With more
+// tiles than CUs, two blocks of four waves per CU stay faster (gated M =
+// 1024 26.4 against 33.3 us).
 template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2>
 static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t *b2,
                      int M, int K, int N) {
@@ -3258,7 +3261,7 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
             return QH_OK;
         }
     }
-    if constexpr (BM == 64 && BN == 64 && BK == 64 && !GATED) {
+    if constexpr (BK == 64 && BM * BN <= 128 * 128 && !GATED) {
         if (tiles <= g_cus) {
             hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2, 2>), dim3((unsigned)tiles, 1),
                                dim3(XlCfg<BM, BN, BK, GATED, ABF16, SETS, 2, 2>::NT), 0, g_stream, c, a, b, b2, M, K, N,
