@@ -2904,11 +2904,26 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
     // all 256 CUs, gate|up from M = 2048 with A rounded to bf16 by one pass
     // first, 128 x 128 otherwise.
     if (K % 64 == 0 && (size_t)M * K * 4 < (1ull << 32) && (size_t)N * K * 2 < (1ull << 32)) {
+        // One round of 64 x 128 tiles (192 .. 256 of them, eight waves per
+        // block in two k groups), else of 128 x 128 tiles from M = 512, else
+        // of 64 x 64 tiles (measured on MI355X, graph-replayed: 512 x 1024 x
+        // 4096 13.6 -> 11.7 us, 384 x 1024 x 4096 12.4 -> 10.8, 1024 x 1024 x
+        // 2048 13.0 -> 11.4, 2048 x 2048 x 1024 21.9 -> 18.1, 2048 x 3072 x 1024
+        // 30.2 -> 23.8 against the 64 x 64 tiles; 768 x 1024 x 4096 19.3 ->
+        // 17.0 on 128 x 128; 256 x 1024 x 4096 10.3 -> 8.7 against the 32 x 64
+        // ring tiles)
+        if (!gated && M >= 256 && blocks(64, 128) >= 192 && blocks(64, 128) <= g_cus) return PLAN_X64x128;
+        if (!gated && M >= 512 && blocks(128, 128) >= 192 && blocks(128, 128) <= g_cus) return PLAN_X128x128;
+        if (!gated && M >= 256 && blocks(64, 64) >= 192 && blocks(64, 64) <= g_cus) return PLAN_X64x64s3;
+        // gated between 128 and 512 rows where 128 x 128 tiles would leave
+        // half the chip idle: 64 x 128 tiles (256 x 1024 x 3072: 15.3 -> 12.8 us
+        // against the 64 x 64 tiles)
+        if (gated && M > 128 && blocks(128, 128) < 128 && blocks(64, 128) >= 128) return PLAN_X64x128;
         // 64 x 64 tiles (two blocks per CU, three stages in flight) where they
         // make one or two rounds at K = 1024 (measured on MI355X: 512x1024x2048
         // 9.3 -> 8.2 us, 512x1024x4096 12.8 -> 12.2, 1024x1024x2048 12.4 -> 11.5,
         // 1024x1024x1024 8.5 -> 8.0; at 512x1024x1024 they lose, 7.6 vs 6.6)
-        if (!gated && M >= 512 && M <= 1024 && K <= 1024 && blocks(64, 64) >= 256 && blocks(64, 64) <= 512)
+        if (!gated && M >= 256 && M <= 1024 && K <= 1024 && blocks(64, 64) >= 256 && blocks(64, 64) <= 512)
             return PLAN_X64x64s3;
         // and for the K-heavy narrow shapes (o, down) at M = 1024 .. 2048, where
         // the third stage in flight pays (1024x2048x1024 15.8 -> 13.9 us,
@@ -2931,7 +2946,10 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
             // 256 x 256 tiles; below M = 8192 without the bf16 rounding pass of A
             // (measured on MI355X, 4096 x 1024 x 4096: 42.3 vs 45.6 us)
             if (!gated && blocks(256, 256) >= 256) return M >= 8192 ? PLAN_XB256x256s1 : PLAN_X256x256;
-            if (gated && M >= 2048) return PLAN_XB128x128;
+            // gated from M = 2048: one round of 256 x 256 tiles on eight waves
+            // where they fit (2048 x 1024 x 3072: 38.3 -> 36.7 us), else A
+            // rounded to bf16 first and 128 x 128 tiles
+            if (gated && M >= 2048) return blocks(256, 256) <= g_cus ? PLAN_X256x256 : PLAN_XB128x128;
             return PLAN_X128x128;
         }
         if (M > 128 && blocks(128, 128) >= 128)

@@ -56,12 +56,15 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (128, H, KV, False, "narrow"), (128, H, Q, False, "narrow"), (128, Q, H, False, "narrow"),   # M = 128 prefill
     (128, I, H, False, "narrow"), (256, H, KV, False, "narrow"), (256, Q, H, False, "pipe32x64k128s4"),
     (128, H, I, True, "pipe32x64k64s4"), (160, H, Q, False, "pipe32x64k128s4"),
+    (256, H, I, True, "xl64x128"), (256, H, Q + 2 * KV, False, "xl64x64s3"), (1024, H, Q, False, "xl64x128"),
+    (2048, I, H, False, "xl64x128"), (384, H, Q + 2 * KV, False, "xl64x128"),
+    (768, H, Q + 2 * KV, False, "xl128x128"), (2048, H, I, True, "xl256x256"), (4096, H, I, True, "xb128x128"),
     (64, H, Q + 2 * KV, False, "narrow"), (64, H, I, True, "pipe32x64k128s4"),   # q|k|v, gate|up
     (64, H, Q, False, "narrow"), (128, H, Q + 2 * KV, False, "pipe32x64k128s4"),
-    (512, H, Q + 2 * KV, False, "xl64x64s3"), (512, H, I, True, "xl128x128"),
+    (512, H, Q + 2 * KV, False, "xl64x128"), (512, H, I, True, "xl128x128"),
     (512, H, Q, False, "xl64x64s3"), (512, I, H, False, "pipe32x64k128s4"), (512, H, KV, False, "pipe32x64k128s4"),
     (1024, H, KV, False, "xl64x64s3"), (2048, H, KV, False, "xl64x128"),
-    (1024, I, H, False, "xl64x64s3"), (2048, Q, H, False, "xl64x64s3"), (4096, I, H, False, "xl128x128"),
+    (1024, I, H, False, "xl64x64s3"), (2048, Q, H, False, "xl64x128"), (4096, I, H, False, "xl128x128"),
     (8, 33, 128, False, "mfma64x64-scalar"),                      # K % 8 != 0: element-wise loads
 ])
 def test_automatic_plan_table(M, K, N, gated, plan):
