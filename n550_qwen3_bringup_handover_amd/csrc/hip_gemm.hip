@@ -879,14 +879,15 @@ __device__ __forceinline__ int swz(int r) {
 // encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at max)
 #define QH_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
 
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_ = 32>
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_ = 32, int KG = 1>
 struct RingCfg {
     static constexpr int BK = BK_;                      // k per stage (32, 64, 128)
     static constexpr int KS = BK / 32;                  // MFMA k-steps per stage
+    static constexpr int KSG = KS / KG;                 // ... per wave group
     static constexpr int CA = BK / 4, CB = BK / 8;      // 16-byte chunks per A / B row
     static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 2;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int NW = WM * WN;                  // waves
+    static constexpr int NW = WM * WN * KG;             // waves: KG groups of WM x WN
     static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB copies per wave per step
     static constexpr int B_DMA = B_BYTES / 1024 / NW;
     static constexpr int LPS = A_DMA + B_DMA;           // copies per wave per step
@@ -895,7 +896,8 @@ struct RingCfg {
     static constexpr int BNO = GATED ? BN / 2 : BN;
     static constexpr int LDS = STAGES * STAGE;
     static constexpr int vm(int k) { return k * LPS > 63 ? 63 : k * LPS; }
-    static_assert(WM * WN == 4 || WM * WN == 8, "4 or 8 waves");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+    static_assert((KG == 1 || KG == 2) && KSG * KG == KS, "wave groups split a stage's k-steps");
     static_assert(A_DMA * NW * 1024 == A_BYTES && B_DMA * NW * 1024 == B_BYTES, "every wave issues the same number of copies");
     static_assert(A_DMA >= 1 && B_DMA >= 1, "copies per wave");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
@@ -917,25 +919,29 @@ template <int V> struct IC { static constexpr int value = V; };
 // The copy into slot (it-1) % STAGES is safe after the barrier: every wave
 // consumed stage it-1 (its MFMAs ran) before reaching it.  LDS destinations
 // of the copies are wave-uniform and computed from a scalar wave index.
-// WM x WN waves: 2 x 2, or 2 x 4 (16 x 16 wave tiles, two waves per SIMD) for
-// the plain 32 x 64 tiles, whose one block per CU otherwise leaves a single
-// wave per SIMD (measured on MI355X, graph-replayed: 512 x {1024, 2048,
-// 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.75 / 10.6 / 14.5 us, 128 x 1024 x 4096
-// 6.7 -> 6.5 us).
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_>
-__global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict__ c,
+// KG groups of WM x WN waves: with KG = 2 (the 32 x 64 tiles with 128-deep
+// stages, one block per CU) the groups split each stage's k-steps and the
+// second adds its sums into the first's through LDS at the end, so that two
+// waves share each SIMD (measured on MI355X, graph-replayed, against one
+// group of 2 x 2: 512 x {1024, 2048, 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.4 /
+// 9.65 / 12.8 us, 128 x 1024 x 4096 6.7 -> 6.2, gate|up + SiLU 64 x 1024 x
+// 3072 6.74 -> 6.27; 2 x 4 waves on the plain tiles instead reached 6.75 /
+// 10.6 / 14.5).
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_, int KG>
+__global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__restrict__ c,
                                                           const float *__restrict__ a,
                                                           const uint16_t *__restrict__ b,
                                                           const uint16_t *__restrict__ b2,
                                                           int M, int K, int N, TileMap map) {
-    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_>;
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_, KG>;
     static_assert(STAGES >= 3, "one stage being read, one in use, one or more in flight");
     extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // scalar
-    const int wm = wave / WN, wn = wave % WN;
+    const int kg = wave / (WM * WN), wq = wave % (WM * WN);   // k group, wave within it
+    const int wm = wq / WN, wn = wq % WN;
     int tm, tn;
     tile_of(blockIdx.x, map, tm, tn);
     const int m0 = tm * BM;
@@ -1004,23 +1010,24 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict
         brow_sw[j] = swz<R::CB>(row);
     }
 
-    u32x4 fa[2][R::KS][R::TM][2], fb[2][R::KS][R::TN];
+    u32x4 fa[2][R::KSG][R::TM][2], fb[2][R::KSG][R::TN];
     // `SET` selects the register set at compile time (IC<0> / IC<1>)
     auto read_frags = [&](int step, auto SET) {
         constexpr int set = decltype(SET)::value;
         const unsigned char *slot = smem + (step % STAGES) * R::STAGE;
 #pragma unroll
-        for (int t = 0; t < R::KS; t++) {
+        for (int tt = 0; tt < R::KSG; tt++) {
+            const int t = kg * R::KSG + tt;                   // this group's k-steps
 #pragma unroll
             for (int i = 0; i < R::TM; i++) {
                 const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + arow_off[i]);
-                fa[set][t][i][0] = rowp[(8 * t + 2 * lgrp) ^ arow_sw[i]];
-                fa[set][t][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ arow_sw[i]];
+                fa[set][tt][i][0] = rowp[(8 * t + 2 * lgrp) ^ arow_sw[i]];
+                fa[set][tt][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ arow_sw[i]];
             }
 #pragma unroll
             for (int j = 0; j < R::TN; j++) {
                 const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + brow_off[j]);
-                fb[set][t][j] = rowp[(4 * t + lgrp) ^ brow_sw[j]];
+                fb[set][tt][j] = rowp[(4 * t + lgrp) ^ brow_sw[j]];
             }
         }
     };
@@ -1034,7 +1041,7 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict
     auto mfmas = [&](auto SET) {
         constexpr int set = decltype(SET)::value;
 #pragma unroll
-        for (int t = 0; t < R::KS; t++) {
+        for (int t = 0; t < R::KSG; t++) {
             bf16x8 af[R::TM];
 #pragma unroll
             for (int i = 0; i < R::TM; i++) {
@@ -1097,6 +1104,24 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void k_gemm_pipe(float *__restrict
     for (int it = 0; it < nk; it += 2) {
         step(it, IC<0>{});
         if (it + 1 < nk) step(it + 1, IC<1>{});
+    }
+
+    // two wave groups: the second adds its sums into the first's through LDS
+    if constexpr (KG == 2) {
+        f32x4 *xred = reinterpret_cast<f32x4 *>(smem);
+        __syncthreads();                                   // every wave is done with the ring
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < R::TM; i++)
+#pragma unroll
+                for (int j = 0; j < R::TN; j++) xred[((wq * R::TM + i) * R::TN + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < R::TM; i++)
+#pragma unroll
+            for (int j = 0; j < R::TN; j++) acc[i][j] += xred[((wq * R::TM + i) * R::TN + j) * 64 + lane];
     }
 
     // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
@@ -3128,13 +3153,13 @@ static int launch_tile(float *c, const float *a, const uint16_t *b, const uint16
 }
 
 // requires K % BK == 0 and 16-byte aligned a, b, b2 (checked by the caller)
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32>
+template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32, int KG = 1>
 static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                        int M, int K, int N) {
-    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK>;
+    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK, KG>;
     static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
     if (!attr_set) {
-        HCHECK(hipFuncSetAttribute((const void *)k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK>,
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK, KG>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS),
                QH_ELAUNCH);
         attr_set = true;
@@ -3142,8 +3167,8 @@ static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
     if (tiles < 0) return QH_ETOOBIG;
-    hipLaunchKernelGGL((k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK>), dim3((unsigned)tiles),
-                       dim3(64 * WM * WN), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
+    hipLaunchKernelGGL((k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK, KG>), dim3((unsigned)tiles),
+                       dim3(64 * WM * WN * KG), R::LDS, g_stream, c, a, b, b2, M, K, N, map);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
@@ -3644,7 +3669,7 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_T32x128:  return launch_tile<32, 128, 64, 2, 2, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_T16x64:   return launch_tile<16, 128, 64, 1, 4, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_SCALAR64: return launch_tile<64, 64, 64, 2, 2, GATED, false>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, GATED ? 2 : 4, 4, GATED, 128>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, 2, 4, GATED, 128, 2>(c, a, b, b2, M, K, N);
         case PLAN_P32x64k64s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P64x64k64s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256k32: case PLAN_XB128x128: case PLAN_XB256x256s1: {
