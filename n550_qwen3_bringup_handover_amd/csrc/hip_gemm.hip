@@ -2935,11 +2935,11 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
         // 4096 13.6 -> 11.7 us, 384 x 1024 x 4096 12.4 -> 10.8, 1024 x 1024 x
         // 2048 13.0 -> 11.4, 2048 x 2048 x 1024 21.9 -> 18.1, 2048 x 3072 x 1024
         // 30.2 -> 23.8 against the 64 x 64 tiles; 768 x 1024 x 4096 19.3 ->
-        // 17.0 on 128 x 128; 256 x 1024 x 4096 10.3 -> 8.7 against the 32 x 64
-        // ring tiles)
+        // 17.0 on 128 x 128; 256 / 192 x 1024 x 4096 10.3 / 9.6 -> 8.7 / 8.2
+        // against the 32 x 64 ring tiles)
         if (!gated && M >= 256 && blocks(64, 128) >= 192 && blocks(64, 128) <= g_cus) return PLAN_X64x128;
         if (!gated && M >= 512 && blocks(128, 128) >= 192 && blocks(128, 128) <= g_cus) return PLAN_X128x128;
-        if (!gated && M >= 256 && blocks(64, 64) >= 192 && blocks(64, 64) <= g_cus) return PLAN_X64x64s3;
+        if (!gated && M > 128 && blocks(64, 64) >= 192 && blocks(64, 64) <= g_cus) return PLAN_X64x64s3;
         // gated between 128 and 512 rows where 128 x 128 tiles would leave
         // half the chip idle: 64 x 128 tiles (256 x 1024 x 3072: 15.3 -> 12.8 us
         // against the 64 x 64 tiles)
