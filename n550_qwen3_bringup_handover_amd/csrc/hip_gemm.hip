@@ -2941,9 +2941,11 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
         if (!gated && M >= 512 && blocks(128, 128) >= 192 && blocks(128, 128) <= g_cus) return PLAN_X128x128;
         if (!gated && M > 128 && blocks(64, 64) >= 192 && blocks(64, 64) <= g_cus) return PLAN_X64x64s3;
         // gated between 128 and 512 rows where 128 x 128 tiles would leave
-        // half the chip idle: 64 x 128 tiles (256 x 1024 x 3072: 15.3 -> 12.8 us
-        // against the 64 x 64 tiles)
+        // half the chip idle, and between 512 and 1024: 64 x 128 tiles (256 x
+        // 1024 x 3072: 15.3 -> 10.4 us against the 64 x 64 tiles; 768 / 1024
+        // rows 25.6 / 26.7 -> 24.2 / 25.7 against 128 x 128)
         if (gated && M > 128 && blocks(128, 128) < 128 && blocks(64, 128) >= 128) return PLAN_X64x128;
+        if (gated && M > 512 && M <= 1024) return PLAN_X64x128;
         // 64 x 64 tiles (two blocks per CU, three stages in flight) where they
         // make one or two rounds at K = 1024 (measured on MI355X: 512x1024x2048
         // 9.3 -> 8.2 us, 512x1024x4096 12.8 -> 12.2, 1024x1024x2048 12.4 -> 11.5,
@@ -3278,7 +3280,8 @@ static Ws lib_ws(void) { return Ws{g_abf, g_abf_elems, g_part, g_part_bytes, tru
 // When one round of blocks covers the tiles, a block with one wave per SIMD
 // leaves the MFMA pipe idle while that wave waits, so two layouts run eight
 // waves instead: gated 128 x 128 tiles as 4 x 2 waves, and the other tiles
-// up to 128 x 128 (BK = 64) as two groups of 2 x 2 waves that split each
+// up to 128 x 128 (BK = 64; gated 64 x 128 too: 256 x 1024 -> 3072 gate|up +
+// SiLU 12.1 -> 10.4 us) as two groups of 2 x 2 waves that split each
 // stage's k-steps, the second group adding its sums into the first's
 // through LDS at the end (measured on MI355X, graph-replayed: gate|up + SiLU
 // 512 x 1024 -> 3072 18.0 -> 16.7 us, 256 rows 15.8 -> 13.7-14.9; 64 x 64
@@ -3304,7 +3307,7 @@ static int launch_xl(float *c, const void *a, const uint16_t *b, const uint16_t 
             return QH_OK;
         }
     }
-    if constexpr (BK == 64 && BM * BN <= 128 * 128 && !GATED) {
+    if constexpr (BK == 64 && BM * BN <= 128 * 128 && (!GATED || BM * BN < 128 * 128)) {
         if (tiles <= g_cus) {
             hipLaunchKernelGGL((k_gemm_xl<BM, BN, BK, GATED, ABF16, SETS, 2, 2>), dim3((unsigned)tiles, 1),
                                dim3(XlCfg<BM, BN, BK, GATED, ABF16, SETS, 2, 2>::NT), 0, g_stream, c, a, b, b2, M, K, N,
