@@ -2974,9 +2974,11 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
             // (measured on MI355X, 4096 x 1024 x 4096: 42.3 vs 45.6 us)
             if (!gated && blocks(256, 256) >= 256) return M >= 8192 ? PLAN_XB256x256s1 : PLAN_X256x256;
             // gated from M = 2048: one round of 256 x 256 tiles on eight waves
-            // where they fit (2048 x 1024 x 3072: 38.3 -> 36.7 us), else A
-            // rounded to bf16 first and 128 x 128 tiles
-            if (gated && M >= 2048) return blocks(256, 256) <= g_cus ? PLAN_X256x256 : PLAN_XB128x128;
+            // where they fit, and from M = 8192 (2048 / 8192 x 1024 x 3072: 39.4 /
+            // 136 -> 37.3 / 120.6 us), else A rounded to bf16 first and 128 x 128
+            // tiles (4096 rows: 68 against 75 us on 256 x 256)
+            if (gated && M >= 2048)
+                return (blocks(256, 256) <= g_cus || M >= 8192) ? PLAN_X256x256 : PLAN_XB128x128;
             return PLAN_X128x128;
         }
         if (M > 128 && blocks(128, 128) >= 128)
