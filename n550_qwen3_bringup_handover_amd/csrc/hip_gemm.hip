@@ -2243,7 +2243,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
 // ---------------------------------------------------------------------------
 // One block per CU, four independent waves.  The block's 16 MT rows of A sit
 // in LDS as bf16 for the whole launch (RNE; 16-byte chunks XOR-swizzled by
-// row); each wave walks its own 32-column tiles (tile t = wave + j * waves)
+// row); each wave walks its own 32-column tiles (DEF = 0: tile t = wave + j
+// waves)
 // over the whole of K, in chunks of 64 k.  A chunk's weights -- 32 rows x
 // 128 bytes -- are read with every load instruction covering 8 rows x 128
 // contiguous bytes (the MFMA fragment order, 16 rows x 64 bytes per
@@ -2251,13 +2252,20 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
 // own 4 KB of LDS, and read back as 16x16x32 MFMA fragments.  WIDE_D chunks
 // are in flight per wave; no block or wave waits for another.  Loads past N
 // read zeros at out-of-range offsets; rows past M are zeros in LDS.
+// DEF > 0 (every wave has at most DEF tiles, as for the 151,936-column
+// lm_head): wave gw takes the DEF consecutive tiles from DEF gw, holds each
+// finished tile's sums in registers and writes them all after its last one,
+// so that C goes out in rows of DEF x 128 contiguous bytes after the weight
+// stream instead of interleaved with it (measured on MI355X, graph-replayed,
+// 64 / 32 / 8 x 1024 x 151936: 66.0 / 58.9 / 50.7 -> 59.6 / 52.0 / 47.8 us;
+// holding the tiles but keeping the strided tile order: 64.2 / 54.8 / 48.9).
 #define WIDE_KC 64            // k per chunk
 #define WIDE_D 4              // chunks in flight per wave (K / WIDE_KC must be a multiple)
 #define WIDE_A_BYTES (128 * 1024)
 #define WIDE_B_U4 (32 * WIDE_KC / 8)   // 16-byte chunks of one wave's staged weights
 __device__ __forceinline__ int wide_key(int row) { return (row ^ (row >> 3)) & 7; }
 
-template <int MT, int NCH>
+template <int MT, int NCH, int DEF>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c, const float *__restrict__ a,
                                                           const uint16_t *__restrict__ b, int M, int N,
                                                           int ntiles) {
@@ -2269,7 +2277,11 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
     u32x4 *const sa = wide_lds;                            // [ROWS][CHA] A, swizzled
     u32x4 *const sb = wide_lds + ROWS * CHA + w * WIDE_B_U4;   // this wave's staged chunk
     const int gw = blockIdx.x * NW + w, nwaves = gridDim.x * NW;
-    const int my_tiles = gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0;
+    // tiles of this wave: gw, gw + nwaves, ...; with DEF, the DEF consecutive
+    // tiles from gw DEF (their C rows then go out DEF x 128 contiguous bytes)
+    const int my_tiles = DEF > 0 ? min(max(ntiles - gw * DEF, 0), DEF)
+                                 : (gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0);
+    auto tile_index = [&](int ti) { return DEF > 0 ? gw * DEF + ti : gw + ti * nwaves; };
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
 
     // the loads of chunk kc of tile number ti (of this wave): instruction i
@@ -2277,7 +2289,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
     // (32-bit offsets, N * K * 2 < 2^31; computed without branches so that
     // every load is issued where it stands)
     auto issue = [&](u32x4 (&dst)[4], int ti, int kc) {
-        const int t = gw + ti * nwaves;
+        const int t = tile_index(ti);
         const bool live = ti < my_tiles;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -2322,6 +2334,42 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
     }
     __syncthreads();
 
+    // The tile out through the wave's staging space (see below)
+    auto store_half = [&](const f32x4 (&acc)[2][MT], int ti, const int h) {
+        // The tile out through the wave's staging space, 32 rows at a time, so
+        // that every store instruction writes 8 rows x 128 contiguous bytes
+        // (4-byte stores straight from the MFMA layout, 4 rows x 64 bytes per
+        // instruction, write back at well under half the speed).  Lane holds
+        // rows 16 mt + 4 g + r, column 16 nt + r16; LDS row-major [32][32]
+        // fp32 with the 16-byte chunk XOR-swizzled by row.
+        const int t = tile_index(ti);
+        float *const sc = reinterpret_cast<float *>(sb);
+        const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, (size_t)M * N * 4);
+        {
+#pragma unroll
+            for (int mh = 0; mh < 2 && 2 * h + mh < MT; mh++)
+#pragma unroll
+                for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int row = 16 * mh + 4 * g + r, col = 16 * nt + r16;
+                        sc[row * 32 + ((((col >> 2) ^ (row & 7)) << 2) | (col & 3))] = acc[nt][2 * h + mh][r];
+                    }
+#pragma unroll
+            for (int i = 0; i < (MT >= 2 ? 4 : 2); i++) {
+                const int row = 8 * i + (lane >> 3), cq = lane & 7;
+                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sc[row * 32 + ((cq ^ (row & 7)) << 2)]);
+                const int m = 32 * h + row, n = 32 * t + 4 * cq;
+                const uint32_t off = (m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 0);
+            }
+        }
+    };
+    auto store_tile = [&](const f32x4 (&acc)[2][MT], int ti) {
+#pragma unroll
+        for (int h = 0; h < (MT + 1) / 2; h++) store_half(acc, ti, h);
+    };
+    f32x4 held[DEF > 0 ? DEF : 1][2][MT];                 // finished tiles, written after the last one
     // one iteration per tile, its NCH chunks unrolled: chunk kc always uses
     // ring slot kc % WIDE_D, and the accumulators live inside the iteration
     for (int ti = 0; ti < my_tiles; ti++) {
@@ -2365,35 +2413,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
                         acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[nt][mt], 0, 0, 0);
             }
         }
-        // The tile out through the wave's staging space, 32 rows at a time, so
-        // that every store instruction writes 8 rows x 128 contiguous bytes
-        // (4-byte stores straight from the MFMA layout, 4 rows x 64 bytes per
-        // instruction, write back at well under half the speed).  Lane holds
-        // rows 16 mt + 4 g + r, column 16 nt + r16; LDS row-major [32][32]
-        // fp32 with the 16-byte chunk XOR-swizzled by row.
-        const int t = gw + ti * nwaves;
-        float *const sc = reinterpret_cast<float *>(sb);
-        const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, (size_t)M * N * 4);
+        if constexpr (DEF == 0) {
+            store_tile(acc, ti);
+        } else {
 #pragma unroll
-        for (int h = 0; h < (MT + 1) / 2; h++) {
+            for (int q = 0; q < DEF; q++)
+                if (q == ti) {
 #pragma unroll
-            for (int mh = 0; mh < 2 && 2 * h + mh < MT; mh++)
+                    for (int nt = 0; nt < 2; nt++)
 #pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int row = 16 * mh + 4 * g + r, col = 16 * nt + r16;
-                        sc[row * 32 + ((((col >> 2) ^ (row & 7)) << 2) | (col & 3))] = acc[nt][2 * h + mh][r];
-                    }
-#pragma unroll
-            for (int i = 0; i < (MT >= 2 ? 4 : 2); i++) {
-                const int row = 8 * i + (lane >> 3), cq = lane & 7;
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sc[row * 32 + ((cq ^ (row & 7)) << 2)]);
-                const int m = 32 * h + row, n = 32 * t + 4 * cq;
-                const uint32_t off = (m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 0);
-            }
+                        for (int mt = 0; mt < MT; mt++) held[q][nt][mt] = acc[nt][mt];
+                }
         }
+    }
+    if constexpr (DEF > 0) {
+#pragma unroll
+        for (int h = 0; h < (MT + 1) / 2; h++)
+#pragma unroll
+            for (int q = 0; q < DEF; q++)
+                if (q < my_tiles) store_half(held[q], q, h);
     }
 }
 
@@ -3537,7 +3575,10 @@ static int launch_wide_t(float *c, const float *a, const uint16_t *b, int M, int
     const size_t lds = (size_t)16 * MT * NCH * WIDE_KC * 2 + (size_t)nw * WIDE_B_U4 * 16;
     static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
     if (!attr_set) {
-        HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH>, hipFuncAttributeMaxDynamicSharedMemorySize,
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH, 0>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)lds),
+               QH_ELAUNCH);
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH, 5>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)lds),
                QH_ELAUNCH);
         attr_set = true;
@@ -3545,8 +3586,12 @@ static int launch_wide_t(float *c, const float *a, const uint16_t *b, int M, int
     const int ntiles = (N + 31) / 32;
     int blocks = (ntiles + nw - 1) / nw;
     if (blocks > g_cus) blocks = g_cus;
-    hipLaunchKernelGGL((k_gemm_wide<MT, NCH>), dim3((unsigned)blocks), dim3(NTHREADS), lds, g_stream, c, a, b, M, N,
-                       ntiles);
+    if ((ntiles + (long)blocks * nw - 1) / ((long)blocks * nw) <= 5)
+        hipLaunchKernelGGL((k_gemm_wide<MT, NCH, 5>), dim3((unsigned)blocks), dim3(NTHREADS), lds, g_stream, c, a, b,
+                           M, N, ntiles);
+    else
+        hipLaunchKernelGGL((k_gemm_wide<MT, NCH, 0>), dim3((unsigned)blocks), dim3(NTHREADS), lds, g_stream, c, a, b,
+                           M, N, ntiles);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }

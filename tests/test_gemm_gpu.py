@@ -268,7 +268,8 @@ def test_narrow_kernel(gated):
 
 
 @pytest.mark.parametrize("M,K,N", [(64, 1024, 151936), (48, 1024, 40000), (33, 1024, 1000), (16, 1024, 76),
-                                   (5, 512, 4100), (64, 512, 32), (1, 1024, 9000), (64, 1024, 36)])
+                                   (5, 512, 4100), (64, 512, 32), (1, 1024, 9000), (64, 1024, 36),
+                                   (8, 512, 200000)])      # more than five tiles per wave: the strided order
 def test_wide_kernel(M, K, N):
     """The wide kernel (A resident in LDS, each wave streaming its own
     32-column tiles through LDS): the tied lm_head of a 64-sequence batch,
