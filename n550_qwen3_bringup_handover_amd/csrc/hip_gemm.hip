@@ -3199,12 +3199,12 @@ template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK = 32, i
 static int launch_pipe(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                        int M, int K, int N) {
     using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK, KG>;
-    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
-    if (!attr_set) {
+    static int attr_dev = -1;              // dynamic LDS above 64 KB must be opted into, per device
+    if (attr_dev != g_device) {
         HCHECK(hipFuncSetAttribute((const void *)k_gemm_pipe<BM, BN, WM, WN, STAGES, GATED, BK, KG>,
                                    hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS),
                QH_ELAUNCH);
-        attr_set = true;
+        attr_dev = g_device;
     }
     TileMap map;
     const long tiles = make_map(map, M, N, K, BM, BN, R::BNO);
@@ -3573,15 +3573,15 @@ template <int MT, int NCH>
 static int launch_wide_t(float *c, const float *a, const uint16_t *b, int M, int N) {
     const int nw = NTHREADS / WAVE;
     const size_t lds = (size_t)16 * MT * NCH * WIDE_KC * 2 + (size_t)nw * WIDE_B_U4 * 16;
-    static bool attr_set = false;          // dynamic LDS above 64 KB must be opted into
-    if (!attr_set) {
+    static int attr_dev = -1;              // dynamic LDS above 64 KB must be opted into, per device
+    if (attr_dev != g_device) {
         HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH, 0>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)lds),
                QH_ELAUNCH);
         HCHECK(hipFuncSetAttribute((const void *)k_gemm_wide<MT, NCH, 5>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)lds),
                QH_ELAUNCH);
-        attr_set = true;
+        attr_dev = g_device;
     }
     const int ntiles = (N + 31) / 32;
     int blocks = (ntiles + nw - 1) / nw;
@@ -3607,12 +3607,12 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
 template <int NWV, int KT, int CT>
 static int launch_m16_t(float *c, const float *a, const uint16_t *b, int M, int N) {
     const size_t lds = (size_t)CT * 16 * KT * 2 + (size_t)NWV * CT * 16 * 17 * 4;   // weights, then the wave tiles
-    static bool attr = false;              // dynamic LDS above 64 KB must be opted into
-    if (!attr) {
+    static int attr_dev = -1;              // dynamic LDS above 64 KB must be opted into, per device
+    if (attr_dev != g_device) {
         HCHECK(hipFuncSetAttribute((const void *)k_gemm_m16<NWV, KT, CT>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)lds),
                QH_ELAUNCH);
-        attr = true;
+        attr_dev = g_device;
     }
     hipLaunchKernelGGL((k_gemm_m16<NWV, KT, CT>), dim3((unsigned)((N + 16 * CT - 1) / (16 * CT))), dim3(NWV * WAVE),
                        lds, g_stream, c, a, b, M, N);

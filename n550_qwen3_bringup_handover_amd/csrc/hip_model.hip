@@ -723,13 +723,15 @@ extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const 
     if (!qkv || !out || !kc || !vc || !qn || !kn || !rcos || !rsin || !pos_d) return QH_EINVAL;
     if (nt <= 0 || max_seq <= 0 || nt > QM_MAX_CHUNK || max_seq > QM_MAX_SEQ) return QH_EINVAL;
     if (ctx_bound < nt || ctx_bound > max_seq) return QH_EINVAL;
-    static bool attr_set = false;
-    if (!attr_set) {
+    static int attr_dev = -1;                  // the attribute is held per device
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return QH_ELAUNCH;
+    if (attr_dev != dev) {
         // one token per block at the longest context needs more than the default 64 KB
         if (hipFuncSetAttribute((const void *)k_attention<1>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)qm_attention_lds_bytes(1, QM_MAX_SEQ)) != hipSuccess)
             return QH_ELAUNCH;
-        attr_set = true;
+        attr_dev = dev;
     }
     // 1 / sqrt(head_dim), the constant of qwen3.c:311
     const float scale = 0.08838834764831845f;
