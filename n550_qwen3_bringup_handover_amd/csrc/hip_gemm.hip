@@ -896,8 +896,8 @@ struct RingCfg {
     static constexpr int BNO = GATED ? BN / 2 : BN;
     static constexpr int LDS = STAGES * STAGE;
     static constexpr int vm(int k) { return k * LPS > 63 ? 63 : k * LPS; }
-    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-    static_assert((KG == 1 || KG == 2) && KSG * KG == KS, "wave groups split a stage's k-steps");
+    static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
+    static_assert((KG == 1 || KG == 2 || KG == 4) && KSG * KG == KS, "wave groups split a stage's k-steps");
     static_assert(A_DMA * NW * 1024 == A_BYTES && B_DMA * NW * 1024 == B_BYTES, "every wave issues the same number of copies");
     static_assert(A_DMA >= 1 && B_DMA >= 1, "copies per wave");
     static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
@@ -919,14 +919,16 @@ template <int V> struct IC { static constexpr int value = V; };
 // The copy into slot (it-1) % STAGES is safe after the barrier: every wave
 // consumed stage it-1 (its MFMAs ran) before reaching it.  LDS destinations
 // of the copies are wave-uniform and computed from a scalar wave index.
-// KG groups of WM x WN waves: with KG = 2 (the 32 x 64 tiles with 128-deep
-// stages, one block per CU) the groups split each stage's k-steps and the
-// second adds its sums into the first's through LDS at the end, so that two
-// waves share each SIMD (measured on MI355X, graph-replayed, against one
-// group of 2 x 2: 512 x {1024, 2048, 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.4 /
-// 9.65 / 12.8 us, 128 x 1024 x 4096 6.7 -> 6.2, gate|up + SiLU 64 x 1024 x
-// 3072 6.74 -> 6.27; 2 x 4 waves on the plain tiles instead reached 6.75 /
-// 10.6 / 14.5).
+// KG groups of WM x WN waves: with KG = 2 or 4 (the 32 x 64 tiles with
+// 128-deep stages, one block per CU) the groups split each stage's k-steps
+// and the others add their sums into the first group's through LDS at the
+// end, in group order, so that two or four waves share each SIMD (measured
+// on MI355X, graph-replayed, against one group of 2 x 2: 512 x {1024, 2048,
+// 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.4 / 9.65 / 12.8 us with two groups,
+// 128 x 1024 x 4096 6.7 -> 6.2, gate|up + SiLU 64 x 1024 x 3072 6.74 ->
+// 6.27; four groups from K = 2048: 512 x {2048, 3072} x 1024 9.5 / 12.7 ->
+// 9.1 / 12.2, but at K = 1024 they lose, 6.24 -> 6.35; 2 x 4 waves on the
+// plain tiles instead reached 6.75 / 10.6 / 14.5).
 template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_, int KG>
 __global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__restrict__ c,
                                                           const float *__restrict__ a,
@@ -1107,21 +1109,26 @@ __global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__res
     }
 
     // two wave groups: the second adds its sums into the first's through LDS
-    if constexpr (KG == 2) {
+    if constexpr (KG > 1) {
+        constexpr int PER_G = WM * WN * R::TM * R::TN * 64;   // f32x4 per group
         f32x4 *xred = reinterpret_cast<f32x4 *>(smem);
         __syncthreads();                                   // every wave is done with the ring
-        if (kg == 1) {
+        if (kg > 0) {
 #pragma unroll
             for (int i = 0; i < R::TM; i++)
 #pragma unroll
-                for (int j = 0; j < R::TN; j++) xred[((wq * R::TM + i) * R::TN + j) * 64 + lane] = acc[i][j];
+                for (int j = 0; j < R::TN; j++)
+                    xred[(kg - 1) * PER_G + ((wq * R::TM + i) * R::TN + j) * 64 + lane] = acc[i][j];
         }
         __syncthreads();
-        if (kg == 1) return;
+        if (kg > 0) return;
 #pragma unroll
-        for (int i = 0; i < R::TM; i++)
+        for (int q = 1; q < KG; q++)                       // the groups' sums in group order
 #pragma unroll
-            for (int j = 0; j < R::TN; j++) acc[i][j] += xred[((wq * R::TM + i) * R::TN + j) * 64 + lane];
+            for (int i = 0; i < R::TM; i++)
+#pragma unroll
+                for (int j = 0; j < R::TN; j++)
+                    acc[i][j] += xred[(q - 1) * PER_G + ((wq * R::TM + i) * R::TN + j) * 64 + lane];
     }
 
     // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
@@ -3719,7 +3726,9 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_T32x128:  return launch_tile<32, 128, 64, 2, 2, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_T16x64:   return launch_tile<16, 128, 64, 1, 4, GATED, true>(c, a, b, b2, M, K, N);
         case PLAN_SCALAR64: return launch_tile<64, 64, 64, 2, 2, GATED, false>(c, a, b, b2, M, K, N);
-        case PLAN_P32x64k128s4: return launch_pipe<32, 64, 2, 2, 4, GATED, 128, 2>(c, a, b, b2, M, K, N);
+        case PLAN_P32x64k128s4:   // four k groups (16 waves) from K = 2048, two below (see k_gemm_pipe)
+            return K >= 2048 ? launch_pipe<32, 64, 2, 2, 4, GATED, 128, 4>(c, a, b, b2, M, K, N)
+                             : launch_pipe<32, 64, 2, 2, 4, GATED, 128, 2>(c, a, b, b2, M, K, N);
         case PLAN_P32x64k64s4:  return launch_pipe<32, 64, 2, 2, 4, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_P64x64k64s3:  return launch_pipe<64, 64, 2, 2, 3, GATED, 64>(c, a, b, b2, M, K, N);
         case PLAN_XB256x256k32: case PLAN_XB128x128: case PLAN_XB256x256s1: {
