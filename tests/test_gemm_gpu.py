@@ -368,6 +368,38 @@ def test_every_kernel_variant_gated(plan, M, K, N):
     numerics.compare_gated(h, x, wg, wu, M, K, N, rows=numerics.pick_rows(M, 24))
 
 
+PIPE_PLANS = [p for p in ALL_PLANS if p.startswith("pipe")]
+
+
+@pytest.mark.parametrize("plan", PIPE_PLANS)
+@pytest.mark.parametrize("gated", [False, True])
+@pytest.mark.parametrize("stages", [3, 5, 6, 7, 9, 17, 19])
+def test_ring_stage_counts(plan, gated, stages):
+    """The ring kernels run straight-line steps while a copy is due and the
+    conditional steps for the last stages: every stage count around that
+    boundary (K = stages x the plan's k per stage; 17 and 19 stages of 128
+    take the four-group form), gated and not, against the oracle."""
+    bk = 128 if plan == "pipe32x64k128s4" else 64
+    M, K, N = 70, bk * stages, 200
+    x = oracle.f32_bf16_normal(M * K, 4700 + stages)
+    w = oracle.bf16_normal(2 * N * K, 4701 + stages, 0.02)
+    out = np.full(M * N, np.nan, np.float32)
+    print(f"{plan} gated={gated} {M}x{K}x{N}", flush=True)
+    abi.force_plan(abi.PLANS[plan])
+    try:
+        if gated:
+            abi.gemm_gate_up_silu(out, x, w[:N * K], w[N * K:], M, K, N)
+        else:
+            abi.gemm(out, x, w[:N * K], M, K, N)
+        assert abi.last_plan() == plan
+    finally:
+        abi.force_plan(0)
+    if gated:
+        numerics.compare_gated(out, x, w[:N * K], w[N * K:], M, K, N, rows=numerics.pick_rows(M, 12))
+    else:
+        numerics.compare(out, x, w[:N * K], M, K, N, rows=numerics.pick_rows(M, 12))
+
+
 def _random_cases(n, seed):
     """seeded random (plan, M, K, N, gated) cases over the plan table, sized so
     the oracle checks each in well under a second"""
