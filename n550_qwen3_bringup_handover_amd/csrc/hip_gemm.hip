@@ -2466,32 +2466,51 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
 // ---------------------------------------------------------------------------
 // 16-row GEMM for M <= 16 (small decode batches)
 // ---------------------------------------------------------------------------
-// blockIdx.x owns 16 columns of C (16 rows of B); the block's NWV waves split
-// K = KT (wave w: k range [w KW, (w + 1) KW)), each computing a 16 x 16 tile
-// with v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand =
+// blockIdx.x owns 16 CT columns of C (16 CT rows of B); the block's NWV waves
+// split K = KT (wave w: k range [w KW, (w + 1) KW)), each computing 16 x 16
+// tiles with v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand =
 // weights), and the NWV tiles are added through LDS in wave order.  Each lane
-// issues all of its loads at once: its share of the wave's weights, 16 rows x
-// KW, each load instruction covering 8 rows x 128 contiguous bytes (the
-// fragment order itself, 16 rows x 64 bytes per instruction, streams from HBM
-// more slowly), then its A fragments (fp32, from L2, rows past M reading
-// zeros), rounded to bf16 (RNE) on arrival.  The weights pass through the
-// wave's own LDS rows (16-byte chunks XOR-swizzled by row) and are read back
-// as fragments by the same wave, so a wave-scope fence, not a block barrier,
-// orders those writes and reads.  Lane (r, g) = (lane % 16, lane / 16)
-// holds k = 32s + 8g .. 32s + 8g + 7 of step s for row r of both operands.
-// Rows of B past N read zeros and their columns of C are not stored.
+// issues all of its loads at once: its share of the wave's weights, then its
+// share of the wave's 16 x KW slice of A (fp32; rows past M read zeros) --
+// both in row order, every load instruction covering whole 128-byte lines (8
+// rows x 128 bytes of weights, 2 rows x 512 bytes of A at KW = 128).  Loading
+// A in the MFMA fragment order instead (16 rows x two 16-byte pieces 32 bytes
+// apart per instruction) made A the larger part of the kernel (measured on
+// MI355X, graph-replayed per call: 16 x 1024 x 3072 3.87 -> 3.01 us, 16 x
+// 2048 x 2048 5.74 -> 3.68, 8 x 1024 x 3072 3.24 -> 2.82).  Both pass through
+// the wave's own LDS rows (16-byte chunks XOR-swizzled by row; A rounded to
+// bf16 (RNE) on the way in) and come back as fragments; only the wave itself
+// reads its rows, so a wave-scope fence, not a block barrier, orders the
+// writes and reads.  Where the block's LDS does not hold weights and A side
+// by side (m16_asep false), the wave reads its weight fragments into
+// registers first and A then reuses the same rows.  Lane (r, g) =
+// (lane % 16, lane / 16) holds k = 32s + 8g .. 32s + 8g + 7 of step s for
+// row r of both operands.  Rows of B past N read zeros and their columns of C
+// are not stored.
+constexpr bool m16_asep(int nwv, int kt, int ct) {
+    return ct * 16 * kt * 2 + 16 * kt * 2 + nwv * ct * 16 * 17 * 4 <= 160 * 1024;
+}
+constexpr size_t m16_lds_bytes(int nwv, int kt, int ct) {   // weights, A (if separate), wave tiles
+    return (size_t)ct * 16 * kt * 2 + (m16_asep(nwv, kt, ct) ? (size_t)16 * kt * 2 : 0) +
+           (size_t)nwv * ct * 16 * 17 * 4;
+}
 template <int NWV, int KT, int CT>
 __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, const float *__restrict__ a,
                                                         const uint16_t *__restrict__ b, int M, int N) {
     constexpr int KW = KT / NWV, CHW = KW / 8, STEPS = KW / 32, NBL = 16 * CHW / WAVE;
+    constexpr int PPR = KW / 4, APL = 16 * PPR / WAVE;   // 16-byte fp32 pieces of A per row / per lane
     constexpr int SW = CHW >= 16 ? 15 : CHW - 1;           // swizzle mask: within the row's chunks
-    static_assert(KW * NWV == KT && CHW % 8 == 0 && NBL * WAVE == 16 * CHW && NWV * WAVE >= 256 * CT, "k split");
-    extern __shared__ __align__(16) u32x4 m16_lds[];       // [NWV][CT][16][CHW] weights, then [NWV][CT][16][17] fp32
+    constexpr bool ASEP = m16_asep(NWV, KT, CT);
+    static_assert(KW * NWV == KT && CHW % 8 == 0 && NBL * WAVE == 16 * CHW && APL * WAVE == 16 * PPR &&
+                  NWV * WAVE >= 256 * CT, "k split");
+    // LDS: [NWV][CT][16][CHW] weights, [NWV][16][CHW] A if separate, [NWV][CT][16][17] fp32 tiles
+    extern __shared__ __align__(16) u32x4 m16_lds[];
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int r16 = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.x * 16 * CT;
     u32x4 *const sb = m16_lds + w * CT * 16 * CHW;
-    float *const red = reinterpret_cast<float *>(m16_lds + NWV * CT * 16 * CHW);
+    u32x4 *const sa = ASEP ? m16_lds + NWV * CT * 16 * CHW + w * 16 * CHW : sb;
+    float *const red = reinterpret_cast<float *>(m16_lds + NWV * CT * 16 * CHW + (ASEP ? NWV * 16 * CHW : 0));
 
     // weights: load i of tile t covers rows 16 t + 8 (i % 2) + lane / 8, chunks 8 (i / 2) + lane % 8
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * KT * 2);
@@ -2505,26 +2524,32 @@ __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, 
             const uint32_t off = n < N ? ((uint32_t)n * KT + w * KW + 8 * ch) * 2u : BUF_OOB;
             bw[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
         }
-    // A fragments of this wave's k range
+    // A: piece q = j WAVE + lane is row q / PPR, floats 4 (q % PPR) .. + 3 of the wave's k range
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * KT * 4);
-    const uint32_t aoff = r16 < M ? ((uint32_t)r16 * KT + w * KW + 8 * g) * 4u : BUF_OOB;
-    u32x4 alo[STEPS], ahi[STEPS];
+    u32x4 ap[APL];
 #pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-        alo[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 128 * s, 0, 0);
-        ahi[s] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoff + 128 * s + 16, 0, 0);
+    for (int j = 0; j < APL; j++) {
+        const int q = j * WAVE + lane, row = q / PPR, pc = q % PPR;
+        const uint32_t off = row < M ? ((uint32_t)row * KT + w * KW + 4 * pc) * 4u : BUF_OOB;
+        ap[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
-    bf16x8 af[STEPS];
+    auto wave_sync = [] {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto store_a = [&] {        // rounded to bf16, 8 bytes = half a 16-byte chunk per piece
 #pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-        u32x4 p;
-        p.x = pack_bf16x2(__uint_as_float(alo[s].x), __uint_as_float(alo[s].y));
-        p.y = pack_bf16x2(__uint_as_float(alo[s].z), __uint_as_float(alo[s].w));
-        p.z = pack_bf16x2(__uint_as_float(ahi[s].x), __uint_as_float(ahi[s].y));
-        p.w = pack_bf16x2(__uint_as_float(ahi[s].z), __uint_as_float(ahi[s].w));
-        af[s] = __builtin_bit_cast(bf16x8, p);
-    }
+        for (int j = 0; j < APL; j++) {
+            const int q = j * WAVE + lane, row = q / PPR, pc = q % PPR;
+            uint2 v;
+            v.x = pack_bf16x2(__uint_as_float(ap[j].x), __uint_as_float(ap[j].y));
+            v.y = pack_bf16x2(__uint_as_float(ap[j].z), __uint_as_float(ap[j].w));
+            *reinterpret_cast<uint2 *>(reinterpret_cast<unsigned char *>(sa + row * CHW + ((pc >> 1) ^ (row & SW))) +
+                                       8 * (pc & 1)) = v;
+        }
+    };
 #pragma unroll
     for (int t = 0; t < CT; t++)
 #pragma unroll
@@ -2532,9 +2557,19 @@ __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, 
             const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
             sb[(16 * t + row) * CHW + (ch ^ (row & SW))] = bw[t][i];
         }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (ASEP) store_a();
+    wave_sync();
+    bf16x8 bf[ASEP ? 1 : STEPS][CT];
+    if constexpr (!ASEP) {      // weight fragments to registers, then A into the same rows
+#pragma unroll
+        for (int s = 0; s < STEPS; s++)
+#pragma unroll
+            for (int t = 0; t < CT; t++)
+                bf[s][t] = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + ((4 * s + g) ^ (r16 & SW))]);
+        wave_sync();
+        store_a();
+        wave_sync();
+    }
 
     f32x4 acc[CT];
 #pragma unroll
@@ -2542,10 +2577,13 @@ __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, 
 #pragma unroll
     for (int s = 0; s < STEPS; s++) {
         const int ch = 4 * s + g;
+        const bf16x8 af = __builtin_bit_cast(bf16x8, sa[r16 * CHW + (ch ^ (r16 & SW))]);
 #pragma unroll
         for (int t = 0; t < CT; t++) {
-            const bf16x8 bf = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + (ch ^ (r16 & SW))]);
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s], bf, acc[t], 0, 0, 0);
+            bf16x8 wf;
+            if constexpr (ASEP) wf = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + (ch ^ (r16 & SW))]);
+            else wf = bf[s][t];
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf, acc[t], 0, 0, 0);
         }
     }
     // lane (r, g) holds rows 4g .. 4g + 3 of C, column 16 t + r of the block's
@@ -2914,15 +2952,20 @@ static int choose_bf16a_plan(int M, int K, int N, int gated) {
 static int choose_plan(int M, int K, int N, int gated, bool vec) {
     if (!vec) return PLAN_SCALAR64;
     // 2 <= M <= 16 (config 1's gate_proj, small decode batches): the 16-row
-    // kernel, 16 or 32 columns per block and K split over its waves, where
-    // measured faster (MI355X, graph-replayed per call: 16 x 1024 x 3072 /
-    // 4096 / 8192 3.7 / 3.8 / 4.5 us against 4.8 / 5.0 / 5.9 on the GEMV-shaped
-    // and weight-streaming kernels; 4 x 1024 x 3072 2.7 against 3.5 on the
-    // GEMV; 8 x 2048 x 1024 4.2 against 5.3 on the skinny kernel; at K = 3072
-    // and M > 8 its blocks' re-reads of A make it slower than the skinny one)
+    // kernel, 16 or 32 columns per block and K split over its waves, where a
+    // sweep of M 2..16 x K 1024..3072 x N 1024..16384 measured it fastest
+    // (MI355X, graph-replayed per call: 16 x 1024 x 3072 3.3 us against 5.3 on
+    // the GEMV-shaped kernel; 16 x 3072 x {1024, 3072} 5.5 / 5.9 against 6.3
+    // on the narrow and 15.7 on the weight-streaming kernel; 4 x 2048 x 3072
+    // 4.2 against 6.2 on the GEMV).  Not at N > 8192 with K >= 2048, where
+    // every block re-reads all of A (the GEMV at M <= 4, the weight-streaming
+    // kernel above: 16 x 2048 x 16384 17.6 against 18.4 us), nor at M = 2
+    // with K = 2048, N <= 2048 or K = 3072, N > 4096, or at N > 8192, where
+    // the GEMV is as fast or faster.
     if (!gated && M >= 2 && m16_fits(M, K, N) &&
-        ((K == 1024 && N <= 16384) ||
-         (K == 2048 && M > 4 && N <= 2048) || (K == 3072 && M > 4 && M <= 8 && N <= 1024)))
+        (M >= 4 ? (N <= 8192 || (K == 1024 && N <= 16384))
+                : ((K == 1024 && N <= 8192) || (K == 2048 && N > 2048 && N <= 8192) ||
+                   (K == 3072 && N <= 4096))))
         return PLAN_M16;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
     // 16 < M <= 64, not gated (every projection of a decode batch but
@@ -3634,7 +3677,7 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
 
 template <int NWV, int KT, int CT>
 static int launch_m16_t(float *c, const float *a, const uint16_t *b, int M, int N) {
-    const size_t lds = (size_t)CT * 16 * KT * 2 + (size_t)NWV * CT * 16 * 17 * 4;   // weights, then the wave tiles
+    const size_t lds = m16_lds_bytes(NWV, KT, CT);
     static int attr_dev = -1;              // dynamic LDS above 64 KB must be opted into, per device
     if (attr_dev != g_device) {
         HCHECK(hipFuncSetAttribute((const void *)k_gemm_m16<NWV, KT, CT>, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -43,7 +43,7 @@ def run(L, fn, a, b, M, K, N):
 # (first call, second smaller call): plan family each pair reaches
 PAIRS = [
     ((64, 3072, 1024), (48, 2048, 1024)),      # narrow: slice sums and tickets in scratch
-    ((16, 3072, 1024), (12, 3072, 1024)),      # skinny, K split: slice sums in scratch
+    ((16, 4096, 1024), (12, 3136, 1024)),      # skinny, K split: slice sums in scratch
     ((8, 4096, 4096), (5, 4096, 3072)),        # stream, K split: slice sums in scratch
     ((8192, 1024, 4096), (8192, 512, 4096)),   # xb256x256s1: bf16 copy of A in scratch
     ((1, 1024, 3072), (1, 1024, 1024)),        # gemv: no workspace
