@@ -2057,7 +2057,14 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // of 8 slices each XCD reads one slice of A).  Every thread issues all of its
 // loads at once: the block's slice of A first (from L2), then its wave's
 // weights (from HBM); the slice is rounded to bf16 (RNE) into LDS (16-byte
-// chunks XOR-swizzled by row) while the weights are in flight.  The four
+// chunks XOR-swizzled by row) while the weights are in flight.  Where the
+// block's LDS also holds them (even KPW), the weights are loaded in row order
+// -- every instruction 8 rows x 128 contiguous bytes -- and pass through the
+// wave's own LDS rows, instead of straight into registers in the MFMA
+// fragment order (16 rows x 64 bytes per instruction; measured on MI355X,
+// graph-replayed, M = 64: q 4.9 -> 4.25 us, q|k|v 5.74 -> 5.6, k/v 5.88 ->
+// 5.62, o 6.66 -> 6.49, down 7.39 -> 7.25; M = 128 k/v 4.4 -> 4.05, q 5.5 ->
+// 5.05).  The four
 // waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
 // their partial tiles are added through LDS (reusing the A slice's space) in
 // wave order.  With one slice the block writes C (silu(gate) * up when
@@ -2083,6 +2090,12 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * NARROW_RSTRIDE / 4;
     static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
     __shared__ __align__(16) u32x4 smem[SA_U4 > RED_U4 ? SA_U4 : RED_U4];
+    // weights in row order through per-wave LDS rows where they fit
+    constexpr int BR = NJ * NT * 16, CW = 4 * KPW;        // a wave's weight rows, 16-byte chunks per row
+    constexpr bool BROW = KPW % 2 == 0 &&
+        ((SA_U4 > RED_U4 ? SA_U4 : RED_U4) + NW * BR * CW) * 16 + 64 <= 160 * 1024;
+    constexpr int BSW = CW % 16 == 0 ? 15 : 7;            // row swizzle within a row's chunks
+    __shared__ __align__(16) u32x4 sbw[BROW ? NW * BR * CW : 1];
     u32x4 *const sa = smem;                               // the A slice, then
     float *const red = reinterpret_cast<float *>(smem);   // [wave][j][row][RSTRIDE] wave partials
     __shared__ unsigned last_s;
@@ -2111,18 +2124,40 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
     const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
     u32x4 bq[NJ][NT][KPW];
+    if constexpr (BROW) {
+        // load i: rows 8 (i % (BR / 8)) + lane / 8 of the wave's BR rows (Wg rows,
+        // then Wu rows), chunks 8 (i / (BR / 8)) + lane % 8: 8 rows x 128 bytes
+        u32x4 *const flat = &bq[0][0][0];
 #pragma unroll
-    for (int nt = 0; nt < NT; nt++) {
-        const int n = n0 + 16 * nt + r16;
-        const uint32_t base = (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * g) * 2);
+        for (int i = 0; i < NJ * NT * KPW; i++) {
+            const int row = 8 * (i % (BR / 8)) + (lane >> 3), ch = 8 * (i / (BR / 8)) + (lane & 7);
+            const int j = row / (NT * 16), n = n0 + row % (NT * 16);
+            const uint32_t off = n < N ? (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * ch) * 2) : BUF_OOB;
+            flat[i] = __builtin_amdgcn_raw_buffer_load_b128(j ? rb2 : rb, off, 0, 2);
+        }
+    } else {                                              // fragment order: rows n0 + 16 nt + r16
 #pragma unroll
-        for (int s = 0; s < KPW; s++) {
-            const uint32_t off = n < N ? base + 64u * s : BUF_OOB;
-            bq[0][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
-            if constexpr (GATED) bq[NJ - 1][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
+        for (int nt = 0; nt < NT; nt++) {
+            const int n = n0 + 16 * nt + r16;
+            const uint32_t base = (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * g) * 2);
+#pragma unroll
+            for (int s = 0; s < KPW; s++) {
+                const uint32_t off = n < N ? base + 64u * s : BUF_OOB;
+                bq[0][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
+                if constexpr (GATED) bq[NJ - 1][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
+            }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    u32x4 *const sbwave = sbw + (BROW ? w * BR * CW : 0);
+    if constexpr (BROW) {
+        const u32x4 *const flat = &bq[0][0][0];
+#pragma unroll
+        for (int i = 0; i < NJ * NT * KPW; i++) {
+            const int row = 8 * (i % (BR / 8)) + (lane >> 3), ch = 8 * (i / (BR / 8)) + (lane & 7);
+            sbwave[row * CW + (ch ^ (row & BSW))] = flat[i];
+        }
+    }
 
     // 2. A rounded to bf16 (RNE) into LDS
 #pragma unroll
@@ -2160,8 +2195,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
             for (int nt = 0; nt < NT; nt++)
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
+                {
+                    u32x4 wf;
+                    if constexpr (BROW) {
+                        const int row = (j * NT + nt) * 16 + r16, ch = 4 * s + g;
+                        wf = sbwave[row * CW + (ch ^ (row & BSW))];
+                    } else {
+                        wf = bq[j][nt][s];
+                    }
                     acc[j][nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        af[mt], __builtin_bit_cast(bf16x8, bq[j][nt][s]), acc[j][nt][mt], 0, 0, 0);
+                        af[mt], __builtin_bit_cast(bf16x8, wf), acc[j][nt][mt], 0, 0, 0);
+                }
     }
     __syncthreads();                                      // every wave is done reading the A slice
 
