@@ -1880,9 +1880,14 @@ __global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__rest
 // most 256) and blockIdx.z a slab of 64 rows of A and C.  The block stages its slice of A once in LDS as bf16 (RNE), rows
 // of 16-byte chunks XOR-swizzled by row, so that the four waves read their
 // v_mfma_f32_16x16x32_bf16 A fragments from one copy instead of each block
-// re-reading A per 16-row tile; each wave issues all of its B loads (one 16-B
-// chunk per lane per 32-deep step) before the staging wait, so the weight
-// stream is in flight while A is converted.  No cross-wave reduction: a wave
+// re-reading A per 16-row tile; each wave issues all of its B loads before
+// the staging wait, so the weight stream is in flight while A is converted.
+// The weights are loaded in row order (8 rows x 128 contiguous bytes per
+// instruction) and pass through the wave's own LDS rows; straight into
+// registers in the MFMA fragment order (16 rows x 64 bytes per instruction)
+// they took longer (measured on MI355X, graph-replayed: 16 x {3072, 4096} x
+// 1024 6.53 / 6.81 -> 6.14 / 6.41 us, 64 x 3072 x 1024 10.3 -> 9.2, 48 x
+// 2048 x 1024 9.06 -> 8.26; 8 x 2048 x 1024 5.73 -> 5.84).  No cross-wave reduction: a wave
 // owns its 16 output columns.  With more than one slice the fp32 sums go to
 // part[slice][j][M][N] (j = gate/up when GATED) and k_stream_reduce adds the
 // slices in order; otherwise C (or silu(gate)*up) is written directly.
@@ -1896,6 +1901,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
     constexpr int NJ = GATED ? 2 : 1;
     constexpr int KSMAX = 256 / 32;                      // 32-deep steps per slice, at most
     __shared__ __align__(16) u32x4 sa[MT * 16 * (256 / 8)];   // [row][chunk ^ swz(row)], bf16
+    __shared__ __align__(16) u32x4 sbw[NTHREADS / WAVE][NJ * 16 * 32];   // each wave's weight rows
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.y * ksl;
@@ -1926,11 +1932,14 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
     const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
     const int n = blockIdx.x * 64 + w * 16 + r16;
-    const uint32_t boff = n < N ? (uint32_t)(((size_t)n * K + k0 + 8 * g) * 2) : BUF_OOB;
+    // in row order: load s covers rows 8 (s % 2) + lane / 8 of the wave's 16,
+    // chunks 8 (s / 2) + lane % 8 of the slice (8 rows x 128 bytes)
     u32x4 bq[NJ][KSMAX];
 #pragma unroll
     for (int s = 0; s < KSMAX; s++) {
-        const uint32_t off = (s < nst && n < N) ? boff + 64u * s : BUF_OOB;
+        const int row = 8 * (s & 1) + (lane >> 3), ch = 8 * (s >> 1) + (lane & 7);
+        const int nr = blockIdx.x * 64 + w * 16 + row;
+        const uint32_t off = (ch < ncs && nr < N) ? (uint32_t)(((size_t)nr * K + k0 + 8 * ch) * 2) : BUF_OOB;
         bq[0][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
         if constexpr (GATED) bq[1][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
     }
@@ -1948,6 +1957,13 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
         v.w = pack_bf16x2(__uint_as_float(ahi[i].z), __uint_as_float(ahi[i].w));
         if (q < total) sa[m * ncs + (ch ^ (m & 7))] = v;
     }
+#pragma unroll
+    for (int j = 0; j < NJ; j++)
+#pragma unroll
+        for (int s = 0; s < KSMAX; s++) {
+            const int row = 8 * (s & 1) + (lane >> 3), ch = 8 * (s >> 1) + (lane & 7);
+            sbw[w][(j * 16 + row) * 32 + (ch ^ (row & 15))] = bq[j][s];
+        }
     __syncthreads();
 
     // 3. MFMA over the slice: A fragment rows 16 mt + r16, chunk 4 s + g
@@ -1967,7 +1983,7 @@ __global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c,
             }
 #pragma unroll
             for (int j = 0; j < NJ; j++) {
-                const bf16x8 bf = __builtin_bit_cast(bf16x8, bq[j][s]);
+                const bf16x8 bf = __builtin_bit_cast(bf16x8, sbw[w][(j * 16 + r16) * 32 + ((4 * s + g) ^ (r16 & 15))]);
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++)
                     acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[j][mt], 0, 0, 0);
