@@ -2546,7 +2546,8 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
 // registers first and A then reuses the same rows.  Lane (r, g) =
 // (lane % 16, lane / 16) holds k = 32s + 8g .. 32s + 8g + 7 of step s for
 // row r of both operands.  Rows of B past N read zeros and their columns of C
-// are not stored.
+// are not stored.  GATED: the block's two tiles are the Wg and the Wu rows of
+// the same 16 columns (CT = 2), and C = silu(x Wg^T) * (x Wu^T).
 constexpr bool m16_asep(int nwv, int kt, int ct) {
     return ct * 16 * kt * 2 + 16 * kt * 2 + nwv * ct * 16 * 17 * 4 <= 160 * 1024;
 }
@@ -2554,35 +2555,39 @@ constexpr size_t m16_lds_bytes(int nwv, int kt, int ct) {   // weights, A (if se
     return (size_t)ct * 16 * kt * 2 + (m16_asep(nwv, kt, ct) ? (size_t)16 * kt * 2 : 0) +
            (size_t)nwv * ct * 16 * 17 * 4;
 }
-template <int NWV, int KT, int CT>
+template <int NWV, int KT, int CT, bool GATED = false>
 __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, const float *__restrict__ a,
-                                                        const uint16_t *__restrict__ b, int M, int N) {
+                                                        const uint16_t *__restrict__ b,
+                                                        const uint16_t *__restrict__ b2, int M, int N) {
     constexpr int KW = KT / NWV, CHW = KW / 8, STEPS = KW / 32, NBL = 16 * CHW / WAVE;
     constexpr int PPR = KW / 4, APL = 16 * PPR / WAVE;   // 16-byte fp32 pieces of A per row / per lane
     constexpr int SW = CHW >= 16 ? 15 : CHW - 1;           // swizzle mask: within the row's chunks
     constexpr bool ASEP = m16_asep(NWV, KT, CT);
     static_assert(KW * NWV == KT && CHW % 8 == 0 && NBL * WAVE == 16 * CHW && APL * WAVE == 16 * PPR &&
-                  NWV * WAVE >= 256 * CT, "k split");
+                  NWV * WAVE >= 256 * CT && (!GATED || CT == 2), "k split");
+    constexpr int COLS = GATED ? 16 : 16 * CT;             // columns of C per block
     // LDS: [NWV][CT][16][CHW] weights, [NWV][16][CHW] A if separate, [NWV][CT][16][17] fp32 tiles
     extern __shared__ __align__(16) u32x4 m16_lds[];
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16 * CT;
+    const int n0 = blockIdx.x * COLS;
     u32x4 *const sb = m16_lds + w * CT * 16 * CHW;
     u32x4 *const sa = ASEP ? m16_lds + NWV * CT * 16 * CHW + w * 16 * CHW : sb;
     float *const red = reinterpret_cast<float *>(m16_lds + NWV * CT * 16 * CHW + (ASEP ? NWV * 16 * CHW : 0));
 
-    // weights: load i of tile t covers rows 16 t + 8 (i % 2) + lane / 8, chunks 8 (i / 2) + lane % 8
+    // weights: load i of tile t covers rows 16 t + 8 (i % 2) + lane / 8 (GATED: rows
+    // 8 (i % 2) + lane / 8 of Wg for t = 0, of Wu for t = 1), chunks 8 (i / 2) + lane % 8
     const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * KT * 2);
+    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * KT * 2);
     u32x4 bw[CT][NBL];
 #pragma unroll
     for (int t = 0; t < CT; t++)
 #pragma unroll
         for (int i = 0; i < NBL; i++) {
             const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
-            const int n = n0 + 16 * t + row;
+            const int n = n0 + (GATED ? 0 : 16 * t) + row;
             const uint32_t off = n < N ? ((uint32_t)n * KT + w * KW + 8 * ch) * 2u : BUF_OOB;
-            bw[t][i] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0);
+            bw[t][i] = __builtin_amdgcn_raw_buffer_load_b128(GATED && t ? rb2 : rb, off, 0, 0);
         }
     // A: piece q = j WAVE + lane is row q / PPR, floats 4 (q % PPR) .. + 3 of the wave's k range
     const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * KT * 4);
@@ -2652,7 +2657,19 @@ __global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, 
 #pragma unroll
         for (int r = 0; r < 4; r++) red[((w * CT + t) * 16 + 4 * g + r) * 17 + r16] = acc[t][r];
     __syncthreads();
-    if (threadIdx.x < 256 * CT) {
+    if constexpr (GATED) {
+        if (threadIdx.x < 256) {
+            const int m = (threadIdx.x >> 4) & 15, col = threadIdx.x & 15;
+            float sg = red[m * 17 + col], su = red[(16 + m) * 17 + col];
+#pragma unroll
+            for (int v = 1; v < NWV; v++) {
+                sg += red[((v * 2) * 16 + m) * 17 + col];
+                su += red[((v * 2 + 1) * 16 + m) * 17 + col];
+            }
+            const int n = n0 + col;
+            if (m < M && n < N) c[(size_t)m * N + n] = silu_mul(sg, su);
+        }
+    } else if (threadIdx.x < 256 * CT) {
         const int t = threadIdx.x >> 8, m = (threadIdx.x >> 4) & 15, col = threadIdx.x & 15;
         float sum = red[(t * 16 + m) * 17 + col];
 #pragma unroll
@@ -3026,6 +3043,17 @@ static int choose_plan(int M, int K, int N, int gated, bool vec) {
         (M >= 4 ? (N <= 8192 || (K == 1024 && N <= 16384))
                 : ((K == 1024 && N <= 8192) || (K == 2048 && N > 2048 && N <= 8192) ||
                    (K == 3072 && N <= 4096))))
+        return PLAN_M16;
+    // gated (gate|up + SiLU of a small decode batch) above M = 4: the same
+    // kernel with the Wg and the Wu rows of 16 columns as a block's two tiles
+    // (K <= 2048), where measured faster (graph-replayed: 16 x 1024 x 3072 3.7
+    // us against 5.8 on the 32x64 ring tiles, 16 x 2048 x 3072 5.9 against
+    // 7.9; not at N = 8192 beyond M = 8 or K = 1024; batched decode of 16 / 8
+    // sequences 13.7k / 7.6k -> 14.5k / 8.1k tok/s).  At M <= 4 the GEMV stays:
+    // alone the 16-row kernel was faster there too (4 x 1024 x 3072 3.6 against
+    // 5.1 us), but decode of 4 sequences lost 1% with it.
+    if (gated && M > 4 && K <= 2048 && m16_fits(M, K, N) &&
+        (N <= 4096 || (K == 1024 && M <= 8 && N <= 8192)))
         return PLAN_M16;
     if (M <= 4 && (size_t)M * K * 4 <= 64 * 1024) return PLAN_GEMV;
     // 16 < M <= 64, not gated (every projection of a decode batch but
@@ -3735,31 +3763,41 @@ static int launch_wide(float *c, const float *a, const uint16_t *b, int M, int K
     return QH_EINVAL;
 }
 
-template <int NWV, int KT, int CT>
-static int launch_m16_t(float *c, const float *a, const uint16_t *b, int M, int N) {
+template <int NWV, int KT, int CT, bool GATED = false>
+static int launch_m16_t(float *c, const float *a, const uint16_t *b, const uint16_t *b2, int M, int N) {
     const size_t lds = m16_lds_bytes(NWV, KT, CT);
     static int attr_dev = -1;              // dynamic LDS above 64 KB must be opted into, per device
     if (attr_dev != g_device) {
-        HCHECK(hipFuncSetAttribute((const void *)k_gemm_m16<NWV, KT, CT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                   (int)lds),
+        HCHECK(hipFuncSetAttribute((const void *)k_gemm_m16<NWV, KT, CT, GATED>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
                QH_ELAUNCH);
         attr_dev = g_device;
     }
-    hipLaunchKernelGGL((k_gemm_m16<NWV, KT, CT>), dim3((unsigned)((N + 16 * CT - 1) / (16 * CT))), dim3(NWV * WAVE),
-                       lds, g_stream, c, a, b, M, N);
+    const int cols = GATED ? 16 : 16 * CT;
+    hipLaunchKernelGGL((k_gemm_m16<NWV, KT, CT, GATED>), dim3((unsigned)((N + cols - 1) / cols)), dim3(NWV * WAVE),
+                       lds, g_stream, c, a, b, b2, M, N);
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
-// sizes within m16_fits, 16-byte aligned a and b (checked by the caller)
-static int launch_m16(float *c, const float *a, const uint16_t *b, int M, int K, int N) {
-    const int ct = m16_ct(K, N);
-    switch (K * 10 + ct) {
-        case 10241: return launch_m16_t<8, 1024, 1>(c, a, b, M, N);
-        case 10242: return launch_m16_t<8, 1024, 2>(c, a, b, M, N);
-        case 20481: return launch_m16_t<8, 2048, 1>(c, a, b, M, N);
-        case 20482: return launch_m16_t<8, 2048, 2>(c, a, b, M, N);
-        case 30721: return launch_m16_t<8, 3072, 1>(c, a, b, M, N);
-        default: return QH_EINVAL;
+// sizes within m16_fits (gated: K <= 2048), 16-byte aligned a, b, b2 (checked by the caller)
+template <bool GATED>
+static int launch_m16(float *c, const float *a, const uint16_t *b, const uint16_t *b2, int M, int K, int N) {
+    if constexpr (GATED) {
+        switch (K) {
+            case 1024: return launch_m16_t<8, 1024, 2, true>(c, a, b, b2, M, N);
+            case 2048: return launch_m16_t<8, 2048, 2, true>(c, a, b, b2, M, N);
+            default: return QH_EINVAL;
+        }
+    } else {
+        const int ct = m16_ct(K, N);
+        switch (K * 10 + ct) {
+            case 10241: return launch_m16_t<8, 1024, 1>(c, a, b, nullptr, M, N);
+            case 10242: return launch_m16_t<8, 1024, 2>(c, a, b, nullptr, M, N);
+            case 20481: return launch_m16_t<8, 2048, 1>(c, a, b, nullptr, M, N);
+            case 20482: return launch_m16_t<8, 2048, 2>(c, a, b, nullptr, M, N);
+            case 30721: return launch_m16_t<8, 3072, 1>(c, a, b, nullptr, M, N);
+            default: return QH_EINVAL;
+        }
     }
 }
 
@@ -3875,9 +3913,7 @@ static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint
         case PLAN_GEMV16:
             if constexpr (GATED) return QH_EINVAL;
             else return launch_gemv16(c, a, b, M, K, N);
-        case PLAN_M16:
-            if constexpr (GATED) return QH_EINVAL;
-            else return launch_m16(c, a, b, M, K, N);
+        case PLAN_M16: return launch_m16<GATED>(c, a, b, b2, M, K, N);
         case PLAN_STREAM_KS1: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 1);
         case PLAN_STREAM_KS2: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 2);
         case PLAN_STREAM_KS4: return launch_stream<GATED>(ws, c, a, b, b2, M, K, N, 4);
@@ -3919,7 +3955,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     }
     if (plan == PLAN_WIDE && (gated || !wide_fits(M, K, N))) plan = PLAN_T64x64;
     if (plan == PLAN_GEMV16 && (gated || !gemv16_fits(M, K, N))) plan = PLAN_T64x64;
-    if (plan == PLAN_M16 && (gated || !m16_fits(M, K, N))) plan = PLAN_T64x64;
+    if (plan == PLAN_M16 && (!m16_fits(M, K, N) || (gated && K > 2048))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
         const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(M, K, N, gated) : NarrowGeom{0, 0, 0, 0};

@@ -52,8 +52,9 @@ H, Q, KV, I, V = 1024, 2048, 1024, 3072, 151936
     (16, I, H, False, "m16"), (32, H, Q, False, "narrow"),
     (8, H, I, False, "m16"), (16, H, H, False, "m16"), (4, H, I, False, "m16"), (2, H, Q, False, "m16"),
     (8, Q, H, False, "m16"), (8, I, H, False, "m16"), (12, I, H, False, "m16"), (16, H, 16384, False, "m16"),
-    (4, Q, H, False, "m16"), (2, Q, H, False, "gemv"), (2, Q, I, False, "m16"), (2, I, 8192, False, "gemv"),
-    (16, Q, 16384, False, "stream"), (8, I, I, False, "m16"), (16, 3072 + 64, H, False, "skinny"), (16, H, 32768, False, "wide"), (16, H, I, True, "pipe32x64k128s4"),
+    (4, Q, H, False, "m16"), (2, Q, H, False, "gemv"), (8, H, I, True, "m16"), (2, H, 2048, True, "gemv"),
+    (16, H, 8192, True, "pipe32x64k128s4"), (1, H, I, True, "gemv"), (4, Q, Q, True, "gemv"), (5, Q, Q, True, "m16"), (16, I, H, True, "pipe32x64k128s4"), (2, Q, I, False, "m16"), (2, I, 8192, False, "gemv"),
+    (16, Q, 16384, False, "stream"), (8, I, I, False, "m16"), (16, 3072 + 64, H, False, "skinny"), (16, H, 32768, False, "wide"), (16, H, I, True, "m16"),
     (128, H, KV, False, "narrow"), (128, H, Q, False, "narrow"), (128, Q, H, False, "narrow"),   # M = 128 prefill
     (128, I, H, False, "narrow"), (256, H, KV, False, "narrow"), (256, Q, H, False, "pipe32x64k128s4"),
     (128, H, I, True, "pipe32x64k64s4"), (160, H, Q, False, "pipe32x64k128s4"),

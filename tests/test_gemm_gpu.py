@@ -351,8 +351,32 @@ def test_m16_kernel(M, K, N):
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
 
 
+@pytest.mark.parametrize("M,K,N", [(16, 1024, 3072), (1, 1024, 48), (7, 2048, 2052), (12, 1024, 1000),
+                                   (16, 2048, 520), (3, 1024, 8200), (16, 1024, 17)])
+def test_m16_gated(M, K, N):
+    """The 16-row kernel's gated form (Wg and Wu rows of 16 columns as a
+    block's two tiles, silu(gate) * up in the epilogue), forced, against the
+    oracle, twice (bit-identical)."""
+    x = oracle.f32_bf16_normal(M * K, 4800 + M)
+    wg = oracle.bf16_normal(N * K, 4801 + M, 0.02)
+    wu = oracle.bf16_normal(N * K, 4802 + M, 0.02)
+    outs = []
+    abi.force_plan(abi.PLANS["m16"])
+    try:
+        for rep in range(2):
+            print(f"m16 gated {M}x{K}x{N} rep {rep}", flush=True)
+            h = np.full(M * N, np.nan, np.float32)
+            abi.gemm_gate_up_silu(h, x, wg, wu, M, K, N)
+            assert abi.last_plan() == "m16"
+            outs.append(h)
+    finally:
+        abi.force_plan(0)
+    numerics.compare_gated(outs[0], x, wg, wu, M, K, N, rows=numerics.pick_rows(M, 16))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("plan", [p for p in ALL_PLANS
-                                  if p.startswith(("ring", "pipe", "xl", "stream", "skinny", "narrow")) or p == "gemv"])
+                                  if p.startswith(("ring", "pipe", "xl", "stream", "skinny", "narrow")) or p in ("gemv", "m16")])
 @pytest.mark.parametrize("M,K,N", [(1, 1024, 640), (70, 1024, 200), (129, 2048, 96), (300, 1024, 400),
                                    (40, 2048, 300), (16, 1024, 3072)])
 def test_every_kernel_variant_gated(plan, M, K, N):
