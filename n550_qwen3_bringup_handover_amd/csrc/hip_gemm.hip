@@ -1887,7 +1887,8 @@ __global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__rest
 // registers in the MFMA fragment order (16 rows x 64 bytes per instruction)
 // they took longer (measured on MI355X, graph-replayed: 16 x {3072, 4096} x
 // 1024 6.53 / 6.81 -> 6.14 / 6.41 us, 64 x 3072 x 1024 10.3 -> 9.2, 48 x
-// 2048 x 1024 9.06 -> 8.26; 8 x 2048 x 1024 5.73 -> 5.84).  No cross-wave reduction: a wave
+// 2048 x 1024 9.06 -> 8.26; 8 x 2048 x 1024 5.73 -> 5.84).  No cross-wave
+// reduction: a wave
 // owns its 16 output columns.  With more than one slice the fp32 sums go to
 // part[slice][j][M][N] (j = gate/up when GATED) and k_stream_reduce adds the
 // slices in order; otherwise C (or silu(gate)*up) is written directly.
