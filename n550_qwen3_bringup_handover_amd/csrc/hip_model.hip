@@ -227,7 +227,11 @@ __global__ __launch_bounds__(NTH) void k_qk_rope_cache(float *__restrict__ qkv, 
 // of a chunk falls by QT.  Positions past a row's own context score -inf
 // and weigh 0: its max, sums and weighted V are those of a one-token block
 // bit for bit (only exact zeros are added, after its own positions).
-// grid = (ceil(nt / QT), NKV), 256 threads, dynamic LDS =
+// grid = ceil(nt / QT) * NKV blocks, block b taking kv head b % NKV and tokens
+// QT (b / NKV) ..: blocks run on XCD b mod 8, so each XCD serves one head's K
+// and V from its own L2 (measured on MI355X against a (tokens, head) grid:
+// 128-token prefill 1.65 -> 1.62 ms, 2,014 tokens 39.7 -> 39.1 ms); 256 threads,
+// dynamic LDS =
 // qm_attention_lds_bytes(QT, ldp); ldp >= pos0 + nt is the score row stride.
 // ---------------------------------------------------------------------------
 template <int QT>
@@ -238,7 +242,7 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
                                                    const int *__restrict__ pos_d, int nt, int max_seq,
                                                    int ldp, float scale) {
     constexpr int R = QT * GRP;
-    const int i0 = blockIdx.x * QT, g = blockIdx.y, tid = threadIdx.x;
+    const int g = blockIdx.x % NKV, i0 = (int)(blockIdx.x / NKV) * QT, tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63;
     const int pos0 = *pos_d;
     const int nq = min(QT, nt - i0);           // tokens of this block
@@ -740,7 +744,7 @@ extern "C" int qm_attention(float *qkv, float *out, float *kc, float *vc, const 
     if (hipGetLastError() != hipSuccess) return QH_ELAUNCH;
     const int qt = attention_qt(ctx_bound);
     const size_t lds = qm_attention_lds_bytes(qt, ctx_bound);
-    const dim3 grid((nt + qt - 1) / qt, NKV);
+    const dim3 grid((unsigned)(((nt + qt - 1) / qt) * NKV));
     if (qt == 2)
         hipLaunchKernelGGL(k_attention<2>, grid, dim3(NTH), lds, stream(), qkv, out, kc, vc, pos_d, nt, max_seq,
                            ctx_bound, scale);
