@@ -21,11 +21,13 @@ the library's QW3M writer and compare the checksum first.  The prompt comes
 from the oracle's SplitMix64 stream.  Usage:
 
     python tests/golden/make_model_fixtures.py [short|p128_d128|batch|dump|all]
-    python tests/golden/make_model_fixtures.py [long|p128_d128_logits|steps]
+    python tests/golden/make_model_fixtures.py [long|p128_d128_logits|ctx2048|steps]
 
-  model_long.npz, model_p128_d128_logits.npz ("steps"): the reference built
-  with a 2048-position cache; prompt, greedy tokens, margins, the last
-  prefill logits row and the logits after chosen decode steps (float16).
+  model_long.npz, model_p128_d128_logits.npz, model_ctx2048.npz ("steps"):
+  the reference built with a 2048-position cache; prompt, greedy tokens,
+  margins, the last prefill logits row and the logits after chosen decode
+  steps (float16).  ctx2048 runs to position 2047 on the prompt of sequence 0
+  of the 64-sequence batched-decode workload.
 """
 import ctypes
 import os
@@ -105,7 +107,19 @@ STEP_CASES = {
     # name: (n_prompt, n_decode, decode steps whose logits are kept, prompt seed)
     "long": (1100, 8, (1, 4, 8), PROMPT_SEED + 0x100),
     "p128_d128_logits": (128, 128, (1, 32, 64, 128), PROMPT_SEED),
+    # the batched-decode workload's sequence 0 (64 sequences at context 2048:
+    # a 2014-token prompt, 2 untimed steps, then 32 timed ones, the last at
+    # position 2047): its prompt is the first draw of numpy's default_rng(5)
+    "ctx2048": (2014, 34, (1, 2, 3, 8, 16, 34), ("numpy", 5)),
 }
+
+
+def step_prompt(n_prompt, pseed):
+    """A case's prompt: the oracle's SplitMix64 stream for an integer seed,
+    or numpy's default_rng(seed).integers(0, VOCAB, n) for ("numpy", seed)."""
+    if isinstance(pseed, tuple):
+        return np.random.default_rng(pseed[1]).integers(0, VOCAB, n_prompt).astype(np.int32)
+    return prompt_tokens(n_prompt, pseed)
 
 
 def run_steps(name):
@@ -121,7 +135,7 @@ def run_steps(name):
     L.refdrv_max_seq.restype = ctypes.c_int
     assert L.refdrv_max_seq() == 2048
     blob = M.qw3m_random(SEED, M.LAYOUT_ROW, threads=8)
-    prompt = prompt_tokens(n_prompt, pseed)
+    prompt = step_prompt(n_prompt, pseed)
     out = np.zeros(n_decode + 1, np.int32)
     margins = np.zeros(n_decode + 1, np.float32)
     logits = np.zeros(VOCAB, np.float32)
