@@ -4173,6 +4173,9 @@ extern "C" int qh_graph_launch(int id) {
 
 extern "C" int qh_graph_destroy(int id) {
     if (id < 0 || id >= QH_MAX_GRAPHS || !g_graph_exec[id]) return QH_EINVAL;
+    // a launch of this graph may still run: wait for the stream first, so
+    // no caller has to
+    HCHECK(hipStreamSynchronize(g_stream), QH_ERUNTIME);
     HCHECK(hipGraphExecDestroy(g_graph_exec[id]), QH_ERUNTIME);
     g_graph_exec[id] = nullptr;
     g_graph_ws[id][0] = g_graph_ws[id][1] = nullptr;

@@ -291,14 +291,23 @@ __global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p)
             put_rows<1>(v, out + OUT_X, x + 3 * XCH_LD, gw, tag, lane);
         }
     }
-    // every workgroup read the epoch before producing anything, and workgroup
-    // 0 gets here only after every workgroup's last outputs reached it
-    if (blockIdx.x == 0 && tid == 0) __hip_atomic_store(p.state, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the next launch's epoch is published by the last workgroup to finish
+    // (an arrival count in state[2]): every workgroup read this launch's
+    // epoch before it arrives, so none -- not even one that started late,
+    // after another gave up waiting -- can tag its words with the next one
+    if (tid == 0) {
+        const unsigned arrived =
+            __hip_atomic_fetch_add(p.state + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (arrived == gridDim.x - 1) {
+            __hip_atomic_store(p.state + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.state, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // ---- host side ------------------------------------------------------------------
 static uint64_t *g_xch = nullptr;     // [PS_MAX_LAYERS][4][XCH_LD] exchange words
-static unsigned *g_state = nullptr;   // epoch, error flags
+static unsigned *g_state = nullptr;   // epoch, error flags, arrivals of the running launch
 static int g_ps_ok = 0;               // 1 = the device keeps the grid resident
 
 // at library init (device current): the exchange words start at tag 0,
