@@ -137,13 +137,11 @@ def run_cpu_baseline(budget_s):
 MODEL_SEED = 0x03550040      # random-init weights of the full-forward workload
 
 
-def cpu_model_child(n_prompt=16, n_decode=16):
+def cpu_model_child(n_prompt=128, n_decode=128):
     """The reference forward (qwen3.c + kernels_scalar.c + ops_scalar.c,
-    compiled from source into oracle/_ref) on 1 core, on a bounded sample of
-    the 128-token-prompt + 128-greedy-step workload: a 16-token prompt
-    prefilled, then the same with 16 greedy decode steps; the difference of
-    the two times is the decode time of 16 steps (the full workload would take
-    about 80 s on one core)."""
+    compiled from source into oracle/_ref) on 1 core on the full-forward
+    workload itself: the 128-token prompt prefilled, then 128 greedy decode
+    steps; the driver times the prefill and the decode loop separately."""
     import numpy as np
     import oracle
     from n550_qwen3_bringup_handover_amd import model as M
@@ -151,41 +149,49 @@ def cpu_model_child(n_prompt=16, n_decode=16):
     if L is None:
         print(json.dumps({"value": None, "error": "oracle/_ref/libref_model_scalar.so not built"}))
         return
-    blob = M.qw3m_random(MODEL_SEED, M.LAYOUT_ROW, threads=16)   # before pinning to one core
-    os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    blob = M.qw3m_random(MODEL_SEED, M.LAYOUT_ROW, threads=4)    # before pinning to one core
+    core = sorted(os.sched_getaffinity(0))[-1]
+    os.sched_setaffinity(0, {core})
     L.refdrv_generate.restype = ctypes.c_int
     L.refdrv_generate.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int),
                                   ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                   ctypes.c_void_p, ctypes.c_void_p]
+    L.refdrv_last_times.restype = None
+    L.refdrv_last_times.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]
     prompt = np.random.default_rng(4).integers(0, V, n_prompt).astype(np.int32)
     out = np.zeros(n_decode + 1, np.int32)
-
-    def run(nd):
-        t0 = time.perf_counter()
-        n = L.refdrv_generate(blob.ctypes.data_as(ctypes.c_void_p), blob.nbytes,
-                              prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), n_prompt, nd, 0,
-                              out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), None, None)
-        return n, time.perf_counter() - t0
-    n0, t_pre = run(0)
-    n1, t_all = run(n_decode)
-    dec = t_all - t_pre
-    ok = n0 == 1 and n1 == n_decode + 1 and dec > 0
-    print(json.dumps({"value": n_decode / dec if ok else None, "unit": "tok/s", "cores": 1, "kind": "reference",
-                      "prefill_tok_s": n_prompt / t_pre if ok else None,
-                      "sample": f"reference forward qwen3.c + kernels_scalar.c + ops_scalar.c on 1 core: "
-                                f"a {n_prompt}-token prompt prefilled ({t_pre:.2f} s), then the same with "
-                                f"{n_decode} greedy decode steps ({t_all:.2f} s); decode tok/s = "
-                                f"{n_decode} / the difference.  A bounded sample of the 128 + 128 workload "
-                                f"(per decode step the scalar GEMMs dominate; attention at these "
-                                f"positions is < 1% of a step)"}))
+    n = L.refdrv_generate(blob.ctypes.data_as(ctypes.c_void_p), blob.nbytes,
+                          prompt.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), n_prompt, n_decode, 0,
+                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), None, None)
+    t_pre, t_dec = ctypes.c_double(), ctypes.c_double()
+    L.refdrv_last_times(ctypes.byref(t_pre), ctypes.byref(t_dec))
+    ok = n == n_decode + 1 and t_dec.value > 0
+    print(json.dumps({"value": n_decode / t_dec.value if ok else None, "unit": "tok/s", "cores": 1,
+                      "kind": "reference", "prefill_tok_s": n_prompt / t_pre.value if ok else None,
+                      "prefill_s": round(t_pre.value, 2), "decode_s": round(t_dec.value, 2),
+                      "first_tokens": [int(t) for t in out[:8]],
+                      "sample": f"the whole workload: reference forward qwen3.c + kernels_scalar.c + "
+                                f"ops_scalar.c on 1 core (core {core}, run beside the GPU measurements), "
+                                f"the {n_prompt}-token prompt prefilled in {t_pre.value:.1f} s, then "
+                                f"{n_decode} greedy decode steps in {t_dec.value:.1f} s"}))
 
 
-def run_cpu_model():
-    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-model-child"],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        return {"value": None, "error": r.stderr.strip()[-400:]}
-    return json.loads(r.stdout.strip().splitlines()[-1])
+def start_cpu_model():
+    """the full-forward CPU baseline as a child process on its own core,
+    started before the GPU measurements and collected after them"""
+    return subprocess.Popen([sys.executable, os.path.abspath(__file__), "--cpu-model-child"],
+                            stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def finish_cpu_model(proc):
+    try:
+        out, err = proc.communicate(timeout=900)
+    except subprocess.TimeoutExpired:
+        proc.kill()
+        return {"value": None, "error": "timed out"}
+    if proc.returncode != 0:
+        return {"value": None, "error": err.strip()[-400:]}
+    return json.loads(out.strip().splitlines()[-1])
 
 
 def host_path(steps=5):
@@ -723,9 +729,10 @@ def main():
                                    "not built", "n_gpus": args.gpus}))
         return 2
 
-    # CPU baselines first, before this process touches the GPU
+    # CPU baselines before this process touches the GPU: the full-forward one
+    # runs in the background on the last core until the model measurements
+    cpu_model_proc = None if (args.no_cpu_baseline or args.no_model) else start_cpu_model()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args.cpu_budget)
-    cpu_model = None if (args.no_cpu_baseline or args.no_model) else run_cpu_model()
 
     g = Gpu()
     layers, emb, act = build_decode_model(g)
@@ -787,7 +794,10 @@ def main():
     model = batch = None
     if not args.no_model:
         model = model_forward_p128_d128()
-        model["cpu_baseline"] = cpu_model
+        model["cpu_baseline"] = None
+        if cpu_model_proc is not None:
+            print("waiting for the full-forward CPU baseline", file=sys.stderr, flush=True)
+            model["cpu_baseline"] = finish_cpu_model(cpu_model_proc)
         batch = model_batch_decode()
     hostp = None if args.no_extras else host_path()
 

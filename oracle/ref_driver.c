@@ -7,10 +7,24 @@
  * of the prompt (chunked by QWEN3_MAX_BATCH), argmax of the last logits,
  * then one qwen3_forward per generated token.
  */
+#define _POSIX_C_SOURCE 199309L
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "qwen3.h"
+
+/* wall-clock seconds of the last refdrv_generate's prefill and decode loops */
+static double g_t_prefill, g_t_decode;
+static double now_s(void) {
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (double)t.tv_sec + 1e-9 * (double)t.tv_nsec;
+}
+void refdrv_last_times(double *prefill_s, double *decode_s) {
+    *prefill_s = g_t_prefill;
+    *decode_s = g_t_decode;
+}
 
 size_t refdrv_scratch_bytes(void) { return qwen3_scratch_bytes(); }
 int refdrv_max_seq(void) { return QWEN3_MAX_SEQ; }
@@ -91,6 +105,7 @@ int refdrv_generate(const void *blob, size_t blob_size,
         return QWEN3_ERR_SHAPE;
     }
 
+    const double t0 = now_s();
     for (int p0 = 0; p0 < n_prompt; p0 += QWEN3_MAX_BATCH) {
         int nt = n_prompt - p0 < QWEN3_MAX_BATCH ? n_prompt - p0 : QWEN3_MAX_BATCH;
         qwen3_forward_batch(&m, prompt + p0, nt, p0);
@@ -102,6 +117,7 @@ int refdrv_generate(const void *blob, size_t blob_size,
     int next = qwen3_argmax(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
     if (margins) margins[n_out] = top2_margin(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
     out[n_out++] = next;
+    const double t1 = now_s();
     for (int step = 0; step < n_decode; step++) {
         if (stop_at_eos &&
             (next == QWEN3_EOS_TOKEN_ID_0 || next == QWEN3_EOS_TOKEN_ID_1))
@@ -111,6 +127,8 @@ int refdrv_generate(const void *blob, size_t blob_size,
         if (margins) margins[n_out] = top2_margin(qwen3_last_logits(&m), QWEN3_VOCAB_SIZE);
         out[n_out++] = next;
     }
+    g_t_prefill = t1 - t0;
+    g_t_decode = now_s() - t1;
     free(scratch);
     return n_out;
 }
