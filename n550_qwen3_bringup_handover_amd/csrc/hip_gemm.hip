@@ -330,12 +330,14 @@ struct GemvPro {
 // MERGE: a holds split attention partials (qh_gemv_merge) and the activation
 // row is their softmax merge; their loads go out before the weight loads,
 // the merge arithmetic after them.
-template <int ROWS, int CPL, bool GATED, bool PRO = false, bool MERGE = false>
-__global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
-                                                   const float *__restrict__ a,
-                                                   const uint16_t *__restrict__ b,
-                                                   const uint16_t *__restrict__ b2,
-                                                   int K, int N, GemvPro pro) {
+// KA: the activation row arrives already rounded to packed bf16 pairs in the
+// kernel arguments (ka: the kernel-argument segment, GemvKaRow first) -- the
+// host-pointer path's M = 1 calls with K <= 1024, which then need no copy of
+// A to the device before the GEMV.
+template <int ROWS, int CPL, bool GATED, bool PRO, bool MERGE, bool KA>
+__device__ __forceinline__ void gemv1_body(float *__restrict__ c, const float *__restrict__ a,
+                                           const uint16_t *__restrict__ b, const uint16_t *__restrict__ b2,
+                                           int K, int N, GemvPro pro, const uint2 *__restrict__ ka) {
     constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
     constexpr int NQ = CPL * 2 * WAVE;               // 4-element groups of the padded row (512*CPL)
     constexpr int QMAX = (NQ + NTHREADS - 1) / NTHREADS;
@@ -376,6 +378,8 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
                                                          rp, ps + 16u + (uint32_t)(ii & 31) * 16u, 0, 0));
             }
         }
+    } else if constexpr (KA) {
+        // nothing to load ahead: the row is in the kernel arguments
     } else if constexpr (!PRO) {
         const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)K * 4);
 #pragma unroll
@@ -429,7 +433,14 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
     // 3. activation through LDS as bf16 (RNE), normalised first for PRO;
     //    zeros past K
     uint2 *sx2 = reinterpret_cast<uint2 *>(sx);
-    if constexpr (PRO) {
+    if constexpr (KA) {
+        // the host rounded the row and zeroed it past K
+#pragma unroll
+        for (int q = 0; q < QMAX; q++) {
+            const int i = tid + NTHREADS * q;
+            if (NQ % NTHREADS == 0 || i < NQ) sx2[i] = ka[i];
+        }
+    } else if constexpr (PRO) {
 #pragma unroll
         for (int q = 0; q < QMAX; q++)
             xa[q] = f32x4{bf16_lo(e[q].x), bf16_hi(e[q].x), bf16_lo(e[q].y), bf16_hi(e[q].y)} + (xv[q] + rv[q]);
@@ -514,6 +525,29 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
         }
     }
     if (lane < ROWS && row0 + lane < N) c[row0 + lane] = GATED ? silu_mul(tot, up) : tot;
+}
+
+template <int ROWS, int CPL, bool GATED, bool PRO = false, bool MERGE = false>
+__global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
+                                                   const float *__restrict__ a,
+                                                   const uint16_t *__restrict__ b,
+                                                   const uint16_t *__restrict__ b2,
+                                                   int K, int N, GemvPro pro) {
+    gemv1_body<ROWS, CPL, GATED, PRO, MERGE, false>(c, a, b, b2, K, N, pro, nullptr);
+}
+
+// the activation row of a KA launch: K <= 1024 bf16 values, zero past K
+// (first kernel argument, so it sits at offset 0 of the argument segment)
+struct GemvKaRow {
+    uint32_t w[512];
+};
+template <int ROWS, int CPL, bool GATED>
+__global__ __launch_bounds__(NTHREADS) void k_gemv1_ka(GemvKaRow row, float *__restrict__ c,
+                                                      const uint16_t *__restrict__ b,
+                                                      const uint16_t *__restrict__ b2, int K, int N) {
+    (void)row;   // read in place, through the argument segment
+    const uint2 *ka = (const uint2 *)__builtin_amdgcn_kernarg_segment_ptr();   // address space 4 to generic
+    gemv1_body<ROWS, CPL, GATED, false, false, true>(c, nullptr, b, b2, K, N, GemvPro{}, ka);
 }
 
 // Fused gate/up GEMV: rows of Wg and Wu with the same index share a wave, and
@@ -2691,6 +2725,7 @@ static char g_devname[256];
 static hipEvent_t g_ev[64];
 static int g_ev_made[64];
 static int g_forced_plan = 0;
+static int g_last_plan = 0;        // the plan the last GEMM call launched (PLAN_AUTO: none yet)
 #define QH_MAX_GRAPHS 16
 static hipGraphExec_t g_graph_exec[QH_MAX_GRAPHS];
 static void *g_graph_ws[QH_MAX_GRAPHS][2];   // library workspaces each graph uses (abf, part)
@@ -3263,6 +3298,47 @@ static int launch_gemv1_t(float *c, const float *a, const uint16_t *b, const uin
 static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                         int K, int N, bool gated) {
     return launch_gemv1_t<false>(c, a, b, b2, K, N, gated, GemvPro{});
+}
+
+// M = 1 with K <= 1024 (K % 8 == 0) and the activation row already rounded
+// to bf16 on the host (`row`: 1024 bf16 values, zero past K): the row goes
+// in the launch's kernel arguments, so nothing is copied to the device before
+// the GEMV.  Same kernel body, row choice and results as launch_gemv1_t.
+template <int ROWS, int CPL>
+static int launch_gemv1_ka(float *c, const GemvKaRow &row, const uint16_t *b, const uint16_t *b2, int K, int N) {
+    const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
+    const size_t lds = (size_t)(4 * WAVE * CPL + 8) * sizeof(uint32_t);
+    if (b2)
+        hipLaunchKernelGGL((k_gemv1_ka<ROWS, CPL, true>), dim3(grid), dim3(NTHREADS), lds, g_stream, row, c, b, b2,
+                           K, N);
+    else
+        hipLaunchKernelGGL((k_gemv1_ka<ROWS, CPL, false>), dim3(grid), dim3(NTHREADS), lds, g_stream, row, c, b,
+                           nullptr, K, N);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+extern "C" int qh_gemv_ka(float *c, const uint16_t *row_bf16, const uint16_t *b, const uint16_t *b2, int K, int N) {
+    if (!g_inited) return QH_ESTATE;
+    if (!c || !row_bf16 || !b || K <= 0 || K > 1024 || (K % 8) || N <= 0 || !aligned16(b) || (b2 && !aligned16(b2)))
+        return QH_EINVAL;
+    if ((size_t)N * K * 2 >= (1ull << 31)) return QH_ETOOBIG;
+    GemvKaRow row;
+    memcpy(row.w, row_bf16, sizeof row.w);
+    const int cpl = (K / 8 + WAVE - 1) / WAVE;
+    const int per_row = b2 ? 2 * cpl : cpl;
+    int rows = 4;
+    while (rows > 1 && (long)(N + rows - 1) / rows < 4096) rows /= 2;
+    while (rows > 1 && rows * per_row > 16) rows /= 2;
+    g_last_plan = PLAN_GEMV;
+    switch (rows * 2 + (cpl - 1)) {
+        case 2: return launch_gemv1_ka<1, 1>(c, row, b, b2, K, N);
+        case 3: return launch_gemv1_ka<1, 2>(c, row, b, b2, K, N);
+        case 4: return launch_gemv1_ka<2, 1>(c, row, b, b2, K, N);
+        case 5: return launch_gemv1_ka<2, 2>(c, row, b, b2, K, N);
+        case 8: return launch_gemv1_ka<4, 1>(c, row, b, b2, K, N);
+        case 9: return launch_gemv1_ka<4, 2>(c, row, b, b2, K, N);
+        default: return QH_EINVAL;
+    }
 }
 
 extern "C" int qh_gemv_merge(float *c, const float *part, const uint16_t *b, int K, int N) {
@@ -3868,7 +3944,6 @@ static int dispatch_bf16a(int p, float *c, const uint16_t *a, const uint16_t *b,
     }
 }
 
-static int g_last_plan = PLAN_AUTO;     // the plan the last GEMM call launched
 
 template <bool GATED>
 static int dispatch(int plan, const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
@@ -4265,7 +4340,15 @@ extern "C" int qh_gemv_pro(float *c, const qh_gemv_pro_t *p, const uint16_t *b, 
         (p->x && !aligned16(p->x)) || (p->r && !aligned16(p->r)) ||
         (p->x_out && !aligned16(p->x_out)) || (p->emb && !aligned16(p->emb)))
         return QH_EINVAL;
-    const GemvPro pro{p->emb ? nullptr : p->x, p->emb, p->tok, p->emb_rows,
-                      p->emb ? nullptr : p->r, p->nw, p->x_out, p->eps};
+    GemvPro pro;
+    memset(&pro, 0, sizeof pro);     // no stray stack bytes in the kernel arguments' padding
+    pro.x = p->emb ? nullptr : p->x;
+    pro.emb = p->emb;
+    pro.tok = p->tok;
+    pro.emb_rows = p->emb_rows;
+    pro.r = p->emb ? nullptr : p->r;
+    pro.nw = p->nw;
+    pro.x_out = p->x_out;
+    pro.eps = p->eps;
     return launch_gemv1_t<true>(c, nullptr, b, b2, K, N, gated != 0, pro);
 }

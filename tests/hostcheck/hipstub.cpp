@@ -212,12 +212,14 @@ void check_node(const Node &n, const char *where) {
     }
 }
 
-bool node_uses(const Node &n, uintptr_t base, size_t size) {
+// the node's pointer argument, or 8-byte aligned by-value word (taken as a
+// pointer field, as in check_node), that lies in [base, base + size); 0 if none
+uintptr_t node_uses(const Node &n, uintptr_t base, size_t size) {
     for (uintptr_t p : n.ptrs)
-        if (p >= base && p < base + std::max<size_t>(size, 1)) return true;
+        if (p >= base && p < base + std::max<size_t>(size, 1)) return p;
     for (uintptr_t w : n.words)
-        if (w >= base && w < base + std::max<size_t>(size, 1)) return true;
-    return false;
+        if ((w & 7) == 0 && w >= base && w < base + std::max<size_t>(size, 1)) return w;
+    return 0;
 }
 
 void complete(ihipStream_t *s, uint64_t upto) {
@@ -263,9 +265,9 @@ hipError_t fake_free(void *p, int kind, const char *what) {
     for (auto *e : g_execs) {
         if (!e->alive) continue;
         for (const Node &n : e->nodes)
-            if (node_uses(n, it->first, it->second.size)) {
-                violation("%s(%p): allocation #%ld is used by live graph exec #%ld (kernel %s)", what, p,
-                          it->second.id, e->id, n.name.c_str());
+            if (const uintptr_t u = node_uses(n, it->first, it->second.size)) {
+                violation("%s(%p): allocation #%ld (%zu bytes) is used by live graph exec #%ld (kernel %s, "
+                          "argument %p)", what, p, it->second.id, it->second.size, e->id, n.name.c_str(), (void *)u);
                 break;
             }
     }

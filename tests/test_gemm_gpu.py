@@ -690,3 +690,49 @@ def test_argmax_dev(n):
         abi.argmax_dev(od.ptr, vd.ptr, n)
         got = int(od.download(np.int32, 1)[0])
         assert got == oracle.argmax(t)
+
+
+@pytest.mark.parametrize("K,N,gated", [(1024, 2048, False), (1024, 1024, False), (1024, 3072, True), (1024, V, False),
+                                       (1000, 300, False), (512, 777, True), (8, 64, False), (1032, 100, False),
+                                       (2048, 1024, False), (3072, 1024, False)])
+def test_host_path_m1_matches_device_path(K, N, gated):
+    """M = 1 through the host-pointer ABI -- for K <= 1024 the row rounded to
+    bf16 on the host and passed in the GEMV's kernel arguments, completion
+    seen in the pinned output -- bit-identical to the device-pointer entry
+    point on the same data, including non-bf16-representable activations
+    (ties rounded to even), zeros, infinities and a NaN in A (then every
+    output is NaN on both paths)."""
+    a, b = inputs(1, K, N, 900 + K % 97 + N % 89)
+    a = (a * np.float32(1.0 + 2 ** -9)).astype(np.float32)      # not bf16-representable
+    a[::7] = 0.0
+    a[1] = np.float32(1.0 + 2 ** -8)                              # a tie: rounds to even (1.0)
+    a[2] = np.float32(1.0 + 3 * 2 ** -8)                          # a tie: rounds up
+    b2 = oracle.bf16_normal(N * K, 901 + N % 89, 0.02) if gated else None
+    bb = np.concatenate([b, b2]) if gated else b
+
+    def both(a):
+        c_host = np.full(N, np.nan, np.float32)
+        if gated:
+            abi.gemm_gate_up_silu(c_host, a, b, b2, 1, K, N)
+        else:
+            abi.gemm(c_host, a, b, 1, K, N)
+        ad, bd = abi.DeviceBuffer.from_array(a), abi.DeviceBuffer.from_array(bb)
+        cd = abi.DeviceBuffer(N * 4)
+        if gated:
+            abi.gemm_gate_up_silu_dev(cd.ptr, ad.ptr, bd.ptr, bd.ptr + 2 * N * K, 1, K, N)
+        else:
+            abi.gemm_dev(cd.ptr, ad.ptr, bd.ptr, 1, K, N)
+        abi.sync()
+        return c_host, cd.download(np.float32, N)
+
+    c_host, c_dev = both(a)
+    assert np.array_equal(c_host.view(np.uint32), c_dev.view(np.uint32))
+    if gated:
+        numerics.compare_gated(c_host, a, b, b2, 1, K, N)
+    else:
+        numerics.compare(c_host, a, b, 1, K, N)
+    a_nan = a.copy()
+    a_nan[K // 2] = np.nan
+    a_nan[3] = np.inf
+    c_host, c_dev = both(a_nan)
+    assert np.all(np.isnan(c_host)) and np.all(np.isnan(c_dev))
