@@ -2127,9 +2127,8 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // counter to zero for the next call.  No block waits for another and there
 // is no second launch.  Loads past M and N read zeros at out-of-range
 // offsets.
-#define NARROW_COLS 32
-#define NARROW_RSTRIDE (NARROW_COLS + 4)   // +4: conflict-free column writes, 16-byte aligned rows
-template <int MT, int KPW, bool GATED>
+#define NARROW_COLS 32                // the widest column block (NCOL); 16 is the other
+template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS>
 __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
                                                             unsigned *__restrict__ cnt,
                                                             const float *__restrict__ a,
@@ -2137,8 +2136,9 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
                                                             const uint16_t *__restrict__ b2, int M, int K, int N) {
     constexpr int NJ = GATED ? 2 : 1;
     constexpr int KSL = 128 * KPW, CH = KSL / 8;         // slice depth, 16-byte chunks per row
-    constexpr int NT = NARROW_COLS / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
-    constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * NARROW_RSTRIDE / 4;
+    constexpr int NT = NCOL / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
+    constexpr int RSTRIDE = NCOL + 4;                     // +4: conflict-free column writes, 16-byte aligned rows
+    constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * RSTRIDE / 4;
     static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
     __shared__ __align__(16) u32x4 smem[SA_U4 > RED_U4 ? SA_U4 : RED_U4];
     // weights in row order through per-wave LDS rows where they fit
@@ -2153,7 +2153,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.x * KSL, ks = gridDim.x;
-    const int n0 = blockIdx.y * NARROW_COLS, m0 = blockIdx.z * ROWS;
+    const int n0 = blockIdx.y * NCOL, m0 = blockIdx.z * ROWS;
     const size_t MN = (size_t)M * N;
 
     // 1. every load at once: first the block's A slice (rows past M read
@@ -2161,17 +2161,23 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     //    n0 + 16 nt + r16, k = k0 + 32 (KPW w + s) + 8 g; from HBM), so that the
     //    slice is rounded into LDS while the weights are still in flight
     constexpr int PER = ROWS * CH / NTHREADS;             // 32-byte pieces of A per thread
-    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PER + NJ * NT * KPW <= 64, "loads in flight");
+    // Where A's pieces and the weights together would pass 48 loads in
+    // flight (the 16-wide blocks with one 3072-deep slice), A comes in two
+    // halves: the second is loaded once the first is in LDS, while the
+    // weights are still on their way from HBM.
+    constexpr int PA = (2 * PER + NJ * NT * KPW > 48) ? (PER + 1) / 2 : PER;
+    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PA + NJ * NT * KPW <= 64, "loads in flight");
     const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
-    u32x4 lo[PER], hi[PER];
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
+    u32x4 lo[PA], hi[PA];
+    auto load_a = [&](int i, int slot) {                  // piece i into register slot
         const int q = tid + NTHREADS * i;
         const int m = m0 + q / CH, ch = q % CH;
         const uint32_t off = (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4);
-        lo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
-        hi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off + 16u : BUF_OOB, 0, 0);
-    }
+        lo[slot] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
+        hi[slot] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off + 16u : BUF_OOB, 0, 0);
+    };
+#pragma unroll
+    for (int i = 0; i < PA; i++) load_a(i, i);
     const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
     const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
     u32x4 bq[NJ][NT][KPW];
@@ -2210,17 +2216,25 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
         }
     }
 
-    // 2. A rounded to bf16 (RNE) into LDS
-#pragma unroll
-    for (int i = 0; i < PER; i++) {
+    // 2. A rounded to bf16 (RNE) into LDS (the second half, if any, loaded
+    //    and rounded after the first)
+    auto store_a = [&](int i, int slot) {
         const int q = tid + NTHREADS * i;
         const int m = q / CH, ch = q % CH;
         u32x4 v;
-        v.x = pack_bf16x2(__uint_as_float(lo[i].x), __uint_as_float(lo[i].y));
-        v.y = pack_bf16x2(__uint_as_float(lo[i].z), __uint_as_float(lo[i].w));
-        v.z = pack_bf16x2(__uint_as_float(hi[i].x), __uint_as_float(hi[i].y));
-        v.w = pack_bf16x2(__uint_as_float(hi[i].z), __uint_as_float(hi[i].w));
+        v.x = pack_bf16x2(__uint_as_float(lo[slot].x), __uint_as_float(lo[slot].y));
+        v.y = pack_bf16x2(__uint_as_float(lo[slot].z), __uint_as_float(lo[slot].w));
+        v.z = pack_bf16x2(__uint_as_float(hi[slot].x), __uint_as_float(hi[slot].y));
+        v.w = pack_bf16x2(__uint_as_float(hi[slot].z), __uint_as_float(hi[slot].w));
         sa[m * CH + (ch ^ (m & 15))] = v;
+    };
+#pragma unroll
+    for (int i = 0; i < PA; i++) store_a(i, i);
+    if constexpr (PA < PER) {
+#pragma unroll
+        for (int i = PA; i < PER; i++) load_a(i, i - PA);
+#pragma unroll
+        for (int i = PA; i < PER; i++) store_a(i, i - PA);
     }
     __syncthreads();
 
@@ -2269,14 +2283,15 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
             for (int mt = 0; mt < MT; mt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    red[((w * NJ + j) * ROWS + 16 * mt + 4 * g + r) * NARROW_RSTRIDE + 16 * nt + r16] =
+                    red[((w * NJ + j) * ROWS + 16 * mt + 4 * g + r) * RSTRIDE + 16 * nt + r16] =
                         acc[j][nt][mt][r];
     __syncthreads();
 
-    // 5. quads of 4 columns, q = tid + NTHREADS i: row m0 + q / 8, columns
-    //    4 (q % 8) .. +3, summed over the waves in order; N % 4 == 0, so a
-    //    quad is wholly in or out
-    constexpr int NQ = ROWS * NARROW_COLS / 4, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
+    // 5. quads of 4 columns, q = tid + NTHREADS i: row m0 + q / QR, columns
+    //    4 (q % QR) .. +3 (QR = NCOL / 4 quads per row), summed over the
+    //    waves in order; N % 4 == 0, so a quad is wholly in or out
+    constexpr int QR = NCOL / 4;
+    constexpr int NQ = ROWS * QR, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
     static_assert(NQ % NTHREADS == 0 || NQ < NTHREADS, "quads per thread");
     f32x4 v[NJ][QPT];
     uint32_t coff[QPT];                                   // byte offset of the quad in C, or BUF_OOB
@@ -2284,13 +2299,13 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     for (int i = 0; i < QPT; i++) {
         const bool live = tid + NTHREADS * i < NQ;        // MT = 1: half of the threads
         const int q = live ? tid + NTHREADS * i : 0;
-        const int m = q >> 3, cq = 4 * (q & 7), n = n0 + cq;
+        const int m = q / QR, cq = 4 * (q % QR), n = n0 + cq;
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
-            f32x4 t = *reinterpret_cast<const f32x4 *>(&red[(j * ROWS + m) * NARROW_RSTRIDE + cq]);
+            f32x4 t = *reinterpret_cast<const f32x4 *>(&red[(j * ROWS + m) * RSTRIDE + cq]);
 #pragma unroll
             for (int ww = 1; ww < NW; ww++)
-                t += *reinterpret_cast<const f32x4 *>(&red[((ww * NJ + j) * ROWS + m) * NARROW_RSTRIDE + cq]);
+                t += *reinterpret_cast<const f32x4 *>(&red[((ww * NJ + j) * ROWS + m) * RSTRIDE + cq]);
             v[j][i] = t;
         }
         coff[i] = (live && m0 + m < M && n < N) ? (uint32_t)(((size_t)(m0 + m) * N + n) * 4) : BUF_OOB;
@@ -2484,7 +2499,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c
                 const f32x4 v = *reinterpret_cast<const f32x4 *>(&sc[row * 32 + ((cq ^ (row & 7)) << 2)]);
                 const int m = 32 * h + row, n = 32 * t + 4 * cq;
                 const uint32_t off = (m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 2);   // nt
             }
         }
     };
@@ -3708,73 +3723,86 @@ static int launch_skinny(const Ws &ws, float *c, const float *a, const uint16_t 
 // slice), 64x1024x2048 6.0 -> 4.2 (16-row slabs), 64x2048x1024 7.4 (64 rows,
 // 8 slices) -> 6.2 (32 rows, 4 slices), 64x3072x1024 7.9 -> 6.9.
 struct NarrowGeom {
-    int mt, slabs, kpw, ks;
+    int mt, slabs, kpw, ks, ncol;
 };
 static inline int narrow_kmax(int mt, bool gated) {
     const int lim = 64 / (2 * mt + 2 * (gated ? 2 : 1));
     return lim >= 8 ? 8 : lim >= 6 ? 6 : lim >= 4 ? 4 : lim >= 3 ? 3 : lim >= 2 ? 2 : 1;
 }
+// The geometry of a narrow launch, searched per shape: the most CUs filled in
+// one round, then one slice (no sums at all), then the fewest bytes a block
+// moves, counting the sums its last block reads twice.  Column blocks are 32
+// wide, or 16 wide with 16-row slabs, not gated, and slices of 1024, 2048 or
+// 3072: that form takes K = 1024 - 3072 in one slice where the 32-wide
+// blocks need 2-8 (64 x {1024, 2048, 3072} x 1024: 256 blocks and no slice
+// sums; measured on MI355X, graph-replayed: k/v 5.3 -> 3.1 us, o 6.3 -> 4.4).
 static NarrowGeom narrow_geom(int M, int K, int N, bool gated) {
     static const int opts[] = {8, 6, 4, 3, 2, 1};
+    static const int opts16[] = {24, 16, 8};
     const int nj = gated ? 2 : 1;
-    const long ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
     const int auto_mt = stream_mt(M);
-    NarrowGeom best{0, 0, 0, 0};
+    NarrowGeom best{0, 0, 0, 0, 0};
     long best_blocks = 0, best_cost = 0;
-    for (int mt = auto_mt; mt >= 1; mt /= 2) {
+    auto consider = [&](int mt, int kpw, int ncol) {
+        const long ncb = (N + ncol - 1) / ncol;
         const int slabs = (M + 16 * mt - 1) / (16 * mt);
         const long tiles = ncb * slabs;
-        if (tiles > NARROW_CNT) continue;
-        for (int kpw : opts) {
-            if (kpw > narrow_kmax(mt, gated) || K % (128 * kpw)) continue;
-            const int ks = K / (128 * kpw);
-            const long blocks = tiles * ks;
-            const long ksl = 128L * kpw, rows = 16L * mt;
-            const long cost = rows * ksl * 4 + nj * NARROW_COLS * ksl * 2 +
-                              (ks > 1 ? 2L * ks * rows * NARROW_COLS * 4 * nj : 0);
-            // one round: blocks <= CUs, else (nothing fits) the fewest blocks
-            const bool fits = blocks <= g_cus, best_fits = best_blocks <= g_cus;
-            bool take;
-            if (!best.kpw) take = true;
-            else if (fits != best_fits) take = fits;
-            else if (!fits) take = blocks < best_blocks;
-            // above 64 rows, one slice (no slice sums, no tickets) once it
-            // gives at least half the CUs a block (measured on MI355X, 96 x
-            // 1024 x 1024: 6.4 us on 256 blocks of 4 slices, 4.0 on 192 of one)
-            else if (M > 64 && (ks == 1 && 2 * blocks >= g_cus) != (best.ks == 1 && 2 * best_blocks >= g_cus))
-                take = ks == 1 && 2 * blocks >= g_cus;
-            else if (blocks != best_blocks) take = blocks > best_blocks;
-            else if ((ks == 1) != (best.ks == 1)) take = ks == 1;
-            else take = cost < best_cost;
-            if (take) {
-                best = NarrowGeom{mt, slabs, kpw, ks};
-                best_blocks = blocks;
-                best_cost = cost;
-            }
+        if (tiles > NARROW_CNT || K % (128 * kpw)) return;
+        const int ks = K / (128 * kpw);
+        const long blocks = tiles * ks;
+        const long ksl = 128L * kpw, rows = 16L * mt;
+        const long cost = rows * ksl * 4 + nj * ncol * ksl * 2 + (ks > 1 ? 2L * ks * rows * ncol * 4 * nj : 0);
+        // one round: blocks <= CUs, else (nothing fits) the fewest blocks
+        const bool fits = blocks <= g_cus, best_fits = best_blocks <= g_cus;
+        bool take;
+        if (!best.kpw) take = true;
+        else if (fits != best_fits) take = fits;
+        else if (!fits) take = blocks < best_blocks;
+        // one slice (no slice sums, no tickets) once it gives at least half
+        // the CUs a block (measured on MI355X, 96 x 1024 x 1024: 6.4 us on
+        // 256 blocks of 4 slices, 4.0 on 192 of one)
+        else if ((ks == 1 && 2 * blocks >= g_cus) != (best.ks == 1 && 2 * best_blocks >= g_cus))
+            take = ks == 1 && 2 * blocks >= g_cus;
+        else if (blocks != best_blocks) take = blocks > best_blocks;
+        else if ((ks == 1) != (best.ks == 1)) take = ks == 1;
+        else take = cost < best_cost;
+        if (take) {
+            best = NarrowGeom{mt, slabs, kpw, ks, ncol};
+            best_blocks = blocks;
+            best_cost = cost;
         }
-    }
+    };
+    for (int mt = auto_mt; mt >= 1; mt /= 2)
+        for (int kpw : opts)
+            if (kpw <= narrow_kmax(mt, gated)) consider(mt, kpw, NARROW_COLS);
+    if (!gated)
+        for (int kpw : opts16) consider(1, kpw, 16);
     return best;
 }
 static inline size_t narrow_part_bytes(const NarrowGeom &g, int M, int N, bool gated) {
     return g.ks > 1 ? (size_t)g.ks * (gated ? 2 : 1) * M * N * sizeof(float) : 0;
 }
-// the instantiated (mt, kpw, gated) combinations: loads in flight within 64
-template <int MT, int KPW, bool GATED>
-constexpr bool narrow_ok() { return 2 * MT * KPW + 2 * (GATED ? 2 : 1) * KPW <= 64; }
+// the instantiated (mt, kpw, gated, ncol) combinations: loads in flight
+// within 64 (the 16-wide blocks' A in two halves past 48)
+template <int MT, int KPW, bool GATED, int NCOL>
+constexpr bool narrow_ok() {
+    return NCOL == 16 ? (MT == 1 && !GATED && KPW % 8 == 0 && KPW <= 24)
+                      : 2 * MT * KPW + 2 * (GATED ? 2 : 1) * KPW <= 64;
+}
 
-template <int MT, int KPW, bool GATED>
+template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS>
 static int launch_narrow_t(const Ws &ws, const NarrowGeom &g, float *c, const float *a, const uint16_t *b,
                            const uint16_t *b2, int M, int K, int N) {
-    if constexpr (!narrow_ok<MT, KPW, GATED>()) {
+    if constexpr (!narrow_ok<MT, KPW, GATED, NCOL>()) {
         return QH_EINVAL;
     } else {
-        const int ncb = (N + NARROW_COLS - 1) / NARROW_COLS;
+        const int ncb = (N + NCOL - 1) / NCOL;
         float *part = nullptr;
         if (g.ks > 1) {
             if (narrow_part_bytes(g, M, N, GATED) > ws.part_bytes || !ws.cnt) return QH_ETOOBIG;
             part = use_part(ws);
         }
-        hipLaunchKernelGGL((k_gemm_narrow<MT, KPW, GATED>), dim3((unsigned)g.ks, (unsigned)ncb, (unsigned)g.slabs),
+        hipLaunchKernelGGL((k_gemm_narrow<MT, KPW, GATED, NCOL>), dim3((unsigned)g.ks, (unsigned)ncb, (unsigned)g.slabs),
                            dim3(NTHREADS), 0, g_stream, c, part, ws.cnt, a, b, b2, M, K, N);
         HCHECK(hipGetLastError(), QH_ELAUNCH);
         return QH_OK;
@@ -3786,6 +3814,14 @@ template <bool GATED>
 static int launch_narrow(const Ws &ws, float *c, const float *a, const uint16_t *b, const uint16_t *b2,
                          int M, int K, int N) {
     const NarrowGeom g = narrow_geom(M, K, N, GATED);
+    if (g.ncol == 16) {
+        switch (g.kpw) {
+            case 8: return launch_narrow_t<1, 8, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
+            case 16: return launch_narrow_t<1, 16, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
+            case 24: return launch_narrow_t<1, 24, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
+            default: return QH_EINVAL;
+        }
+    }
 #define QH_NARROW_CASES(MT)                                                                  \
     switch (g.kpw) {                                                                         \
         case 1: return launch_narrow_t<MT, 1, GATED>(ws, g, c, a, b, b2, M, K, N);           \
@@ -4034,7 +4070,7 @@ static int resolve_plan(Ws &ws, int M, int K, int N, bool gated, bool vec, bool 
     if (plan == PLAN_M16 && (!m16_fits(M, K, N) || (gated && K > 2048))) plan = PLAN_T64x64;
     if (is_narrow_plan(plan)) {
         // the slice sums need room in the workspace
-        const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(M, K, N, gated) : NarrowGeom{0, 0, 0, 0};
+        const NarrowGeom g = narrow_fits(M, K, N) ? narrow_geom(M, K, N, gated) : NarrowGeom{0, 0, 0, 0, 0};
         if (g.kpw <= 0) {
             plan = PLAN_T64x64;
         } else {
