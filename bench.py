@@ -644,12 +644,34 @@ PROFILE_NAMES = {"qkv_gemv": "k_gemv1<1, 2, false, false, false>", "o_gemv": "k_
 DECODE_PROFILE = "decode_gemv_set_kernel_trace.txt"
 
 
+def kernel_sources_digest():
+    """sha256 over the library's GPU sources (csrc/*.hip and hip_shim.h, by
+    name): a committed profile records the digest of the sources it was
+    made from, so a profile of other kernels is not taken for these"""
+    import glob
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "n550_qwen3_bringup_handover_amd", "csrc")
+    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + [os.path.join(csrc, "hip_shim.h")]):
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
 def read_profile_us(kernel):
     """average duration (us) of a kernel class in the committed rocprofv3
-    --kernel-trace --stats summary of the decode set, if any"""
+    --kernel-trace --stats summary of the decode set, if there is one and it
+    was made from the current kernel sources (its '# sources:' digest)"""
     path = os.path.join(ROOT, "profiles", DECODE_PROFILE)
     sig = PROFILE_NAMES.get(kernel)
     if not sig or not os.path.exists(path):
+        return None
+    digest = None
+    for line in open(path):
+        if line.startswith("# sources:"):
+            digest = line.split(":", 1)[1].split()[0]
+    if digest != kernel_sources_digest():
         return None
     for line in open(path):
         if line.startswith("#"):
@@ -777,10 +799,12 @@ def main():
                     "traffic": read_traffic(dom), "bytes_per_launch": nb,
                     "us_per_launch_profile": prof_us,
                     "profile": f"profiles/{DECODE_PROFILE}" if prof_us else None,
+                    "profile_sources_sha256": kernel_sources_digest()[:16] if prof_us else None,
                     "us_per_launch_graph_replay": round(d["us_per_launch"], 3),
                     "frac_graph_replay": round(d["hbm_frac"], 4),
-                    "method": "frac = bytes_per_launch / rocprofv3 average duration / peak; "
-                              "frac_graph_replay = bytes_per_launch / graph-replay launch period / peak"}
+                    "method": "frac = bytes_per_launch / rocprofv3 average duration / peak, from the committed "
+                              "profile when it was made from these kernel sources (sha256 of csrc/*.hip), else "
+                              "frac = frac_graph_replay = bytes_per_launch / graph-replay launch period / peak"}
     gemms = None if (args.no_extras or args.no_gemm_tables) else gemm_tables(g)
     if args.calibrate_copy:
         # a kernel of known traffic (64 MiB read + 64 MiB written per launch)
