@@ -1196,7 +1196,7 @@ __global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__res
                 if (col < N) {
 #pragma unroll
                     for (int r = 0; r < 4; r++)
-                        if (rbase + r < M) c[(size_t)(rbase + r) * N + col] = acc[i][j][r];
+                        if (rbase + r < M) __builtin_nontemporal_store(acc[i][j][r], &c[(size_t)(rbase + r) * N + col]);
                 }
             }
         } else {
@@ -1208,7 +1208,8 @@ __global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__res
 #pragma unroll
                     for (int r = 0; r < 4; r++)
                         if (rbase + r < M)
-                            c[(size_t)(rbase + r) * N + col] = silu_mul(acc[i][j][r], acc[i][j + TNO][r]);
+                            __builtin_nontemporal_store(silu_mul(acc[i][j][r], acc[i][j + TNO][r]),
+                                                        &c[(size_t)(rbase + r) * N + col]);
                 }
             }
         }
@@ -1632,7 +1633,7 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN) * KG, WMW * xl_wn(BM, BN) 
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
                         const int row = rbase + 8 * (v >> 2) + (v & 3);
-                        if (row < M) c[(size_t)row * N + col] = acc[i][j][v];
+                        if (row < M) __builtin_nontemporal_store(acc[i][j][v], &c[(size_t)row * N + col]);
                     }
                 }
             }
@@ -1645,7 +1646,9 @@ __global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN) * KG, WMW * xl_wn(BM, BN) 
 #pragma unroll
                     for (int v = 0; v < 16; v++) {
                         const int row = rbase + 8 * (v >> 2) + (v & 3);
-                        if (row < M) c[(size_t)row * N + col] = silu_mul(acc[i][j][v], acc[i][j + TNO][v]);
+                        if (row < M)
+                            __builtin_nontemporal_store(silu_mul(acc[i][j][v], acc[i][j + TNO][v]),
+                                                        &c[(size_t)row * N + col]);
                     }
                 }
             }
