@@ -644,15 +644,21 @@ PROFILE_NAMES = {"qkv_gemv": "k_gemv1<1, 2, false, false, false>", "o_gemv": "k_
 DECODE_PROFILE = "decode_gemv_set_kernel_trace.txt"
 
 
+# the headers hip_gemm.hip includes (its kernel families)
+GEMM_KERNEL_HEADERS = ("gemm_common.h", "gemv_kernels.h", "tile_kernels.h", "misc_kernels.h", "small_m_kernels.h")
+
+
 def kernel_sources_digest():
-    """sha256 over the library's GPU sources (csrc/*.hip and hip_shim.h, by
-    name): a committed profile records the digest of the sources it was
-    made from, so a profile of other kernels is not taken for these"""
+    """sha256 over the library's GPU sources (csrc/*.hip, hip_shim.h and the
+    kernel headers hip_gemm.hip compiles, by name): a committed profile
+    records the digest of the sources it was made from, so a profile of
+    other kernels is not taken for these"""
     import glob
     import hashlib
     h = hashlib.sha256()
     csrc = os.path.join(ROOT, "n550_qwen3_bringup_handover_amd", "csrc")
-    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + [os.path.join(csrc, "hip_shim.h")]):
+    headers = ["hip_shim.h"] + list(GEMM_KERNEL_HEADERS)
+    for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + [os.path.join(csrc, n) for n in headers]):
         h.update(os.path.basename(path).encode())
         with open(path, "rb") as f:
             h.update(f.read())

@@ -1,2736 +1,26 @@
-// CDNA4 (gfx950) kernels for the Qwen3-0.6B projection GEMMs and the shim
-// functions that launch them.  Semantics follow the reference GEMM plug-in
+// CDNA4 (gfx950) GEMM / GEMV library for the Qwen3-0.6B projection GEMMs:
+// the host side of the shim (device and stream, workspaces, the plan table
+// that picks a kernel per M x K x N, the launchers, graph capture) and the
+// extern "C" entry points.  Semantics follow the reference GEMM plug-in
 // (fpga_bringup/src/src/kernels.h:44-57): C[M,N] = A[M,K] . B[N,K]^T with A
 // fp32 row-major, B bf16 bits row-major [out, in], C fp32 row-major,
 // C overwritten.  A is rounded to bf16 with round-to-nearest-even on the
 // load path (the AME kernel does the same, kernels_ame.c:219-236), products
 // of two bf16 values are exact in fp32, and accumulation is fp32.
 //
-// Kernels:
-//   k_gemv<MR,ROWS,CU>   M <= 4: streams B once with 128-bit non-temporal
-//                        loads; A staged in LDS; a transposing wave
-//                        reduction of ROWS*MR partial sums per lane.
-//   k_gemm<...>          M > 4: 256-thread workgroups, 4 waves, bf16 MFMA
-//                        16x16x32 with fp32 accumulate, A/B tiles staged
-//                        through XOR-swizzled LDS, double-buffered; optional
-//                        gated epilogue h = silu(gate) * up.
-//   k_tile_to_row        weight re-layout for the tile-major blob format.
-//   k_argmax_*           first-max reduction for greedy decoding.
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-#include <stdlib.h>
-#include <string.h>
-
-#include "hip_shim.h"
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-#define WAVE 64
-#define NTHREADS 256
-
-// ---------------------------------------------------------------------------
-// bf16 helpers
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
-
-// two fp32 -> packed bf16 pair (low half = first), RNE: one v_cvt_pk_bf16_f32
-__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
-    typedef float f32x2_t __attribute__((ext_vector_type(2)));
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    const f32x2_t f = {x, y};
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-}
-__device__ __forceinline__ float round_bf16(float x) {
-    return __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) << 16);
-}
-
-// raw buffer resource over [p, p + bytes): stride 0, num_records = bytes.  A
-// load at an offset past num_records returns zeros and reads no memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
-}
-#define BUF_OOB 0x80000000u      // an offset past every buffer below 2 GiB
-#define AUX_SC1 16               // buffer-op cache policy: agent scope, coherent across the XCDs' L2s
-
-// w.lo * x.lo + w.hi * x.hi + acc for two packed bf16 pairs (v_dot2_f32_bf16)
-__device__ __forceinline__ float bf16_dot2(uint32_t w, uint32_t x, float acc) {
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), acc,
-                                           false);
-}
-
-// Sum over the 64 lanes of a wave, the same bits in every lane.  Each step
-// adds a lane's value and its partner's, so both partners hold the same sum:
-// DPP within rows of 16 lanes (quad permutes for xor 1 and xor 2, then the
-// half-row mirror and the row mirror, which pair groups that already hold
-// equal sums), then the gfx950 permlane swaps across rows (xor 16, xor 32).
-// All VALU: no LDS round trip.
-template <int CTRL>
-__device__ __forceinline__ float dpp_partner(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float wave_sum(float x) {
-    x += dpp_partner<0xB1>(x);      // quad_perm [1,0,3,2]
-    x += dpp_partner<0x4E>(x);      // quad_perm [2,3,0,1]
-    x += dpp_partner<0x141>(x);     // row_half_mirror
-    x += dpp_partner<0x140>(x);     // row_mirror
-    const auto p16 = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
-    x = __builtin_bit_cast(float, (int)p16[0]) + __builtin_bit_cast(float, (int)p16[1]);
-    const auto p32 = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
-    return __builtin_bit_cast(float, (int)p32[0]) + __builtin_bit_cast(float, (int)p32[1]);
-}
-
-__device__ __forceinline__ float silu_mul(float g, float u) {
-    // reference: (g / (1 + expf(-g))) * u  (ops_scalar.c:46-51)
-    return (g / (1.0f + expf(-g))) * u;
-}
-
-// ---------------------------------------------------------------------------
-// GEMV: M <= 4
-// ---------------------------------------------------------------------------
-// One halving step per template level, so that every index below is a
-// constant (a loop over a run-time `half` would index v dynamically).
-template <int HALF, int MASK>
-__device__ __forceinline__ void wave_halving_steps(float *v, int lane) {
-    if constexpr (HALF >= 1) {
-        const bool hi = (lane & MASK) != 0;
-#pragma unroll
-        for (int i = 0; i < HALF; i++) {
-            const float send = hi ? v[i] : v[i + HALF];
-            const float keep = hi ? v[i + HALF] : v[i];
-            v[i] = keep + __shfl_xor(send, MASK);
-        }
-        wave_halving_steps<HALF / 2, MASK / 2>(v, lane);
-    }
-}
-// After this, lane l holds the 64-lane total of value index l >> (6 - log2 V).
-// Each halving step trades half of the values with the partner lane, so a
-// lane ends up owning one value after log2(V) exchanges instead of V*6.
-template <int V>
-__device__ __forceinline__ float wave_transpose_reduce(float (&v)[V], int lane) {
-    static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of 2 <= 64");
-    wave_halving_steps<V / 2, 32>(v, lane);
-    constexpr int L = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
-    float x = v[0];
-#pragma unroll
-    for (int mask = 32 >> L; mask >= 1; mask >>= 1) x += __shfl_xor(x, mask);
-    return x;
-}
-
-template <int X> struct pow2_ceil { static constexpr int v = (X <= 1) ? 1 : 2 * pow2_ceil<(X + 1) / 2>::v; };
-template <> struct pow2_ceil<1> { static constexpr int v = 1; };
-
-// grid.x = ceil(N / (4 * ROWS)); block = 256 (4 waves); dynamic LDS = MR*K*4.
-// Requires K % 8 == 0 and 16-byte aligned a and b.  Rows >= N are clamped
-// for loading and never stored.
-template <int MR, int ROWS, int CU>
-__global__ __launch_bounds__(NTHREADS) void k_gemv(float *__restrict__ c,
-                                                  const float *__restrict__ a,
-                                                  const uint16_t *__restrict__ b,
-                                                  int K, int N) {
-    extern __shared__ float sA[];   // [MR][K], rounded to bf16
-    const int tid = threadIdx.x;
-    {
-        const f32x4 *a4 = reinterpret_cast<const f32x4 *>(a);
-        f32x4 *s4 = reinterpret_cast<f32x4 *>(sA);
-        const int n4 = (MR * K) >> 2;
-        for (int i = tid; i < n4; i += NTHREADS) {
-            f32x4 v = a4[i];
-            v.x = round_bf16(v.x); v.y = round_bf16(v.y);
-            v.z = round_bf16(v.z); v.w = round_bf16(v.w);
-            s4[i] = v;
-        }
-    }
-    __syncthreads();
-
-    const int wave = tid >> 6, lane = tid & 63;
-    const int row0 = (blockIdx.x * 4 + wave) * ROWS;
-    if (row0 >= N) return;             // no barrier below this point
-    const int nch = K >> 3;            // 16-byte chunks per row
-    const u32x4 *b4 = reinterpret_cast<const u32x4 *>(b);
-
-    constexpr int V = pow2_ceil<MR * ROWS>::v;
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; i++) acc[i] = 0.0f;
-
-    for (int c0 = lane; c0 < nch; c0 += WAVE * CU) {
-        u32x4 bv[CU][ROWS];
-#pragma unroll
-        for (int u = 0; u < CU; u++) {
-            const int ch = c0 + WAVE * u;
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) {
-                const int row = min(row0 + r, N - 1);
-                if (ch < nch)
-                    bv[u][r] = __builtin_nontemporal_load(b4 + (size_t)row * nch + ch);
-                else
-                    bv[u][r] = u32x4{0u, 0u, 0u, 0u};
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < CU; u++) {
-            const int ch = c0 + WAVE * u;
-            if (ch < nch) {
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    const f32x4 *ap = reinterpret_cast<const f32x4 *>(sA + m * K + ch * 8);
-                    const f32x4 x0 = ap[0], x1 = ap[1];
-                    const float av[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                    for (int r = 0; r < ROWS; r++) {
-                        float s = acc[m * ROWS + r];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            s = fmaf(av[2 * e], bf16_lo(bv[u][r][e]), s);
-                            s = fmaf(av[2 * e + 1], bf16_hi(bv[u][r][e]), s);
-                        }
-                        acc[m * ROWS + r] = s;
-                    }
-                }
-            }
-        }
-    }
-
-    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
-    const float tot = wave_transpose_reduce<V>(acc, lane);
-    const int idx = lane >> (6 - LV);
-    if ((lane & ((64 >> LV) - 1)) == 0) {
-        const int m = idx / ROWS, r = idx % ROWS;
-        if (m < MR && row0 + r < N) c[(size_t)m * N + row0 + r] = tot;
-    }
-}
-
-// GEMV-shaped GEMM for 5 <= M <= MR (8 or 16) and K <= 512 * CPL: every
-// weight row is read once, with each load instruction covering 1 KB of one
-// row (lane l owns the 16-byte chunks l, l + 64, ... of every row), and the
-// M rows of A are applied to it from registers with v_dot2_f32_bf16.  The
-// block's NWV waves first load A once between them (fp32, from L2) and
-// round it to bf16 into LDS, then every wave issues its ROWS * CPL weight
-// loads, and A is passed to the lanes while the weights are in flight: a
-// launch costs one HBM round trip.  The ROWS * MR sums of a wave are reduced
-// across its lanes by halving exchanges, one value per lane at the end.
-// Rows of A past M are zeros; weight rows past N read zeros and are not
-// stored.  Dynamic LDS: MR * K * 2 bytes.
-template <int MR, int ROWS, int CPL, int NWV>
-__global__ __launch_bounds__(NWV * WAVE) void k_gemv_m(float *__restrict__ c, const float *__restrict__ a,
-                                                      const uint16_t *__restrict__ b, int M, int K, int N) {
-    constexpr int NT = NWV * WAVE;                    // threads per block
-    extern __shared__ u32x4 sa_m[];                   // [MR][K / 8] bf16 chunks
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nch = K >> 3;
-    const int row0 = (blockIdx.x * NWV + wave) * ROWS;
-
-    // 1. A -> registers (fp32, from L2): MR rows of nch chunks over the block
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * K * 4);
-    constexpr int AQ = (MR * WAVE * CPL + NT - 1) / NT;  // chunks per thread at K = 512 CPL
-    u32x4 alo[AQ], ahi[AQ];
-#pragma unroll
-    for (int i = 0; i < AQ; i++) {
-        const int q = tid + NT * i;
-        const int m = q / nch, ch = q - m * nch;
-        const bool ok = q < MR * nch && m < M;
-        const uint32_t off = ((uint32_t)m * K + 8 * ch) * 4u;   // M * K * 4 < 2^31
-        alo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off : BUF_OOB, 0, 0);
-        ahi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off + 16u : BUF_OOB, 0, 0);
-    }
-    // 2. this wave's weights: rows row0 + r, chunks lane + 64 j (non-temporal)
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
-    u32x4 bw[ROWS][CPL];
-#pragma unroll
-    for (int r = 0; r < ROWS; r++)
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            const bool ok = row0 + r < N && ch < nch;
-            const uint32_t off = ((uint32_t)(row0 + r) * K + 8 * ch) * 2u;   // N * K * 2 < 2^31
-            bw[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? off : BUF_OOB, 0, 2);
-        }
-    __builtin_amdgcn_sched_barrier(0);
-    // 3. A rounded to bf16 (RNE) into LDS while the weights are in flight
-#pragma unroll
-    for (int i = 0; i < AQ; i++) {
-        const int q = tid + NT * i;
-        u32x4 v;
-        v.x = pack_bf16x2(__uint_as_float(alo[i].x), __uint_as_float(alo[i].y));
-        v.y = pack_bf16x2(__uint_as_float(alo[i].z), __uint_as_float(alo[i].w));
-        v.z = pack_bf16x2(__uint_as_float(ahi[i].x), __uint_as_float(ahi[i].y));
-        v.w = pack_bf16x2(__uint_as_float(ahi[i].z), __uint_as_float(ahi[i].w));
-        if (q < MR * nch) sa_m[q] = v;
-    }
-    __syncthreads();
-    // 4. sums: acc[r * MR + m] over this lane's chunks
-    constexpr int V = pow2_ceil<ROWS * MR>::v;
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; i++) acc[i] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; j++) {
-        // chunks past K: the weights read zeros, so any A chunk will do
-        const int ch = min(lane + WAVE * j, nch - 1);
-#pragma unroll
-        for (int m = 0; m < MR; m++) {
-            const u32x4 x = sa_m[m * nch + ch];
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) {
-                float t = acc[r * MR + m];
-                t = bf16_dot2(bw[r][j].x, x.x, t);
-                t = bf16_dot2(bw[r][j].y, x.y, t);
-                t = bf16_dot2(bw[r][j].z, x.z, t);
-                t = bf16_dot2(bw[r][j].w, x.w, t);
-                acc[r * MR + m] = t;
-            }
-        }
-    }
-    // 5. reduce over the lanes; value index r * MR + m ends in lane group idx
-    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
-    const float tot = wave_transpose_reduce<V>(acc, lane);
-    const int idx = lane >> (6 - LV);
-    if ((lane & ((64 >> LV) - 1)) == 0 && idx < ROWS * MR) {
-        const int r = idx / MR, m = idx % MR;
-        if (m < M && row0 + r < N) c[(size_t)m * N + row0 + r] = tot;
-    }
-}
-
-__device__ const int k_zero_token = 0;     // token read by prologues without an embedding
-
-// Activation prologue of the M = 1 GEMV (decode): the GEMV input is
-//   a = rmsnorm(x + r) * nw       (fpga_bringup/src/src/ops_scalar.c:11-16,
-//                                  residual add ops_scalar.c:53-55)
-// where x is either an fp32 row or, when emb is set, the bf16 embedding row
-// emb[*tok] (qwen3.c:295-298).  Block 0 stores x + r to x_out when x_out is
-// set (the updated residual stream).
-struct GemvPro {
-    const float *x;
-    const uint16_t *emb;
-    const int *tok;
-    int emb_rows;
-    const float *r;
-    const uint16_t *nw;
-    float *x_out;
-    float eps;
-};
-
-// M = 1 fast path (decode).  One wave owns ROWS output rows; lane l owns the
-// 16-byte chunks l, l+64, ..., l+64*(CPL-1) of every row (CPL = chunks per
-// lane, K <= 512*CPL).  The block's 256 threads first load the activation
-// row once between them (a quarter per wave, 16 B per thread per 4 KB of
-// row), then every wave issues all of its ROWS*CPL non-temporal weight
-// loads; the activation (rounded to bf16, and for PRO normalised first) is
-// exchanged through LDS while the weights are still in flight, so a launch
-// costs one HBM round trip and each block reads the activation from L2
-// once instead of once per wave.  GATED: rows of Wg and Wu with the same
-// index are both loaded and the epilogue writes silu(gate) * up.  PRO: the
-// activation row comes from the GemvPro prologue instead of a.
-// Dynamic LDS: (K + 8) floats.  Waves without rows still take part in the
-// barriers.
-// MERGE: a holds split attention partials (qh_gemv_merge) and the activation
-// row is their softmax merge; their loads go out before the weight loads,
-// the merge arithmetic after them.
-// KA: the activation row arrives already rounded to packed bf16 pairs in the
-// kernel arguments (ka: the kernel-argument segment, GemvKaRow first) -- the
-// host-pointer path's M = 1 calls with K <= 1024, which then need no copy of
-// A to the device before the GEMV.
-template <int ROWS, int CPL, bool GATED, bool PRO, bool MERGE, bool KA>
-__device__ __forceinline__ void gemv1_body(float *__restrict__ c, const float *__restrict__ a,
-                                           const uint16_t *__restrict__ b, const uint16_t *__restrict__ b2,
-                                           int K, int N, GemvPro pro, const uint2 *__restrict__ ka) {
-    constexpr int NB = GATED ? 2 * ROWS : ROWS;     // weight rows per wave
-    constexpr int NQ = CPL * 2 * WAVE;               // 4-element groups of the padded row (512*CPL)
-    constexpr int QMAX = (NQ + NTHREADS - 1) / NTHREADS;
-    extern __shared__ __align__(16) uint32_t sx[];   // [2*NQ] bf16 pairs of the padded row, then [4] floats
-    float *sred = reinterpret_cast<float *>(sx + 2 * NQ);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int row0 = (blockIdx.x * (NTHREADS / WAVE) + wave) * ROWS;
-    // MERGE is launched for K = 2048 only (the 16 x 128 attention output),
-    // whose 512 groups the 256 threads cover exactly: its merge has no tail
-    static_assert(!MERGE || (CPL == 4 && QMAX == 2), "MERGE expects K = 2048");
-    const int nch = K >> 3, nq = K >> 2;
-
-    // 1. this thread's share of the activation row (issued before the
-    //    weights; groups past K read zeros)
-    f32x4 xa[QMAX];
-    uint2 wn[QMAX];
-    f32x4 xv[PRO ? QMAX : 1], rv[PRO ? QMAX : 1];    // prologue sources (x, r, embedding row)
-    uint2 e[PRO ? QMAX : 1];
-    constexpr int MS = MERGE ? QH_ATT_SPLITS : 1;
-    f32x4 mo[MERGE ? QMAX : 1][MS];
-    float2 mml[MERGE ? QMAX : 1][MS];
-    // Scheduling barriers keep the activation-side loads ahead of the weight
-    // loads and their arithmetic behind them, so a wave waits for the
-    // activation alone before its LDS store.
-    if constexpr (MERGE) {
-        // group i = dims 4i .. 4i+3 of the 2048-vector: head i/32 (kv head
-        // i/64, query head (i/32)&1 of the group), d4 = i%32
-        const __amdgpu_buffer_rsrc_t rp = buf_rsrc(a, (size_t)8 * QH_ATT_SPLITS * 2 * QH_ATT_PART * 4);
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int ii = tid + NTHREADS * q;       // < 512 = nq: no tail for K = 2048
-            const uint32_t pb = (uint32_t)(((ii >> 6) * QH_ATT_SPLITS * 2 + ((ii >> 5) & 1)) * QH_ATT_PART) * 4u;
-#pragma unroll
-            for (int s = 0; s < MS; s++) {
-                const uint32_t ps = pb + (uint32_t)(s * 2 * QH_ATT_PART) * 4u;
-                mml[q][s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rp, ps, 0, 0));
-                mo[q][s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                         rp, ps + 16u + (uint32_t)(ii & 31) * 16u, 0, 0));
-            }
-        }
-    } else if constexpr (KA) {
-        // nothing to load ahead: the row is in the kernel arguments
-    } else if constexpr (!PRO) {
-        const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)K * 4);
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            xa[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                  ra, i < nq ? (uint32_t)i * 16 : BUF_OOB, 0, 0));
-        }
-    } else {
-        // x + r, or the embedding row of the device-held token: every source
-        // is loaded, absent ones from empty buffers, which read as zeros, so
-        // the prologue has no branch
-        const bool emb = pro.emb != nullptr;
-        int t = *(emb ? pro.tok : &k_zero_token);
-        t = t < 0 ? 0 : (t >= pro.emb_rows ? pro.emb_rows - 1 : t);
-        const __amdgpu_buffer_rsrc_t re = buf_rsrc(emb ? pro.emb + (size_t)t * K : nullptr, emb ? (size_t)K * 2 : 0);
-        const __amdgpu_buffer_rsrc_t rx = buf_rsrc(pro.x, (pro.x && !emb) ? (size_t)K * 4 : 0);
-        const __amdgpu_buffer_rsrc_t rr = buf_rsrc(pro.r, (pro.r && !emb) ? (size_t)K * 4 : 0);
-        const __amdgpu_buffer_rsrc_t rw = buf_rsrc(pro.nw, (size_t)K * 2);
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            const uint32_t o16 = i < nq ? (uint32_t)i * 16 : BUF_OOB, o8 = i < nq ? (uint32_t)i * 8 : BUF_OOB;
-            xv[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, o16, 0, 0));
-            rv[q] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rr, o16, 0, 0));
-            e[q] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(re, o8, 0, 0));
-            wn[q] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rw, o8, 0, 0));
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);               // the activation loads go out first
-
-    // 2. all weight loads of this wave; rows past N and chunks past K read
-    //    zeros (the caller keeps N*K*2 below 2 GiB)
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
-    u32x4 bv[NB][CPL];
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-        const int row = row0 + r;
-#pragma unroll
-        for (int j = 0; j < CPL; j++) {
-            const int ch = lane + WAVE * j;
-            const uint32_t off = (row < N && ch < nch) ? (uint32_t)row * (uint32_t)K * 2u + (uint32_t)ch * 16u
-                                                       : BUF_OOB;
-            bv[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);      // nt: read once
-            if constexpr (GATED) bv[ROWS + r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);               // ... then every weight load
-
-    // 3. activation through LDS as bf16 (RNE), normalised first for PRO;
-    //    zeros past K
-    uint2 *sx2 = reinterpret_cast<uint2 *>(sx);
-    if constexpr (KA) {
-        // the host rounded the row and zeroed it past K
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            if (NQ % NTHREADS == 0 || i < NQ) sx2[i] = ka[i];
-        }
-    } else if constexpr (PRO) {
-#pragma unroll
-        for (int q = 0; q < QMAX; q++)
-            xa[q] = f32x4{bf16_lo(e[q].x), bf16_hi(e[q].x), bf16_lo(e[q].y), bf16_hi(e[q].y)} + (xv[q] + rv[q]);
-        float ss = 0.0f;
-#pragma unroll
-        for (int q = 0; q < QMAX; q++)
-            ss += xa[q].x * xa[q].x + xa[q].y * xa[q].y + xa[q].z * xa[q].z + xa[q].w * xa[q].w;
-        ss = wave_sum(ss);
-        if (lane == 0) sred[wave] = ss;
-        if (pro.x_out && blockIdx.x == 0) {
-#pragma unroll
-            for (int q = 0; q < QMAX; q++) {
-                const int i = tid + NTHREADS * q;
-                if (i < nq) reinterpret_cast<f32x4 *>(pro.x_out)[i] = xa[q];
-            }
-        }
-        __syncthreads();
-        ss = (sred[0] + sred[1]) + (sred[2] + sred[3]);
-        const float scale = 1.0f / sqrtf(ss / (float)K + pro.eps);
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            if (NQ % NTHREADS == 0 || i < NQ)
-                sx2[i] = uint2{pack_bf16x2((xa[q].x * scale) * bf16_lo(wn[q].x), (xa[q].y * scale) * bf16_hi(wn[q].x)),
-                               pack_bf16x2((xa[q].z * scale) * bf16_lo(wn[q].y), (xa[q].w * scale) * bf16_hi(wn[q].y))};
-        }
-    } else {
-        if constexpr (MERGE) {
-#pragma unroll
-            for (int q = 0; q < QMAX; q++) {
-                float mx = mml[q][0].x;
-#pragma unroll
-                for (int s = 1; s < MS; s++) mx = fmaxf(mx, mml[q][s].x);
-                float den = 0.0f;
-                f32x4 num = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s = 0; s < MS; s++) {
-                    const float w = mml[q][s].x == -INFINITY ? 0.0f : expf(mml[q][s].x - mx);
-                    den = fmaf(w, mml[q][s].y, den);
-                    num.x = fmaf(w, mo[q][s].x, num.x);
-                    num.y = fmaf(w, mo[q][s].y, num.y);
-                    num.z = fmaf(w, mo[q][s].z, num.z);
-                    num.w = fmaf(w, mo[q][s].w, num.w);
-                }
-                const float inv = 1.0f / den;
-                xa[q] = num * inv;
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < QMAX; q++) {
-            const int i = tid + NTHREADS * q;
-            if (NQ % NTHREADS == 0 || i < NQ)
-                sx2[i] = uint2{pack_bf16x2(xa[q].x, xa[q].y), pack_bf16x2(xa[q].z, xa[q].w)};
-        }
-    }
-    __syncthreads();
-
-    // 4. this lane's activation chunks, then packed bf16 dot products
-    u32x4 xc[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; j++) xc[j] = reinterpret_cast<const u32x4 *>(sx)[lane + WAVE * j];
-    float acc[NB];
-#pragma unroll
-    for (int r = 0; r < NB; r++) {
-        float s = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; j++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) s = bf16_dot2(bv[r][j][e], xc[j][e], s);
-        acc[r] = s;
-    }
-
-    // 5. wave sums (every lane holds every row's total); lane r stores row r
-    float tot = 0.0f, up = 0.0f;
-#pragma unroll
-    for (int r = 0; r < ROWS; r++) {
-        const float t = wave_sum(acc[r]);
-        tot = lane == r ? t : tot;
-        if constexpr (GATED) {
-            const float u = wave_sum(acc[ROWS + r]);
-            up = lane == r ? u : up;
-        }
-    }
-    if (lane < ROWS && row0 + lane < N) c[row0 + lane] = GATED ? silu_mul(tot, up) : tot;
-}
-
-template <int ROWS, int CPL, bool GATED, bool PRO = false, bool MERGE = false>
-__global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
-                                                   const float *__restrict__ a,
-                                                   const uint16_t *__restrict__ b,
-                                                   const uint16_t *__restrict__ b2,
-                                                   int K, int N, GemvPro pro) {
-    gemv1_body<ROWS, CPL, GATED, PRO, MERGE, false>(c, a, b, b2, K, N, pro, nullptr);
-}
-
-// the activation row of a KA launch: K <= 1024 bf16 values, zero past K
-// (first kernel argument, so it sits at offset 0 of the argument segment)
-struct GemvKaRow {
-    uint32_t w[512];
-};
-template <int ROWS, int CPL, bool GATED>
-__global__ __launch_bounds__(NTHREADS) void k_gemv1_ka(GemvKaRow row, float *__restrict__ c,
-                                                      const uint16_t *__restrict__ b,
-                                                      const uint16_t *__restrict__ b2, int K, int N) {
-    (void)row;   // read in place, through the argument segment
-    const uint2 *ka = (const uint2 *)__builtin_amdgcn_kernarg_segment_ptr();   // address space 4 to generic
-    gemv1_body<ROWS, CPL, GATED, false, false, true>(c, nullptr, b, b2, K, N, GemvPro{}, ka);
-}
-
-// Fused gate/up GEMV: rows of Wg and Wu with the same index share a wave, and
-// the epilogue writes silu(gate) * up.  Same constraints as k_gemv.
-template <int MR, int ROWS, int CU>
-__global__ __launch_bounds__(NTHREADS) void k_gemv_gated(float *__restrict__ h,
-                                                        const float *__restrict__ x,
-                                                        const uint16_t *__restrict__ wg,
-                                                        const uint16_t *__restrict__ wu,
-                                                        int K, int N) {
-    extern __shared__ float sA[];
-    const int tid = threadIdx.x;
-    {
-        const f32x4 *a4 = reinterpret_cast<const f32x4 *>(x);
-        f32x4 *s4 = reinterpret_cast<f32x4 *>(sA);
-        const int n4 = (MR * K) >> 2;
-        for (int i = tid; i < n4; i += NTHREADS) {
-            f32x4 v = a4[i];
-            v.x = round_bf16(v.x); v.y = round_bf16(v.y);
-            v.z = round_bf16(v.z); v.w = round_bf16(v.w);
-            s4[i] = v;
-        }
-    }
-    __syncthreads();
-
-    const int wave = tid >> 6, lane = tid & 63;
-    const int row0 = (blockIdx.x * 4 + wave) * ROWS;
-    if (row0 >= N) return;
-    const int nch = K >> 3;
-    const u32x4 *g4 = reinterpret_cast<const u32x4 *>(wg);
-    const u32x4 *u4 = reinterpret_cast<const u32x4 *>(wu);
-
-    constexpr int V = pow2_ceil<2 * MR * ROWS>::v;
-    float acc[V];
-#pragma unroll
-    for (int i = 0; i < V; i++) acc[i] = 0.0f;
-
-    for (int c0 = lane; c0 < nch; c0 += WAVE * CU) {
-        u32x4 bv[CU][2 * ROWS];
-#pragma unroll
-        for (int u = 0; u < CU; u++) {
-            const int ch = c0 + WAVE * u;
-#pragma unroll
-            for (int r = 0; r < ROWS; r++) {
-                const int row = min(row0 + r, N - 1);
-                if (ch < nch) {
-                    bv[u][r] = __builtin_nontemporal_load(g4 + (size_t)row * nch + ch);
-                    bv[u][ROWS + r] = __builtin_nontemporal_load(u4 + (size_t)row * nch + ch);
-                } else {
-                    bv[u][r] = u32x4{0u, 0u, 0u, 0u};
-                    bv[u][ROWS + r] = u32x4{0u, 0u, 0u, 0u};
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < CU; u++) {
-            const int ch = c0 + WAVE * u;
-            if (ch < nch) {
-#pragma unroll
-                for (int m = 0; m < MR; m++) {
-                    const f32x4 *ap = reinterpret_cast<const f32x4 *>(sA + m * K + ch * 8);
-                    const f32x4 x0 = ap[0], x1 = ap[1];
-                    const float av[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-                    for (int r = 0; r < 2 * ROWS; r++) {
-                        float s = acc[m * 2 * ROWS + r];
-#pragma unroll
-                        for (int e = 0; e < 4; e++) {
-                            s = fmaf(av[2 * e], bf16_lo(bv[u][r][e]), s);
-                            s = fmaf(av[2 * e + 1], bf16_hi(bv[u][r][e]), s);
-                        }
-                        acc[m * 2 * ROWS + r] = s;
-                    }
-                }
-            }
-        }
-    }
-
-    constexpr int LV = (V >= 64) ? 6 : (V >= 32) ? 5 : (V >= 16) ? 4 : (V >= 8) ? 3 : (V >= 4) ? 2 : (V >= 2) ? 1 : 0;
-    const float tot = wave_transpose_reduce<V>(acc, lane);
-    // value index idx = m*2*ROWS + r (r < ROWS: gate, r >= ROWS: up); bring
-    // the up total to the lane that holds the matching gate total
-    const int idx = lane >> (6 - LV);
-    const int step = 64 >> LV;                       // lanes per value
-    const float up = __shfl(tot, (lane + ROWS * step) & 63);
-    if ((lane & (step - 1)) == 0) {
-        const int m = idx / (2 * ROWS), r = idx % (2 * ROWS);
-        if (m < MR && r < ROWS && row0 + r < N)
-            h[(size_t)m * N + row0 + r] = silu_mul(tot, up);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// MFMA GEMM: M > 4
-// ---------------------------------------------------------------------------
-// LDS tiles hold rows of BK bf16 (CPR = BK/8 chunks of 16 bytes).  Chunk c of
-// row r lives at chunk slot c ^ f(r).  f makes the 16-byte fragment reads of
-// 16 consecutive rows at one chunk hit distinct banks for 64 four-byte banks
-// (16 lanes/pass) and for 32 banks (8 lanes/pass).
-template <int CPR>
-__device__ __forceinline__ int lds_slot(int row, int ch) {
-    if constexpr (CPR == 16) return row * 16 + (ch ^ (row & 15));
-    else return row * 8 + (ch ^ ((row ^ (row >> 3)) & 7));
-}
-
-template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool VEC>
-struct GemmCfg {
-    static constexpr int CPR = BK / 8;                 // 16-byte chunks per row
-    static constexpr int A_TOTAL = BM * CPR, B_TOTAL = BN * CPR;
-    static constexpr int A_CHUNKS = (A_TOTAL + NTHREADS - 1) / NTHREADS;
-    static constexpr int B_CHUNKS = (B_TOTAL + NTHREADS - 1) / NTHREADS;
-    static constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
-    static constexpr int TM = WTM / 16, TN = WTN / 16;  // MFMA tiles per wave
-    static constexpr int BNO = GATED ? BN / 2 : BN;     // output columns per block
-    static_assert(WM * WN == 4, "4 waves");
-    static_assert(A_TOTAL % NTHREADS == 0 || A_TOTAL < NTHREADS, "chunk split");
-    static_assert(B_TOTAL % NTHREADS == 0 || B_TOTAL < NTHREADS, "chunk split");
-    static_assert(TM >= 1 && TN >= 1, "wave tile");
-    static_assert(!GATED || (TN % 2 == 0), "gated needs paired column tiles");
-};
-
-// Gated column mapping: the wave's TN column tiles are TN/2 gate tiles and
-// the TN/2 up tiles of the same output columns.  B-tile rows [0, BN/2) hold
-// Wg rows, [BN/2, BN) hold Wu rows.
-template <int BN, int WN, int TN, bool GATED>
-__device__ __forceinline__ int b_tile_row(int wn, int j) {
-    if constexpr (!GATED) {
-        return wn * (BN / WN) + 16 * j;
-    } else {
-        constexpr int BNO = BN / 2, TNO = TN / 2;
-        const int base = wn * (BNO / WN);
-        return (j < TNO) ? base + 16 * j : BNO + base + 16 * (j - TNO);
-    }
-}
-
-// Output-tile order for a 1-D grid.  Workgroups are handed to the 8 XCDs
-// round-robin (workgroup b runs on XCD b % 8) and each XCD has its own L2, so
-// the MT x NT tile grid is cut into rm x rn = 8 regions, one per XCD, and the
-// workgroups of an XCD walk their region m-major (consecutive ones share an A
-// panel).  Each XCD then pulls only its A and B slabs into its L2.  rm == 0
-// means plain row-major order (used when the grid does not split evenly).
-struct TileMap {
-    int MT, NT, rm, rn;
-};
-
-__device__ __forceinline__ void tile_of(int bid, const TileMap &map, int &tm, int &tn) {
-    if (map.rm == 0) {
-        tm = bid / map.NT;
-        tn = bid % map.NT;
-        return;
-    }
-    const int xcd = bid & 7, local = bid >> 3;
-    const int rmt = map.MT / map.rm, rnt = map.NT / map.rn;    // tiles per region
-    tm = (xcd / map.rn) * rmt + local / rnt;
-    tn = (xcd % map.rn) * rnt + local % rnt;
-}
-
-template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool VEC>
-__global__ __launch_bounds__(NTHREADS, 2) void k_gemm(float *__restrict__ c,
-                                                     const float *__restrict__ a,
-                                                     const uint16_t *__restrict__ b,
-                                                     const uint16_t *__restrict__ b2,
-                                                     int M, int K, int N, TileMap map) {
-    using C = GemmCfg<BM, BN, BK, WM, WN, GATED, VEC>;
-    __shared__ u32x4 sA[2][BM * C::CPR];
-    __shared__ u32x4 sB[2][BN * C::CPR];
-
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, lane = tid & 63;
-    const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    tile_of(blockIdx.x, map, tm, tn);
-    const int m0 = tm * BM;
-    const int n0 = tn * C::BNO;
-
-    // ---- global -> register staging ----
-    float ra[C::A_CHUNKS][8];
-    u32x4 rb[C::B_CHUNKS];
-
-    auto load_a = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < C::A_CHUNKS; i++) {
-            const int q = tid + NTHREADS * i;
-            if (C::A_TOTAL < NTHREADS && q >= C::A_TOTAL) break;
-            const int row = q / C::CPR, ch = q % C::CPR;
-            const int gm = m0 + row, gk = k0 + ch * 8;
-            if constexpr (VEC) {
-                if (gm < M && gk < K) {
-                    const f32x4 *p = reinterpret_cast<const f32x4 *>(a + (size_t)gm * K + gk);
-                    const f32x4 x0 = p[0], x1 = p[1];
-                    ra[i][0] = x0.x; ra[i][1] = x0.y; ra[i][2] = x0.z; ra[i][3] = x0.w;
-                    ra[i][4] = x1.x; ra[i][5] = x1.y; ra[i][6] = x1.z; ra[i][7] = x1.w;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) ra[i][e] = 0.0f;
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++)
-                    ra[i][e] = (gm < M && gk + e < K) ? a[(size_t)gm * K + gk + e] : 0.0f;
-            }
-        }
-    };
-    auto load_b = [&](int k0) {
-#pragma unroll
-        for (int i = 0; i < C::B_CHUNKS; i++) {
-            const int q = tid + NTHREADS * i;
-            if (C::B_TOTAL < NTHREADS && q >= C::B_TOTAL) break;
-            const int row = q / C::CPR, ch = q % C::CPR;
-            const uint16_t *src;
-            int gn;
-            if constexpr (GATED) {
-                const bool up = row >= C::BNO;
-                gn = n0 + (up ? row - C::BNO : row);
-                src = up ? b2 : b;
-            } else {
-                gn = n0 + row;
-                src = b;
-            }
-            const int gk = k0 + ch * 8;
-            if constexpr (VEC) {
-                if (gn < N && gk < K)
-                    rb[i] = *reinterpret_cast<const u32x4 *>(src + (size_t)gn * K + gk);
-                else
-                    rb[i] = u32x4{0u, 0u, 0u, 0u};
-            } else {
-                uint32_t w[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    uint32_t lo = (gn < N && gk + 2 * e < K) ? src[(size_t)gn * K + gk + 2 * e] : 0u;
-                    uint32_t hi = (gn < N && gk + 2 * e + 1 < K) ? src[(size_t)gn * K + gk + 2 * e + 1] : 0u;
-                    w[e] = lo | (hi << 16);
-                }
-                rb[i] = u32x4{w[0], w[1], w[2], w[3]};
-            }
-        }
-    };
-    auto store_tiles = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < C::A_CHUNKS; i++) {
-            const int q = tid + NTHREADS * i;
-            if (C::A_TOTAL < NTHREADS && q >= C::A_TOTAL) break;
-            const int row = q / C::CPR, ch = q % C::CPR;
-            u32x4 w;
-            w.x = pack_bf16x2(ra[i][0], ra[i][1]);
-            w.y = pack_bf16x2(ra[i][2], ra[i][3]);
-            w.z = pack_bf16x2(ra[i][4], ra[i][5]);
-            w.w = pack_bf16x2(ra[i][6], ra[i][7]);
-            sA[buf][lds_slot<C::CPR>(row, ch)] = w;
-        }
-#pragma unroll
-        for (int i = 0; i < C::B_CHUNKS; i++) {
-            const int q = tid + NTHREADS * i;
-            if (C::B_TOTAL < NTHREADS && q >= C::B_TOTAL) break;
-            const int row = q / C::CPR, ch = q % C::CPR;
-            sB[buf][lds_slot<C::CPR>(row, ch)] = rb[i];
-        }
-    };
-
-    f32x4 acc[C::TM][C::TN];
-#pragma unroll
-    for (int i = 0; i < C::TM; i++)
-#pragma unroll
-        for (int j = 0; j < C::TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int nk = (K + BK - 1) / BK;
-    load_a(0);
-    load_b(0);
-    store_tiles(0);
-    __syncthreads();
-
-    const int lrow = lane & 15, lgrp = lane >> 4;
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            load_a((kt + 1) * BK);
-            load_b((kt + 1) * BK);
-        }
-#pragma unroll
-        for (int s = 0; s < BK / 32; s++) {
-            const int ch = 4 * s + lgrp;
-            bf16x8 af[C::TM], bfr[C::TN];
-#pragma unroll
-            for (int i = 0; i < C::TM; i++) {
-                const int row = wm * C::WTM + 16 * i + lrow;
-                af[i] = __builtin_bit_cast(bf16x8, sA[cur][lds_slot<C::CPR>(row, ch)]);
-            }
-#pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const int row = b_tile_row<BN, WN, C::TN, GATED>(wn, j) + lrow;
-                bfr[j] = __builtin_bit_cast(bf16x8, sB[cur][lds_slot<C::CPR>(row, ch)]);
-            }
-#pragma unroll
-            for (int i = 0; i < C::TM; i++)
-#pragma unroll
-                for (int j = 0; j < C::TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store_tiles(cur ^ 1);
-        __syncthreads();
-    }
-
-    // ---- epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
-#pragma unroll
-    for (int i = 0; i < C::TM; i++) {
-        const int rbase = m0 + wm * C::WTM + 16 * i + 4 * lgrp;
-        if constexpr (!GATED) {
-#pragma unroll
-            for (int j = 0; j < C::TN; j++) {
-                const int col = n0 + wn * C::WTN + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int row = rbase + r;
-                        if (row < M) c[(size_t)row * N + col] = acc[i][j][r];
-                    }
-                }
-            }
-        } else {
-            constexpr int TNO = C::TN / 2;
-#pragma unroll
-            for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (C::BNO / WN) + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int row = rbase + r;
-                        if (row < M) c[(size_t)row * N + col] = silu_mul(acc[i][j][r], acc[i][j + TNO][r]);
-                    }
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Ring-pipelined MFMA GEMM (K % 32 == 0, 16-byte aligned operands)
-// ---------------------------------------------------------------------------
-// A k-loop that waits for one global round trip per step is latency-bound
-// (~0.7 us per step on MI355X).  Here every 32-wide k step of the A tile
-// (fp32) and B tile (bf16) is copied straight from global memory into a ring
-// of STAGES LDS slots by global_load_lds_dwordx4 (no registers involved), and
-// STAGES-1 steps are always in flight.  Per step each wave waits only for its
-// own oldest copies (s_waitcnt vmcnt), one barrier publishes the slot and
-// frees the previous one, the next copy is issued, then MFMAs run on the
-// slot; A is converted to bf16 (RNE) as its fragments are read.
-//
-// LDS slot layout (one step): A rows of 32 fp32 (128 B = 8 chunks of 16 B),
-// then B rows of 32 bf16 (64 B = 4 chunks).  Chunk c of row r sits at
-// c ^ swzA(r) / c ^ swzB(r); both swizzles keep 16 consecutive rows at one
-// logical chunk on distinct banks (checked for 8- and 16-lane LDS passes).
-// A wave's LDS copy always fills 1 KB contiguously (lane i -> bytes 16i..),
-// so each lane picks the global chunk that belongs at its LDS position.
-// Swizzle for rows of CH 16-byte chunks (64, 128, 256 or 512 bytes).
-template <int CH>
-__device__ __forceinline__ int swz(int r) {
-    if constexpr (CH == 4) return ((r >> 1) ^ (r >> 3)) & 3;
-    else if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
-    else return r & 15;                       // 16 or 32 chunks
-}
-
-// s_waitcnt immediate for "at most n vector-memory ops outstanding" (gfx9
-// encoding: vmcnt bits [3:0] and [15:14]; expcnt and lgkmcnt left at max)
-#define QH_VMCNT(n) ((((n) & 15) | (((n) >> 4) << 14)) | (7 << 4) | (15 << 8))
-
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_ = 32, int KG = 1>
-struct RingCfg {
-    static constexpr int BK = BK_;                      // k per stage (32, 64, 128)
-    static constexpr int KS = BK / 32;                  // MFMA k-steps per stage
-    static constexpr int KSG = KS / KG;                 // ... per wave group
-    static constexpr int CA = BK / 4, CB = BK / 8;      // 16-byte chunks per A / B row
-    static constexpr int A_BYTES = BM * BK * 4, B_BYTES = BN * BK * 2;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int NW = WM * WN * KG;             // waves: KG groups of WM x WN
-    static constexpr int A_DMA = A_BYTES / 1024 / NW;  // 1 KB copies per wave per step
-    static constexpr int B_DMA = B_BYTES / 1024 / NW;
-    static constexpr int LPS = A_DMA + B_DMA;           // copies per wave per step
-    static constexpr int WTM = BM / WM, WTN = BN / WN;
-    static constexpr int TM = WTM / 16, TN = WTN / 16;
-    static constexpr int BNO = GATED ? BN / 2 : BN;
-    static constexpr int LDS = STAGES * STAGE;
-    static constexpr int vm(int k) { return k * LPS > 63 ? 63 : k * LPS; }
-    static_assert(NW == 4 || NW == 8 || NW == 16, "4, 8 or 16 waves");
-    static_assert((KG == 1 || KG == 2 || KG == 4) && KSG * KG == KS, "wave groups split a stage's k-steps");
-    static_assert(A_DMA * NW * 1024 == A_BYTES && B_DMA * NW * 1024 == B_BYTES, "every wave issues the same number of copies");
-    static_assert(A_DMA >= 1 && B_DMA >= 1, "copies per wave");
-    static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
-    static_assert(STAGES >= 2 && (STAGES - 2) * LPS <= 63, "vmcnt range");
-};
-
-// ---------------------------------------------------------------------------
-// Software-pipelined ring GEMM
-// ---------------------------------------------------------------------------
-template <int V> struct IC { static constexpr int value = V; };
-
-// A and B stream straight into an LDS ring of STAGES slots with
-// global_load_lds (16-byte copies, explicit vmcnt waits, one barrier per
-// stage), and the phases of consecutive stages overlap inside each wave: while the MFMAs of stage `it` run on
-// fragments already in registers, the LDS reads of stage it+1 fill a second
-// register set and the copies of stage it+STAGES-1 are in flight.  Per stage:
-//   wait (own copies of it+1) -> barrier -> issue copies of it+STAGES-1 ->
-//   read fragments of it+1 -> MFMAs of it.
-// The copy into slot (it-1) % STAGES is safe after the barrier: every wave
-// consumed stage it-1 (its MFMAs ran) before reaching it.  LDS destinations
-// of the copies are wave-uniform and computed from a scalar wave index.
-// KG groups of WM x WN waves: with KG = 2 or 4 (the 32 x 64 tiles with
-// 128-deep stages, one block per CU) the groups split each stage's k-steps
-// and the others add their sums into the first group's through LDS at the
-// end, in group order, so that two or four waves share each SIMD (measured
-// on MI355X, graph-replayed, against one group of 2 x 2: 512 x {1024, 2048,
-// 3072} x 1024 6.9 / 10.9 / 15.0 -> 6.4 / 9.65 / 12.8 us with two groups,
-// 128 x 1024 x 4096 6.7 -> 6.2, gate|up + SiLU 64 x 1024 x 3072 6.74 ->
-// 6.27; four groups from K = 2048: 512 x {2048, 3072} x 1024 9.5 / 12.7 ->
-// 9.1 / 12.2, but at K = 1024 they lose, 6.24 -> 6.35; 2 x 4 waves on the
-// plain tiles instead reached 6.75 / 10.6 / 14.5).
-template <int BM, int BN, int WM, int WN, int STAGES, bool GATED, int BK_, int KG>
-__global__ __launch_bounds__(64 * WM * WN * KG, 1) void k_gemm_pipe(float *__restrict__ c,
-                                                          const float *__restrict__ a,
-                                                          const uint16_t *__restrict__ b,
-                                                          const uint16_t *__restrict__ b2,
-                                                          int M, int K, int N, TileMap map) {
-    using R = RingCfg<BM, BN, WM, WN, STAGES, GATED, BK_, KG>;
-    static_assert(STAGES >= 3, "one stage being read, one in use, one or more in flight");
-    extern __shared__ __align__(16) unsigned char smem[];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);     // scalar
-    const int kg = wave / (WM * WN), wq = wave % (WM * WN);   // k group, wave within it
-    const int wm = wq / WN, wn = wq % WN;
-    int tm, tn;
-    tile_of(blockIdx.x, map, tm, tn);
-    const int m0 = tm * BM;
-    const int n0 = tn * R::BNO;
-    const int nk = K / R::BK;
-
-    const float *asrc[R::A_DMA];
-    const uint16_t *bsrc[R::B_DMA];
-#pragma unroll
-    for (int i = 0; i < R::A_DMA; i++) {
-        const int seg = wave * R::A_DMA + i;
-        const int r = seg * (64 / R::CA) + lane / R::CA;
-        const int cl = (lane % R::CA) ^ swz<R::CA>(r);
-        const int gm = min(m0 + r, M - 1);
-        asrc[i] = a + (size_t)gm * K + cl * 4;
-    }
-#pragma unroll
-    for (int i = 0; i < R::B_DMA; i++) {
-        const int seg = wave * R::B_DMA + i;
-        const int r = seg * (64 / R::CB) + lane / R::CB;
-        const int cl = (lane % R::CB) ^ swz<R::CB>(r);
-        const uint16_t *src = b;
-        int gn;
-        if constexpr (GATED) {
-            const bool up = r >= R::BNO;
-            gn = n0 + (up ? r - R::BNO : r);
-            src = up ? b2 : b;
-        } else {
-            gn = n0 + r;
-        }
-        gn = min(gn, N - 1);
-        bsrc[i] = src + (size_t)gn * K + cl * 8;
-    }
-    // wave-uniform LDS byte offsets of this wave's copies within a slot
-    const int a_dst = wave * R::A_DMA * 1024;
-    const int b_dst = R::A_BYTES + wave * R::B_DMA * 1024;
-
-    auto issue = [&](int step) {
-        unsigned char *slot = smem + (step % STAGES) * R::STAGE;
-        const int k0 = step * R::BK;
-#pragma unroll
-        for (int i = 0; i < R::A_DMA; i++)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(asrc[i] + k0),
-                (__attribute__((address_space(3))) void *)(slot + a_dst + i * 1024), 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < R::B_DMA; i++)
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(bsrc[i] + k0),
-                (__attribute__((address_space(3))) void *)(slot + b_dst + i * 1024), 16, 0, 0);
-    };
-
-    const int lrow = lane & 15, lgrp = lane >> 4;
-    // per-lane LDS offsets of this lane's fragment rows (within a slot)
-    int arow_off[R::TM], arow_sw[R::TM], brow_off[R::TN], brow_sw[R::TN];
-#pragma unroll
-    for (int i = 0; i < R::TM; i++) {
-        const int row = wm * R::WTM + 16 * i + lrow;
-        arow_off[i] = row * (R::CA * 16);
-        arow_sw[i] = swz<R::CA>(row);
-    }
-#pragma unroll
-    for (int j = 0; j < R::TN; j++) {
-        const int row = b_tile_row<BN, WN, R::TN, GATED>(wn, j) + lrow;
-        brow_off[j] = R::A_BYTES + row * (R::CB * 16);
-        brow_sw[j] = swz<R::CB>(row);
-    }
-
-    u32x4 fa[2][R::KSG][R::TM][2], fb[2][R::KSG][R::TN];
-    // `SET` selects the register set at compile time (IC<0> / IC<1>)
-    auto read_frags = [&](int step, auto SET) {
-        constexpr int set = decltype(SET)::value;
-        const unsigned char *slot = smem + (step % STAGES) * R::STAGE;
-#pragma unroll
-        for (int tt = 0; tt < R::KSG; tt++) {
-            const int t = kg * R::KSG + tt;                   // this group's k-steps
-#pragma unroll
-            for (int i = 0; i < R::TM; i++) {
-                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + arow_off[i]);
-                fa[set][tt][i][0] = rowp[(8 * t + 2 * lgrp) ^ arow_sw[i]];
-                fa[set][tt][i][1] = rowp[(8 * t + 2 * lgrp + 1) ^ arow_sw[i]];
-            }
-#pragma unroll
-            for (int j = 0; j < R::TN; j++) {
-                const u32x4 *rowp = reinterpret_cast<const u32x4 *>(slot + brow_off[j]);
-                fb[set][tt][j] = rowp[(4 * t + lgrp) ^ brow_sw[j]];
-            }
-        }
-    };
-
-    f32x4 acc[R::TM][R::TN];
-#pragma unroll
-    for (int i = 0; i < R::TM; i++)
-#pragma unroll
-        for (int j = 0; j < R::TN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    auto mfmas = [&](auto SET) {
-        constexpr int set = decltype(SET)::value;
-#pragma unroll
-        for (int t = 0; t < R::KSG; t++) {
-            bf16x8 af[R::TM];
-#pragma unroll
-            for (int i = 0; i < R::TM; i++) {
-                const f32x4 x0 = __builtin_bit_cast(f32x4, fa[set][t][i][0]);
-                const f32x4 x1 = __builtin_bit_cast(f32x4, fa[set][t][i][1]);
-                u32x4 w;
-                w.x = pack_bf16x2(x0.x, x0.y);
-                w.y = pack_bf16x2(x0.z, x0.w);
-                w.z = pack_bf16x2(x1.x, x1.y);
-                w.w = pack_bf16x2(x1.z, x1.w);
-                af[i] = __builtin_bit_cast(bf16x8, w);
-            }
-#pragma unroll
-            for (int i = 0; i < R::TM; i++)
-#pragma unroll
-                for (int j = 0; j < R::TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        af[i], __builtin_bit_cast(bf16x8, fb[set][t][j]), acc[i][j], 0, 0, 0);
-        }
-    };
-
-    // prologue: copies of stages 0 .. STAGES-2 in flight; stage 0 read
-    const int pro = nk < STAGES - 1 ? nk : STAGES - 1;
-    for (int s = 0; s < pro; s++) issue(s);
-    {
-        const int later = min(nk - 1, STAGES - 2);      // stages issued after stage 0
-        switch (later) {
-            case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
-            case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
-            case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
-            case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
-            case 4: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
-            default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(5))); break;
-        }
-        __builtin_amdgcn_s_barrier();
-        read_frags(0, IC<0>{});
-    }
-
-    // one pipeline step: MFMAs on register set CUR while stage it+1 is read
-    // into the other set
-    auto step = [&](int it, auto CUR) {
-        constexpr int cur = decltype(CUR)::value;
-        if (it + 1 < nk) {
-            // own copies of stage it+1 landed: stages it+2 .. it+STAGES-2 may
-            // still be in flight
-            const int later = min(nk - 2 - it, STAGES - 3);
-            switch (later) {
-                case 0: __builtin_amdgcn_s_waitcnt(QH_VMCNT(0)); break;
-                case 1: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(1))); break;
-                case 2: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(2))); break;
-                case 3: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(3))); break;
-                default: __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(4))); break;
-            }
-            __builtin_amdgcn_s_barrier();
-            if (it + STAGES - 1 < nk) issue(it + STAGES - 1);
-            read_frags(it + 1, IC<cur ^ 1>{});
-        }
-        mfmas(CUR);
-    };
-    // the same step where stage it+1 exists, a copy is due and STAGES-3
-    // later stages stay in flight: straight-line code, so that the compiler
-    // waits before the MFMAs only for the older fragment set (lgkmcnt of
-    // the reads just issued) instead of every LDS read (the branches of
-    // `step` leave it with lgkmcnt(0), which serialises the reads of stage
-    // it+1 with the MFMAs of stage it)
-    auto full_step = [&](int it, auto CUR) {
-        constexpr int cur = decltype(CUR)::value;
-        __builtin_amdgcn_s_waitcnt(QH_VMCNT(R::vm(STAGES - 3)));
-        __builtin_amdgcn_s_barrier();
-        issue(it + STAGES - 1);
-        read_frags(it + 1, IC<cur ^ 1>{});
-        mfmas(CUR);
-        __builtin_amdgcn_sched_barrier(0);             // no MFMA moves past the next barrier
-    };
-    int it = 0;
-    for (; it + STAGES < nk; it += 2) {
-        full_step(it, IC<0>{});
-        full_step(it + 1, IC<1>{});
-    }
-    for (; it < nk; it += 2) {
-        step(it, IC<0>{});
-        if (it + 1 < nk) step(it + 1, IC<1>{});
-    }
-
-    // two wave groups: the second adds its sums into the first's through LDS
-    if constexpr (KG > 1) {
-        constexpr int PER_G = WM * WN * R::TM * R::TN * 64;   // f32x4 per group
-        f32x4 *xred = reinterpret_cast<f32x4 *>(smem);
-        __syncthreads();                                   // every wave is done with the ring
-        if (kg > 0) {
-#pragma unroll
-            for (int i = 0; i < R::TM; i++)
-#pragma unroll
-                for (int j = 0; j < R::TN; j++)
-                    xred[(kg - 1) * PER_G + ((wq * R::TM + i) * R::TN + j) * 64 + lane] = acc[i][j];
-        }
-        __syncthreads();
-        if (kg > 0) return;
-#pragma unroll
-        for (int q = 1; q < KG; q++)                       // the groups' sums in group order
-#pragma unroll
-            for (int i = 0; i < R::TM; i++)
-#pragma unroll
-                for (int j = 0; j < R::TN; j++)
-                    acc[i][j] += xred[(q - 1) * PER_G + ((wq * R::TM + i) * R::TN + j) * 64 + lane];
-    }
-
-    // epilogue: lane holds rows 4*(lane>>4)+r, column lane&15 of each tile
-#pragma unroll
-    for (int i = 0; i < R::TM; i++) {
-        const int rbase = m0 + wm * R::WTM + 16 * i + 4 * lgrp;
-        if constexpr (!GATED) {
-#pragma unroll
-            for (int j = 0; j < R::TN; j++) {
-                const int col = n0 + wn * R::WTN + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (rbase + r < M) __builtin_nontemporal_store(acc[i][j][r], &c[(size_t)(rbase + r) * N + col]);
-                }
-            }
-        } else {
-            constexpr int TNO = R::TN / 2;
-#pragma unroll
-            for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (R::BNO / WN) + 16 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++)
-                        if (rbase + r < M)
-                            __builtin_nontemporal_store(silu_mul(acc[i][j][r], acc[i][j + TNO][r]),
-                                                        &c[(size_t)(rbase + r) * N + col]);
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Large-tile MFMA GEMM: 32x32x16 bf16 MFMA, 2 x 2 waves (2 x 4 on 256 x 256
-// tiles), two stages in flight
-// ---------------------------------------------------------------------------
-// Block tile BM x BN, k stages of BK (32 or 64).  Each wave owns a
-// (BM/WMW) x (BN/WNW) tile of TM x TN 32x32 accumulators (fp32, 16 per lane).
-// 256 x 256 tiles run eight waves (two per SIMD, 128 x 64 each): with one
-// wave per SIMD the MFMA pipe idles whenever that wave waits (measured on
-// MI355X, graph-replayed: 4096 x 1024 x 4096 45.2 -> 43.3 us, gated 4096 x
-// 1024 x 3072 84.8 -> 72.4 us, 8192 x 1024 x 4096 bf16 A 88.2 -> 83.9 us).
-// Operands move global -> registers -> LDS with 16-byte buffer loads (a
-// fixed 32-bit offset per lane and load, the stage's k offset in a scalar
-// register): A as fp32, rounded to bf16 (RNE) on the way into LDS; B as
-// bf16.  Registers hold two stages (two sets), LDS two slots; stage `it` is
-// one scheduling region in which the MFMAs of stage it (fragments from slot
-// it&1), the loads of stage it+2 and the conversion and LDS stores of stage
-// it+1 (into the other slot) are interleaved, followed by one barrier.
-// With one wave per SIMD the MFMA pipe only stays busy if the loads and
-// stores issue between MFMAs; run back to back they leave it idle half the
-// time.  Two stages of loads stay in flight, which covers the ~1 us load
-// latency seen under load.
-// Register sets and LDS slots are picked at compile time (loop unrolled by
-// two; each slot is its own LDS array), so the compiler can tell that the
-// stores of stage it+1 do not touch what the MFMAs of stage it read, and its
-// wait analysis follows each register.
-// LDS rows are BK bf16 (CPR = BK/8 chunks of 16 bytes); chunk c of row r
-// sits at slot c ^ f(r), f chosen so that the 32-row fragment reads are
-// conflict-free (SQ_LDS_BANK_CONFLICT reads 0 on MI355X for both row
-// widths; for 64-byte rows f(r) = ((r >> 1) ^ (r >> 3)) & 3 left 37% of the
-// LDS busy cycles to conflicts, 4096 x 1024 x 4096 43.3 -> 42.2 us).
-// Per block per stage the CU moves (4*BM + 2*BN)*BK bytes through its vector
-// memory path for 2*BM*BN*BK flops: 256 x 256 tiles need 3/256 byte per
-// flop, inside the ~64 B/clk a CU loads against its 4096 flop/clk.
-// Requires K % BK == 0, 16-byte aligned a, b, b2, and fewer than 2^32 bytes
-// in A and in each weight matrix.  Rows >= M and columns >= N are clamped for
-// loading and never stored.
-// waves of a large-tile block along N: four on 256 x 256 tiles, else two;
-// along M (WMW): two, or four for gated 128 x 128 tiles when they do not
-// outnumber the CUs (a wave's gate and up columns stay together)
-constexpr int xl_wn(int bm, int bn) { return bm == 256 && bn == 256 ? 4 : 2; }
-template <int BM, int BN, int BK, bool GATED, bool ABF16 = false, int SETS = 2, int WMW = 2, int KG = 1>
-struct XlCfg {
-    static constexpr int WNW = xl_wn(BM, BN);
-    static constexpr int NT = 64 * WMW * WNW * KG;              // threads: KG groups of WMW x WNW waves
-    static constexpr int KSG = BK / 16 / KG;                    // k-steps of a stage per wave group
-    static constexpr int CPR = BK / 8;                          // 16-byte chunks per LDS row
-    static constexpr int WTM = BM / WMW, WTN = BN / WNW;        // wave tile
-    static constexpr int TM = WTM / 32, TN = WTN / 32;          // 32x32 blocks per wave
-    static constexpr int BNO = GATED ? BN / 2 : BN;             // output columns per block
-    static constexpr int A_SLOT = BM * BK * 2, B_SLOT = BN * BK * 2;
-    static constexpr int LDS = 2 * (A_SLOT + B_SLOT);
-    static constexpr int A_CPR = ABF16 ? CPR : BK / 4;          // 16-byte A chunks per row
-    static constexpr int A_LOADS = BM * A_CPR / NT;             // 16-byte A loads per lane
-    static constexpr int B_LOADS = BN * CPR / NT;               // 16-byte bf16 loads per lane
-    static constexpr int B_ROWS_PER_LOAD = NT / CPR;
-    static constexpr int MFMAS = TM * TN * KSG;                 // per wave per stage
-    static constexpr int LOADS = A_LOADS + B_LOADS;             // per lane per stage
-    static_assert(BK == 32 || BK == 64, "k stage");
-    static_assert((KG == 1 || KG == 2) && KSG * KG == BK / 16, "wave groups split a stage's k-steps");
-    static_assert(SETS >= 1 && SETS <= 3, "register sets");
-    static_assert(TM >= 1 && TN >= 1 && (!GATED || TN % 2 == 0), "wave tile");
-    static_assert(A_LOADS >= 1 && B_LOADS >= 1, "loads per lane");
-    static_assert(!GATED || BNO % B_ROWS_PER_LOAD == 0, "a load never mixes Wg and Wu rows");
-    static_assert(LDS <= 160 * 1024, "LDS");
-};
-
-template <int CPR>
-__device__ __forceinline__ int xl_swz(int r) {
-    if constexpr (CPR == 8) return (r ^ (r >> 3)) & 7;
-    else return (r ^ (r >> 2)) & 3;
-}
-
-// B-tile row of 32-column block j of wave column wn (gated: the first TN/2
-// blocks are Wg rows, the rest the Wu rows of the same outputs)
-template <int BN, int TN, bool GATED, int WNW>
-__device__ __forceinline__ int xl_brow(int wn, int j) {
-    if constexpr (!GATED) {
-        return wn * (BN / WNW) + 32 * j;
-    } else {
-        constexpr int TNO = TN / 2;
-        const int base = wn * (BN / (2 * WNW));
-        return (j < TNO) ? base + 32 * j : BN / 2 + base + 32 * (j - TNO);
-    }
-}
-
-// Scheduling pattern of one stage (one wave's instruction order).  The
-// fragments of the first k-step are read first; then every MFMA is followed
-// by its share of: the fragment reads of the next k-step (spread over the
-// MFMAs of the k-step before), the global loads (first half of the MFMAs)
-// and the LDS stores (second half).  Waiting on a fragment read right before
-// its MFMA would expose the LDS latency on every MFMA pair.
-template <int N, int SLOTS, int I>
-struct XlShare {   // how many of N items go after MFMA I of SLOTS (even spread)
-    static constexpr int v = ((I + 1) * N) / SLOTS - (I * N) / SLOTS;
-};
-// STORE_FIRST (one register set): the stores of stage it+1 go in the first
-// half, the loads of stage it+2 (into the registers the stores freed) in the
-// second half.
-template <int I, int MFMAS, int KS, int FR, int LOADS, bool STORE_FIRST = false>
-struct XlSched {
-    static constexpr int PER_K = MFMAS / KS;           // MFMAs per k-step
-    static constexpr int H = MFMAS / 2;
-    static constexpr int FIRST = STORE_FIRST ? 0x200 : 0x020, SECOND = STORE_FIRST ? 0x020 : 0x200;
-    static __device__ __forceinline__ void run() {
-        if constexpr (I == 0) __builtin_amdgcn_sched_group_barrier(0x100, FR, 0);   // first fragments
-        if constexpr (I < MFMAS) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
-            if constexpr (I < MFMAS - PER_K) {                                      // next fragments
-                constexpr int n = XlShare<FR * (KS - 1), MFMAS - PER_K, I>::v;
-                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
-            }
-            if constexpr (I < H) {
-                constexpr int n = XlShare<LOADS, H, I>::v;
-                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(FIRST, n, 0);
-            } else {
-                constexpr int n = XlShare<LOADS, MFMAS - H, I - H>::v;
-                if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(SECOND, n, 0);
-            }
-            XlSched<I + 1, MFMAS, KS, FR, LOADS, STORE_FIRST>::run();
-        }
-    }
-};
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t xl_rsrc(const void *p, size_t bytes) {
-    // raw buffer: stride 0, num_records = bytes, default data format
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)(uint32_t)bytes, 0x00020000);
-}
-
-// ABF16: A is already bf16 (a points to uint16_t bits): it is copied into LDS
-// like B, with no conversion.
-// 64-row tiles (batched decode) are bandwidth kernels: two blocks per CU
-// double the loads in flight
-// SETS = 1: one register set; each stage stores stage it+1 first and then
-// loads stage it+2 into the freed registers (one stage of latency cover, for
-// tiles whose two register sets would not fit).
-template <int BM, int BN, int BK, bool GATED, bool ABF16, int SETS, int WMW, int KG>
-__global__ __launch_bounds__(64 * WMW * xl_wn(BM, BN) * KG, WMW * xl_wn(BM, BN) * KG == 8 ? 1 : (BM * BN <= 128 * 128 ? 2 : 1)) void k_gemm_xl(float *__restrict__ c,
-                                                        const void *__restrict__ a,
-                                                        const uint16_t *__restrict__ b,
-                                                        const uint16_t *__restrict__ b2,
-                                                        int M, int K, int N, TileMap map) {
-    using X = XlCfg<BM, BN, BK, GATED, ABF16, SETS, WMW, KG>;
-    constexpr int CPR = X::CPR;
-    __shared__ __align__(16) unsigned char sa0[X::A_SLOT];
-    __shared__ __align__(16) unsigned char sa1[X::A_SLOT];
-    __shared__ __align__(16) unsigned char sb0[X::B_SLOT];
-    __shared__ __align__(16) unsigned char sb1[X::B_SLOT];
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kg = wave / (WMW * X::WNW), wq = wave % (WMW * X::WNW);   // k group, wave within it
-    const int wm = wq / X::WNW, wn = wq % X::WNW;
-    int tm, tn;
-    tile_of(blockIdx.x, map, tm, tn);
-    const int m0 = tm * BM;
-    const int n0 = tn * X::BNO;
-    const int nk = K / BK;
-
-    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * (ABF16 ? 2 : 4));
-    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = GATED ? xl_rsrc(b2, (size_t)N * K * 2) : rb;
-
-    // A: load i of this lane is fp32 chunk q = i*256 + tid of the tile (BK/4
-    // chunks of 4 floats per row); B: bf16 chunk q (CPR chunks of 8 per row)
-    uint32_t aoffs[X::A_LOADS];
-    int adst[X::A_LOADS];
-#pragma unroll
-    for (int i = 0; i < X::A_LOADS; i++) {
-        const int q = i * X::NT + tid;
-        const int r = q / X::A_CPR, cq = q % X::A_CPR;
-        const uint32_t row = (uint32_t)min(m0 + r, M - 1) * (uint32_t)K;
-        if constexpr (ABF16) {
-            aoffs[i] = (row + (uint32_t)cq * 8u) * 2u;
-            adst[i] = r * (BK * 2) + ((cq ^ xl_swz<CPR>(r)) << 4);
-        } else {
-            aoffs[i] = (row + (uint32_t)cq * 4u) * 4u;
-            adst[i] = r * (BK * 2) + (((cq >> 1) ^ xl_swz<CPR>(r)) << 4) + ((cq & 1) << 3);
-        }
-    }
-    uint32_t boffs[X::B_LOADS];
-    int bdst[X::B_LOADS];
-#pragma unroll
-    for (int i = 0; i < X::B_LOADS; i++) {
-        const int q = i * X::NT + tid;
-        const int r = q / CPR, ch = q % CPR;
-        int gn = n0 + r;
-        if constexpr (GATED) {
-            if (i * X::B_ROWS_PER_LOAD >= X::BNO) gn = n0 + r - X::BNO;   // Wu rows
-        }
-        boffs[i] = ((uint32_t)min(gn, N - 1) * (uint32_t)K + (uint32_t)ch * 8u) * 2u;
-        bdst[i] = r * (BK * 2) + ((ch ^ xl_swz<CPR>(r)) << 4);
-    }
-
-    // fragment read offsets (bytes within an A / B slot) and swizzles
-    const int lrow = lane & 31, lk = lane >> 5;
-    int aoff[X::TM], asw[X::TM], boff[X::TN], bsw[X::TN];
-#pragma unroll
-    for (int i = 0; i < X::TM; i++) {
-        const int r = wm * X::WTM + 32 * i + lrow;
-        aoff[i] = r * (BK * 2);
-        asw[i] = xl_swz<CPR>(r);
-    }
-#pragma unroll
-    for (int j = 0; j < X::TN; j++) {
-        const int r = xl_brow<BN, X::TN, GATED, X::WNW>(wn, j) + lrow;
-        boff[j] = r * (BK * 2);
-        bsw[j] = xl_swz<CPR>(r);
-    }
-
-    u32x4 areg[SETS][X::A_LOADS];
-    u32x4 breg[SETS][X::B_LOADS];
-    // SET: register set (and, for store and compute, LDS slot), compile-time
-    auto load = [&](int step, auto SET) {
-        constexpr int set = SETS == 1 ? 0 : decltype(SET)::value % SETS;
-        const int ka = step * BK * (ABF16 ? 2 : 4), kb = step * BK * 2;   // scalar byte offsets
-#pragma unroll
-        for (int i = 0; i < X::A_LOADS; i++)
-            areg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, aoffs[i], ka, 0);
-#pragma unroll
-        for (int i = 0; i < X::B_LOADS; i++) {
-            const bool up = GATED && i * X::B_ROWS_PER_LOAD >= X::BNO;
-            breg[set][i] = __builtin_amdgcn_raw_buffer_load_b128(up ? rb2 : rb, boffs[i], kb, 0);
-        }
-    };
-    // RSET: the register set that holds the stage (SETS = 3: not the slot)
-    auto store = [&](auto SLOT, auto RSET) {
-        constexpr int slot = decltype(SLOT)::value;
-        constexpr int set = SETS == 1 ? 0 : SETS == 2 ? slot : decltype(RSET)::value % SETS;
-        unsigned char *as = slot ? sa1 : sa0;
-        unsigned char *bs = slot ? sb1 : sb0;
-#pragma unroll
-        for (int i = 0; i < X::A_LOADS; i++) {
-            if constexpr (ABF16) {
-                *reinterpret_cast<u32x4 *>(as + adst[i]) = areg[set][i];
-            } else {
-                const f32x4 x = __builtin_bit_cast(f32x4, areg[set][i]);
-                uint2 w;
-                w.x = pack_bf16x2(x.x, x.y);
-                w.y = pack_bf16x2(x.z, x.w);
-                *reinterpret_cast<uint2 *>(as + adst[i]) = w;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < X::B_LOADS; i++)
-            *reinterpret_cast<u32x4 *>(bs + bdst[i]) = breg[set][i];
-    };
-
-    typedef float f32x16 __attribute__((ext_vector_type(16)));
-    f32x16 acc[X::TM][X::TN];
-#pragma unroll
-    for (int i = 0; i < X::TM; i++)
-#pragma unroll
-        for (int j = 0; j < X::TN; j++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[i][j][v] = 0.f;
-
-    // fragments double-buffered across k-steps: those of k-step t+1 are read
-    // while the MFMAs of k-step t run
-    auto compute = [&](auto SET) {
-        constexpr int set = decltype(SET)::value;
-        constexpr int KS = X::KSG;                               // this group's k-steps: kg KS ..
-        const unsigned char *as = set ? sa1 : sa0;
-        const unsigned char *bs = set ? sb1 : sb0;
-        bf16x8 fa[2][X::TM], fb[2][X::TN];
-        auto read = [&](int t, int f) {
-            const int ch = 2 * (kg * KS + t) + lk;
-#pragma unroll
-            for (int i = 0; i < X::TM; i++)
-                fa[f][i] = *reinterpret_cast<const bf16x8 *>(as + aoff[i] + ((ch ^ asw[i]) << 4));
-#pragma unroll
-            for (int j = 0; j < X::TN; j++)
-                fb[f][j] = *reinterpret_cast<const bf16x8 *>(bs + boff[j] + ((ch ^ bsw[j]) << 4));
-        };
-        read(0, 0);
-#pragma unroll
-        for (int t = 0; t < KS; t++) {
-            if (t + 1 < KS) read(t + 1, (t + 1) & 1);
-#pragma unroll
-            for (int i = 0; i < X::TM; i++)
-#pragma unroll
-                for (int j = 0; j < X::TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[t & 1][i], fb[t & 1][j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    // prologue: stage 0 stored, stage 1 (and with two sets stage 1 too)
-    // in flight
-    if constexpr (SETS == 3) {
-        load(0, IC<0>{});
-        if (nk > 1) load(1, IC<1>{});
-        if (nk > 2) load(2, IC<2>{});
-        store(IC<0>{}, IC<0>{});
-    } else if constexpr (SETS == 2) {
-        load(0, IC<0>{});
-        if (nk > 1) load(1, IC<1>{});
-        store(IC<0>{}, IC<0>{});
-    } else {
-        load(0, IC<0>{});
-        store(IC<0>{}, IC<0>{});
-        if (nk > 1) load(1, IC<0>{});
-    }
-    __syncthreads();
-
-    // steady state (it + 2 < nk): SET = it & 1 is the LDS slot of stage it.
-    // The loads are unconditional here (conditional loads make the
-    // compiler's wait analysis wait for all of them).
-    auto steady = [&](int it, auto SET) {
-        constexpr int set = decltype(SET)::value;
-        if constexpr (SETS == 2) {
-            load(it + 2, IC<set>{});
-            compute(IC<set>{});
-            store(IC<set ^ 1>{}, IC<set ^ 1>{});
-        } else {
-            store(IC<set ^ 1>{}, IC<0>{});
-            load(it + 2, IC<0>{});
-            compute(IC<set>{});
-        }
-        XlSched<0, X::MFMAS, X::KSG, X::TM + X::TN, X::LOADS, SETS == 1>::run();
-        __syncthreads();
-    };
-    auto tail = [&](int it, auto SET) {
-        constexpr int set = decltype(SET)::value;
-        if constexpr (SETS == 2) {
-            if (it + 2 < nk) load(it + 2, IC<set>{});
-            compute(IC<set>{});
-            if (it + 1 < nk) store(IC<set ^ 1>{}, IC<set ^ 1>{});
-        } else {
-            if (it + 1 < nk) store(IC<set ^ 1>{}, IC<0>{});
-            if (it + 2 < nk) load(it + 2, IC<0>{});
-            compute(IC<set>{});
-        }
-        __syncthreads();
-    };
-    // three register sets (SETS = 3): stage it + 3 is loaded while stage it
-    // is computed, so three stages are in flight; R = it mod 6 fixes the LDS
-    // slot (R & 1) and the register sets (R mod 3 loaded, R + 1 mod 3 stored)
-    auto steady3 = [&](int it, auto R) {
-        constexpr int r = decltype(R)::value;
-        load(it + 3, IC<r % 3>{});
-        compute(IC<r & 1>{});
-        store(IC<(r + 1) & 1>{}, IC<(r + 1) % 3>{});
-        XlSched<0, X::MFMAS, X::KSG, X::TM + X::TN, X::LOADS, false>::run();
-        __syncthreads();
-    };
-    auto tail3 = [&](int it, auto R) {
-        constexpr int r = decltype(R)::value;
-        if (it + 3 < nk) load(it + 3, IC<r % 3>{});
-        compute(IC<r & 1>{});
-        if (it + 1 < nk) store(IC<(r + 1) & 1>{}, IC<(r + 1) % 3>{});
-        __syncthreads();
-    };
-    int it = 0;
-    if constexpr (SETS == 3) {
-        for (; it + 8 < nk; it += 6) {
-            steady3(it, IC<0>{});
-            steady3(it + 1, IC<1>{});
-            steady3(it + 2, IC<2>{});
-            steady3(it + 3, IC<3>{});
-            steady3(it + 4, IC<4>{});
-            steady3(it + 5, IC<5>{});
-        }
-        // at most 8 stages left, it a multiple of 6
-        tail3(it, IC<0>{});
-        if (it + 1 < nk) tail3(it + 1, IC<1>{});
-        if (it + 2 < nk) tail3(it + 2, IC<2>{});
-        if (it + 3 < nk) tail3(it + 3, IC<3>{});
-        if (it + 4 < nk) tail3(it + 4, IC<4>{});
-        if (it + 5 < nk) tail3(it + 5, IC<5>{});
-        if (it + 6 < nk) tail3(it + 6, IC<0>{});
-        if (it + 7 < nk) tail3(it + 7, IC<1>{});
-    } else {
-        for (; it + 3 < nk; it += 2) {
-            steady(it, IC<0>{});
-            steady(it + 1, IC<1>{});
-        }
-        // 1 to 3 stages left, it even
-        tail(it, IC<0>{});
-        if (it + 1 < nk) tail(it + 1, IC<1>{});
-        if (it + 2 < nk) tail(it + 2, IC<0>{});
-    }
-
-    // two wave groups: the second adds its sums into the first's through LDS
-    if constexpr (KG == 2) {
-        __shared__ float xred[(X::NT / 2) * X::TM * X::TN * 16];
-        __syncthreads();
-        if (kg == 1) {
-#pragma unroll
-            for (int i = 0; i < X::TM; i++)
-#pragma unroll
-                for (int j = 0; j < X::TN; j++)
-#pragma unroll
-                    for (int v = 0; v < 16; v++) xred[(((wq * X::TM + i) * X::TN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
-        }
-        __syncthreads();
-        if (kg == 1) return;
-#pragma unroll
-        for (int i = 0; i < X::TM; i++)
-#pragma unroll
-            for (int j = 0; j < X::TN; j++)
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[i][j][v] += xred[(((wq * X::TM + i) * X::TN + j) * 16 + v) * 64 + lane];
-    }
-
-    // epilogue: value v of a 32x32 block sits at row 8*(v/4) + 4*(lane/32) + v%4,
-    // column lane%32
-#pragma unroll
-    for (int i = 0; i < X::TM; i++) {
-        const int rbase = m0 + wm * X::WTM + 32 * i + 4 * lk;
-        if constexpr (!GATED) {
-#pragma unroll
-            for (int j = 0; j < X::TN; j++) {
-                const int col = n0 + wn * X::WTN + 32 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int row = rbase + 8 * (v >> 2) + (v & 3);
-                        if (row < M) __builtin_nontemporal_store(acc[i][j][v], &c[(size_t)row * N + col]);
-                    }
-                }
-            }
-        } else {
-            constexpr int TNO = X::TN / 2;
-#pragma unroll
-            for (int j = 0; j < TNO; j++) {
-                const int col = n0 + wn * (X::BNO / X::WNW) + 32 * j + lrow;
-                if (col < N) {
-#pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const int row = rbase + 8 * (v >> 2) + (v & 3);
-                        if (row < M)
-                            __builtin_nontemporal_store(silu_mul(acc[i][j][v], acc[i][j + TNO][v]),
-                                                        &c[(size_t)row * N + col]);
-                    }
-                }
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// misc kernels
-// ---------------------------------------------------------------------------
-// dst[n][k] = src[tile(n,k)], tile-major as in kernels_ame.c:212-215,269
-__global__ void k_tile_to_row(uint16_t *__restrict__ dst, const uint16_t *__restrict__ src,
-                              int N, int K, int tn, int tk) {
-    const size_t total = (size_t)N * K;
-    const size_t ktiles = (size_t)(K / tk);
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const int n = (int)(i / K), k = (int)(i % K);
-        const size_t t = (size_t)(n / tn) * ktiles + (size_t)(k / tk);
-        dst[i] = src[t * (size_t)tn * tk + (size_t)(n % tn) * tk + (k % tk)];
-    }
-}
-
-// (value, index) argmax: larger value wins, ties -> lower index; NaN never
-// wins a comparison (matches the strict ">" scan of ops_scalar.c:57-62 except
-// that a NaN at index 0 is not returned when any value is ordered).
-__device__ __forceinline__ void am_merge(float &v, int &i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i) || (v != v && v2 == v2)) { v = v2; i = i2; }
-}
-
-__global__ __launch_bounds__(NTHREADS) void k_argmax_partial(float *__restrict__ pv,
-                                                            int *__restrict__ pi,
-                                                            const float *__restrict__ v, int n) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int i = blockIdx.x * NTHREADS + threadIdx.x; i < n; i += gridDim.x * NTHREADS)
-        am_merge(bv, bi, v[i], i);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        float ov = __shfl_xor(bv, m);
-        int oi = __shfl_xor(bi, m);
-        am_merge(bv, bi, ov, oi);
-    }
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) { sv[wave] = bv; si[wave] = bi; }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++) am_merge(bv, bi, sv[w], si[w]);
-        pv[blockIdx.x] = bv;
-        pi[blockIdx.x] = bi;
-    }
-}
-
-__global__ __launch_bounds__(WAVE) void k_argmax_final(int *__restrict__ out,
-                                                      const float *__restrict__ pv,
-                                                      const int *__restrict__ pi, int np,
-                                                      const float *__restrict__ v) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < np; i += WAVE) am_merge(bv, bi, pv[i], pi[i]);
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        float ov = __shfl_xor(bv, m);
-        int oi = __shfl_xor(bi, m);
-        am_merge(bv, bi, ov, oi);
-    }
-    // the reference's scan starts from v[0]; a NaN there is never beaten
-    if (threadIdx.x == 0) out[0] = (bi == 0x7FFFFFFF || v[0] != v[0]) ? 0 : bi;
-}
-
-// plain 16-byte-vector copy: a kernel of known traffic (bytes read = bytes
-// written = n16 * 16) against which HBM traffic counters are calibrated
-__global__ __launch_bounds__(NTHREADS) void k_copy16(u32x4 *__restrict__ dst,
-                                                    const u32x4 *__restrict__ src, size_t n16) {
-    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n16;
-         i += (size_t)gridDim.x * NTHREADS)
-        dst[i] = __builtin_nontemporal_load(src + i);
-}
-
-// dst[i] = bf16 RNE of src[i]; 8 elements per lane per step (n % 8 == 0,
-// 16-byte aligned src and dst)
-__global__ __launch_bounds__(NTHREADS) void k_cvt_bf16(uint16_t *__restrict__ dst,
-                                                       const float *__restrict__ src, size_t n8) {
-    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n8; i += (size_t)gridDim.x * NTHREADS) {
-        const f32x4 x0 = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src) + 2 * i);
-        const f32x4 x1 = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(src) + 2 * i + 1);
-        u32x4 w;
-        w.x = pack_bf16x2(x0.x, x0.y);
-        w.y = pack_bf16x2(x0.z, x0.w);
-        w.z = pack_bf16x2(x1.x, x1.y);
-        w.w = pack_bf16x2(x1.z, x1.w);
-        reinterpret_cast<u32x4 *>(dst)[i] = w;
-    }
-}
-
-__global__ __launch_bounds__(NTHREADS) void k_fill_zero(float *__restrict__ c, size_t n) {
-    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n;
-         i += (size_t)gridDim.x * NTHREADS)
-        c[i] = 0.0f;
-}
-
-// ---------------------------------------------------------------------------
-// Weight-streaming MFMA GEMM for 5 <= M <= 64 (small decode batches)
-// ---------------------------------------------------------------------------
-// For M <= 64 the weights are almost all of the traffic, and the tile kernels
-// above keep too few of their bytes in flight per CU to stream them at HBM
-// rate.  Here a block of 8 waves owns 16-row tiles of B (the weights) and a
-// K slice of 256*KS (blockIdx.y picks the slice).  Wave w owns k range
-// [slice + 32*KS*w, +32*KS): it holds its A fragments (MT m-tiles of 16 rows,
-// rounded to bf16 RNE) in registers for the whole kernel and loads its B
-// fragments straight from memory into registers, ST tiles ahead, with
-// v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand = weights).
-// Lane (r, g) = (lane % 16, lane / 16) holds k = 32s + 8g .. 32s + 8g + 7 of
-// step s for row r of both operands.  The 8 partial tiles are summed through
-// LDS in wave order (one barrier per tile, two LDS buffers).  Blocks walk
-// tiles blockIdx.x, +gridDim.x, ... so one launch of <= 256 blocks streams any
-// N.  Every load is an unconditional buffer load: rows past N and tiles past
-// a block's last one read at an offset beyond the buffer, which returns zeros
-// and touches no memory, so the loop has no branches around its loads.
-// part == nullptr: C (or silu(gate)*up) is written; otherwise the fp32 sums
-// of slice ks go to part[ks][j][M][N] (j = 0, or gate/up for GATED) and
-// k_stream_reduce adds the slices in order.
-#define STREAM_THREADS 512
-
-template <int MT, int KS, int ST, bool GATED>
-__global__ __launch_bounds__(STREAM_THREADS, 1) void k_gemm_stream(float *__restrict__ c,
-                                                                float *__restrict__ part,
-                                                                const float *__restrict__ a,
-                                                                const uint16_t *__restrict__ b,
-                                                                const uint16_t *__restrict__ b2,
-                                                                int M, int K, int N, int ntiles) {
-    constexpr int NJ = GATED ? 2 : 1;
-    constexpr int SLOTS = MT * NJ;                       // f32x4 accumulators per lane
-    __shared__ f32x4 red[2][STREAM_THREADS / WAVE][SLOTS][WAVE];
-
-    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    const int r16 = lane & 15, g = lane >> 4;
-    const int kw0 = blockIdx.y * (256 * KS) + w * (32 * KS) + 8 * g;     // this lane's first k
-    const int first = blockIdx.x, stride = gridDim.x;
-    const int nmine = first < ntiles ? (ntiles - 1 - first) / stride + 1 : 0;
-    if (nmine == 0) return;                              // uniform over the block
-
-    // ---- A fragments: the fp32 loads go out first, then the first B tiles'
-    //      loads (below), and only then is A rounded (loads complete in order,
-    //      so waiting for A does not wait for B): one memory round trip
-    //      before the first MFMA instead of two
-    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
-    u32x4 alo[MT][KS], ahi[MT][KS];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int m = 16 * mt + r16;
-        const uint32_t off = m < M ? (uint32_t)(((size_t)m * K + kw0) * 4) : BUF_OOB;
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            alo[mt][s] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 128 * s, 0, 0);
-            ahi[mt][s] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 128 * s + 16, 0, 0);
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    bf16x8 af[MT][KS];                                   // rounded after the B loads below
-
-    // ---- B fragments: ST tiles in flight
-    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
-    u32x4 bq[ST][NJ][KS];
-    auto boff = [&](int i) -> uint32_t {                  // byte offset of this lane's row of tile i
-        const int n = 16 * (first + stride * i) + r16;
-        return (i < nmine && n < N) ? (uint32_t)(((size_t)n * K + kw0) * 2) : BUF_OOB;
-    };
-    auto load = [&](u32x4 (&q)[NJ][KS], int i) {
-        const uint32_t off = boff(i);
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            q[0][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off + 64 * s, 0, 0);
-            if constexpr (GATED) q[1][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off + 64 * s, 0, 0);
-        }
-    };
-
-    const size_t MN = (size_t)M * N;
-    auto tile = [&](const u32x4 (&q)[NJ][KS], int i) {
-        f32x4 acc[NJ][MT];
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KS; s++)
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const bf16x8 bf = __builtin_bit_cast(bf16x8, q[j][s]);
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt][s], bf, acc[j][mt], 0, 0, 0);
-            }
-        const int buf = i & 1;
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) red[buf][w][j * MT + mt][lane] = acc[j][mt];
-        __syncthreads();
-        // thread q < 64*MT sums slot (mt, lane p) over the 8 waves in order:
-        // rows 16*mt + 4*(p/16) + 0..3, column 16*tile + p%16
-        const int t = threadIdx.x;
-        if (t < WAVE * MT) {
-            const int mt = t / WAVE, p = t % WAVE;
-            f32x4 sum[NJ];
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                sum[j] = red[buf][0][j * MT + mt][p];
-#pragma unroll
-                for (int v = 1; v < STREAM_THREADS / WAVE; v++) sum[j] += red[buf][v][j * MT + mt][p];
-            }
-            const int n = 16 * (first + stride * i) + (p & 15);
-            const int m0 = 16 * mt + 4 * (p >> 4);
-            if (n < N) {
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = m0 + r;
-                    if (m < M) {
-                        const size_t o = (size_t)m * N + n;
-                        if (part) {
-                            float *pp = part + (size_t)blockIdx.y * NJ * MN + o;
-                            pp[0] = sum[0][r];
-                            if constexpr (GATED) pp[MN] = sum[1][r];
-                        } else if constexpr (GATED) {
-                            c[o] = silu_mul(sum[0][r], sum[1][r]);
-                        } else {
-                            c[o] = sum[0][r];
-                        }
-                    }
-                }
-            }
-        }
-    };
-
-#pragma unroll
-    for (int d = 0; d < ST; d++) load(bq[d], d);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            u32x4 p;
-            p.x = pack_bf16x2(__uint_as_float(alo[mt][s].x), __uint_as_float(alo[mt][s].y));
-            p.y = pack_bf16x2(__uint_as_float(alo[mt][s].z), __uint_as_float(alo[mt][s].w));
-            p.z = pack_bf16x2(__uint_as_float(ahi[mt][s].x), __uint_as_float(ahi[mt][s].y));
-            p.w = pack_bf16x2(__uint_as_float(ahi[mt][s].z), __uint_as_float(ahi[mt][s].w));
-            af[mt][s] = __builtin_bit_cast(bf16x8, p);
-        }
-    for (int base = 0; base < nmine; base += ST) {
-#pragma unroll
-        for (int d = 0; d < ST; d++) {
-            if (base + d < nmine) tile(bq[d], base + d);     // uniform over the block
-            load(bq[d], base + d + ST);
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Skinny GEMM for M <= 64 with small N (batched-decode projections)
-// ---------------------------------------------------------------------------
-// C[M,N] = A[M,K]·B[N,K]^T with A short: blockIdx.x owns 64 rows of B (four
-// waves, 16 rows each), blockIdx.y a K slice of KSL (a multiple of 64, at
-// most 256) and blockIdx.z a slab of 64 rows of A and C.  The block stages its slice of A once in LDS as bf16 (RNE), rows
-// of 16-byte chunks XOR-swizzled by row, so that the four waves read their
-// v_mfma_f32_16x16x32_bf16 A fragments from one copy instead of each block
-// re-reading A per 16-row tile; each wave issues all of its B loads before
-// the staging wait, so the weight stream is in flight while A is converted.
-// The weights are loaded in row order (8 rows x 128 contiguous bytes per
-// instruction) and pass through the wave's own LDS rows; straight into
-// registers in the MFMA fragment order (16 rows x 64 bytes per instruction)
-// they took longer (measured on MI355X, graph-replayed: 16 x {3072, 4096} x
-// 1024 6.53 / 6.81 -> 6.14 / 6.41 us, 64 x 3072 x 1024 10.3 -> 9.2, 48 x
-// 2048 x 1024 9.06 -> 8.26; 8 x 2048 x 1024 5.73 -> 5.84).  No cross-wave
-// reduction: a wave
-// owns its 16 output columns.  With more than one slice the fp32 sums go to
-// part[slice][j][M][N] (j = gate/up when GATED) and k_stream_reduce adds the
-// slices in order; otherwise C (or silu(gate)*up) is written directly.
-// Loads past M and past N are buffer loads at out-of-range offsets (zeros).
-template <int MT, bool GATED>
-__global__ __launch_bounds__(NTHREADS) void k_gemm_skinny(float *__restrict__ c, float *__restrict__ part,
-                                                          const float *__restrict__ a,
-                                                          const uint16_t *__restrict__ b,
-                                                          const uint16_t *__restrict__ b2,
-                                                          int M, int K, int N, int ksl) {
-    constexpr int NJ = GATED ? 2 : 1;
-    constexpr int KSMAX = 256 / 32;                      // 32-deep steps per slice, at most
-    __shared__ __align__(16) u32x4 sa[MT * 16 * (256 / 8)];   // [row][chunk ^ swz(row)], bf16
-    __shared__ __align__(16) u32x4 sbw[NTHREADS / WAVE][NJ * 16 * 32];   // each wave's weight rows
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int r16 = lane & 15, g = lane >> 4;
-    const int k0 = blockIdx.y * ksl;
-    const int m0 = blockIdx.z * 64;                    // this block's 64-row slab of A and C
-    const int ncs = ksl >> 3;                           // 16-byte chunks per row of the slice
-    const int nst = ksl >> 5;                           // 32-deep steps
-
-    // 1. the block's A slice first (8 floats per chunk, CPT chunks per
-    //    thread; chunks past the slice or rows past M read zeros) ...
-    constexpr int CPT = MT * 16 * (256 / 8) / NTHREADS;
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * K * 4);
-    const int total = MT * 16 * ncs;                     // chunks of the staged slice
-    u32x4 alo[CPT], ahi[CPT];
-#pragma unroll
-    for (int i = 0; i < CPT; i++) {
-        const int q = tid + NTHREADS * i;
-        const int m = q / ncs, ch = q % ncs;
-        const uint32_t off = (q < total && m0 + m < M) ? (uint32_t)(((size_t)(m0 + m) * K + k0 + 8 * ch) * 4)
-                                                         : BUF_OOB;
-        alo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-        ahi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, off + 16, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 2. ... then this wave's B chunks: row n of its 16, k = k0 + 32 s + 8 g
-    //    (in flight while A is converted; loads complete in order, so a wait
-    //    for A does not wait for these)
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * K * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
-    const int n = blockIdx.x * 64 + w * 16 + r16;
-    // in row order: load s covers rows 8 (s % 2) + lane / 8 of the wave's 16,
-    // chunks 8 (s / 2) + lane % 8 of the slice (8 rows x 128 bytes)
-    u32x4 bq[NJ][KSMAX];
-#pragma unroll
-    for (int s = 0; s < KSMAX; s++) {
-        const int row = 8 * (s & 1) + (lane >> 3), ch = 8 * (s >> 1) + (lane & 7);
-        const int nr = blockIdx.x * 64 + w * 16 + row;
-        const uint32_t off = (ch < ncs && nr < N) ? (uint32_t)(((size_t)nr * K + k0 + 8 * ch) * 2) : BUF_OOB;
-        bq[0][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
-        if constexpr (GATED) bq[1][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // the A slice -> LDS as bf16 (RNE), 16-byte chunks XOR-swizzled by row
-#pragma unroll
-    for (int i = 0; i < CPT; i++) {
-        const int q = tid + NTHREADS * i;
-        const int m = q / ncs, ch = q % ncs;
-        u32x4 v;
-        v.x = pack_bf16x2(__uint_as_float(alo[i].x), __uint_as_float(alo[i].y));
-        v.y = pack_bf16x2(__uint_as_float(alo[i].z), __uint_as_float(alo[i].w));
-        v.z = pack_bf16x2(__uint_as_float(ahi[i].x), __uint_as_float(ahi[i].y));
-        v.w = pack_bf16x2(__uint_as_float(ahi[i].z), __uint_as_float(ahi[i].w));
-        if (q < total) sa[m * ncs + (ch ^ (m & 7))] = v;
-    }
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int s = 0; s < KSMAX; s++) {
-            const int row = 8 * (s & 1) + (lane >> 3), ch = 8 * (s >> 1) + (lane & 7);
-            sbw[w][(j * 16 + row) * 32 + (ch ^ (row & 15))] = bq[j][s];
-        }
-    __syncthreads();
-
-    // 3. MFMA over the slice: A fragment rows 16 mt + r16, chunk 4 s + g
-    f32x4 acc[NJ][MT];
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) acc[j][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSMAX; s++) {
-        if (s < nst) {                                   // uniform
-            bf16x8 af[MT];
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const int m = 16 * mt + r16;
-                af[mt] = __builtin_bit_cast(bf16x8, sa[m * ncs + ((4 * s + g) ^ (m & 7))]);
-            }
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const bf16x8 bf = __builtin_bit_cast(bf16x8, sbw[w][(j * 16 + r16) * 32 + ((4 * s + g) ^ (r16 & 15))]);
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bf, acc[j][mt], 0, 0, 0);
-            }
-        }
-    }
-
-    // 4. lane holds rows 16 mt + 4 g + r, column n
-    if (n < N) {
-        const size_t MN = (size_t)M * N;
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + 16 * mt + 4 * g + r;
-                if (m < M) {
-                    const size_t o = (size_t)m * N + n;
-                    if (part) {
-                        float *pp = part + (size_t)blockIdx.y * NJ * MN + o;
-                        pp[0] = acc[0][mt][r];
-                        if constexpr (GATED) pp[MN] = acc[1][mt][r];
-                    } else if constexpr (GATED) {
-                        c[o] = silu_mul(acc[0][mt][r], acc[1][mt][r]);
-                    } else {
-                        c[o] = acc[0][mt][r];
-                    }
-                }
-            }
-    }
-}
-
-// C = sum over the KSPLIT slices of part, in slice order (gated: silu(gate)*up).
-// Four outputs per thread; the loads of every slice (at most RMAX) go out
-// before the first add, so the pass costs one memory round trip, not one per
-// slice.  Requires MN % 4 == 0 and 16-byte aligned c and part (else the
-// scalar tail below handles the last MN % 4).
-#define RMAX 16
-template <bool GATED>
-__global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ c,
-                                                            const float *__restrict__ part,
-                                                            size_t MN, int ksplit) {
-    constexpr int NJ = GATED ? 2 : 1;
-    const __amdgpu_buffer_rsrc_t rp = buf_rsrc(part, (size_t)ksplit * NJ * MN * 4);
-    const size_t n4 = MN / 4;
-    for (size_t i = (size_t)blockIdx.x * NTHREADS + threadIdx.x; i < n4; i += (size_t)gridDim.x * NTHREADS) {
-        f32x4 v[NJ][RMAX];
-#pragma unroll
-        for (int ks = 0; ks < RMAX; ks++)
-#pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                const size_t e = ((size_t)ks * NJ + j) * MN + 4 * i;     // element offset
-                v[j][ks] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rp, ks < ksplit && e * 4 < 0x80000000ull ? (uint32_t)(e * 4) : BUF_OOB, 0, 0));
-            }
-        f32x4 s0 = v[0][0], s1 = GATED ? v[NJ - 1][0] : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 1; ks < RMAX; ks++)
-            if (ks < ksplit) {
-                s0 += v[0][ks];
-                if constexpr (GATED) s1 += v[1][ks];
-            }
-        f32x4 o = s0;
-        if constexpr (GATED) o = f32x4{silu_mul(s0.x, s1.x), silu_mul(s0.y, s1.y), silu_mul(s0.z, s1.z), silu_mul(s0.w, s1.w)};
-        if (((uintptr_t)c & 15) == 0) {
-            reinterpret_cast<f32x4 *>(c)[i] = o;
-        } else {                                     // C only 4-byte aligned
-            c[4 * i] = o.x; c[4 * i + 1] = o.y; c[4 * i + 2] = o.z; c[4 * i + 3] = o.w;
-        }
-    }
-    if (blockIdx.x == 0 && threadIdx.x < MN % 4) {       // tail
-        const size_t i = n4 * 4 + threadIdx.x;
-        float t0 = part[i], t1 = GATED ? part[MN + i] : 0.f;
-        for (int ks = 1; ks < ksplit; ks++) {
-            t0 += part[(size_t)ks * NJ * MN + i];
-            if constexpr (GATED) t1 += part[(size_t)ks * NJ * MN + MN + i];
-        }
-        c[i] = GATED ? silu_mul(t0, t1) : t0;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Narrow GEMM for M <= 64 and K-heavy shapes (o, down of a decode batch)
-// ---------------------------------------------------------------------------
-// blockIdx.y owns 32 columns of C (two 16-column MFMA tiles; with GATED the
-// same columns of both weights), blockIdx.z a slab of ROWS = 16 MT rows and
-// blockIdx.x a K slice of KSL = 128 * KPW (slice-major, so with a multiple
-// of 8 slices each XCD reads one slice of A).  Every thread issues all of its
-// loads at once: the block's slice of A first (from L2), then its wave's
-// weights (from HBM); the slice is rounded to bf16 (RNE) into LDS (16-byte
-// chunks XOR-swizzled by row) while the weights are in flight.  Where the
-// block's LDS also holds them (even KPW), the weights are loaded in row order
-// -- every instruction 8 rows x 128 contiguous bytes -- and pass through the
-// wave's own LDS rows, instead of straight into registers in the MFMA
-// fragment order (16 rows x 64 bytes per instruction; measured on MI355X,
-// graph-replayed, M = 64: q 4.9 -> 4.25 us, q|k|v 5.74 -> 5.6, k/v 5.88 ->
-// 5.62, o 6.66 -> 6.49, down 7.39 -> 7.25; M = 128 k/v 4.4 -> 4.05, q 5.5 ->
-// 5.05).  The four
-// waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
-// their partial tiles are added through LDS (reusing the A slice's space) in
-// wave order.  With one slice the block writes C (silu(gate) * up when
-// GATED).  With several, each block writes its slice sums [slice][j][M][N]
-// with agent-scope (write-through) stores, waits for them, and takes a ticket
-// from its tile's counter; the block that draws the last ticket reads every
-// slice's sums (agent-scope loads), adds them in slice order --
-// deterministic, whatever the arrival order -- writes C and resets the
-// counter to zero for the next call.  No block waits for another and there
-// is no second launch.  Loads past M and N read zeros at out-of-range
-// offsets.
-#define NARROW_COLS 32                // the widest column block (NCOL); 16 is the other
-template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
-                                                            unsigned *__restrict__ cnt,
-                                                            const float *__restrict__ a,
-                                                            const uint16_t *__restrict__ b,
-                                                            const uint16_t *__restrict__ b2, int M, int K, int N) {
-    constexpr int NJ = GATED ? 2 : 1;
-    constexpr int KSL = 128 * KPW, CH = KSL / 8;         // slice depth, 16-byte chunks per row
-    constexpr int NT = NCOL / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
-    constexpr int RSTRIDE = NCOL + 4;                     // +4: conflict-free column writes, 16-byte aligned rows
-    constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * RSTRIDE / 4;
-    static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
-    __shared__ __align__(16) u32x4 smem[SA_U4 > RED_U4 ? SA_U4 : RED_U4];
-    // weights in row order through per-wave LDS rows where they fit
-    constexpr int BR = NJ * NT * 16, CW = 4 * KPW;        // a wave's weight rows, 16-byte chunks per row
-    constexpr bool BROW = KPW % 2 == 0 &&
-        ((SA_U4 > RED_U4 ? SA_U4 : RED_U4) + NW * BR * CW) * 16 + 64 <= 160 * 1024;
-    constexpr int BSW = CW % 16 == 0 ? 15 : 7;            // row swizzle within a row's chunks
-    __shared__ __align__(16) u32x4 sbw[BROW ? NW * BR * CW : 1];
-    u32x4 *const sa = smem;                               // the A slice, then
-    float *const red = reinterpret_cast<float *>(smem);   // [wave][j][row][RSTRIDE] wave partials
-    __shared__ unsigned last_s;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int r16 = lane & 15, g = lane >> 4;
-    const int k0 = blockIdx.x * KSL, ks = gridDim.x;
-    const int n0 = blockIdx.y * NCOL, m0 = blockIdx.z * ROWS;
-    const size_t MN = (size_t)M * N;
-
-    // 1. every load at once: first the block's A slice (rows past M read
-    //    zeros; it comes from L2), then this wave's weights (rows
-    //    n0 + 16 nt + r16, k = k0 + 32 (KPW w + s) + 8 g; from HBM), so that the
-    //    slice is rounded into LDS while the weights are still in flight
-    constexpr int PER = ROWS * CH / NTHREADS;             // 32-byte pieces of A per thread
-    // Where A's pieces and the weights together would pass 48 loads in
-    // flight (the 16-wide blocks with one 3072-deep slice), A comes in two
-    // halves: the second is loaded once the first is in LDS, while the
-    // weights are still on their way from HBM.
-    constexpr int PA = (2 * PER + NJ * NT * KPW > 48) ? (PER + 1) / 2 : PER;
-    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PA + NJ * NT * KPW <= 64, "loads in flight");
-    const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
-    u32x4 lo[PA], hi[PA];
-    auto load_a = [&](int i, int slot) {                  // piece i into register slot
-        const int q = tid + NTHREADS * i;
-        const int m = m0 + q / CH, ch = q % CH;
-        const uint32_t off = (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4);
-        lo[slot] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
-        hi[slot] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off + 16u : BUF_OOB, 0, 0);
-    };
-#pragma unroll
-    for (int i = 0; i < PA; i++) load_a(i, i);
-    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = xl_rsrc(GATED ? b2 : b, (size_t)N * K * 2);
-    u32x4 bq[NJ][NT][KPW];
-    if constexpr (BROW) {
-        // load i: rows 8 (i % (BR / 8)) + lane / 8 of the wave's BR rows (Wg rows,
-        // then Wu rows), chunks 8 (i / (BR / 8)) + lane % 8: 8 rows x 128 bytes
-        u32x4 *const flat = &bq[0][0][0];
-#pragma unroll
-        for (int i = 0; i < NJ * NT * KPW; i++) {
-            const int row = 8 * (i % (BR / 8)) + (lane >> 3), ch = 8 * (i / (BR / 8)) + (lane & 7);
-            const int j = row / (NT * 16), n = n0 + row % (NT * 16);
-            const uint32_t off = n < N ? (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * ch) * 2) : BUF_OOB;
-            flat[i] = __builtin_amdgcn_raw_buffer_load_b128(j ? rb2 : rb, off, 0, 2);
-        }
-    } else {                                              // fragment order: rows n0 + 16 nt + r16
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int n = n0 + 16 * nt + r16;
-            const uint32_t base = (uint32_t)(((size_t)n * K + k0 + 32 * KPW * w + 8 * g) * 2);
-#pragma unroll
-            for (int s = 0; s < KPW; s++) {
-                const uint32_t off = n < N ? base + 64u * s : BUF_OOB;
-                bq[0][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 2);
-                if constexpr (GATED) bq[NJ - 1][nt][s] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, 2);
-            }
-        }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 *const sbwave = sbw + (BROW ? w * BR * CW : 0);
-    if constexpr (BROW) {
-        const u32x4 *const flat = &bq[0][0][0];
-#pragma unroll
-        for (int i = 0; i < NJ * NT * KPW; i++) {
-            const int row = 8 * (i % (BR / 8)) + (lane >> 3), ch = 8 * (i / (BR / 8)) + (lane & 7);
-            sbwave[row * CW + (ch ^ (row & BSW))] = flat[i];
-        }
-    }
-
-    // 2. A rounded to bf16 (RNE) into LDS (the second half, if any, loaded
-    //    and rounded after the first)
-    auto store_a = [&](int i, int slot) {
-        const int q = tid + NTHREADS * i;
-        const int m = q / CH, ch = q % CH;
-        u32x4 v;
-        v.x = pack_bf16x2(__uint_as_float(lo[slot].x), __uint_as_float(lo[slot].y));
-        v.y = pack_bf16x2(__uint_as_float(lo[slot].z), __uint_as_float(lo[slot].w));
-        v.z = pack_bf16x2(__uint_as_float(hi[slot].x), __uint_as_float(hi[slot].y));
-        v.w = pack_bf16x2(__uint_as_float(hi[slot].z), __uint_as_float(hi[slot].w));
-        sa[m * CH + (ch ^ (m & 15))] = v;
-    };
-#pragma unroll
-    for (int i = 0; i < PA; i++) store_a(i, i);
-    if constexpr (PA < PER) {
-#pragma unroll
-        for (int i = PA; i < PER; i++) load_a(i, i - PA);
-#pragma unroll
-        for (int i = PA; i < PER; i++) store_a(i, i - PA);
-    }
-    __syncthreads();
-
-    // 3. MFMA over this wave's steps: A fragment rows 16 mt + r16, chunk 4 (KPW w + s) + g
-    f32x4 acc[NJ][NT][MT];
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[j][nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KPW; s++) {
-        bf16x8 af[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const int m = 16 * mt + r16;
-            af[mt] = __builtin_bit_cast(bf16x8, sa[m * CH + ((4 * (KPW * w + s) + g) ^ (m & 15))]);
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-#pragma unroll
-            for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                {
-                    u32x4 wf;
-                    if constexpr (BROW) {
-                        const int row = (j * NT + nt) * 16 + r16, ch = 4 * s + g;
-                        wf = sbwave[row * CW + (ch ^ (row & BSW))];
-                    } else {
-                        wf = bq[j][nt][s];
-                    }
-                    acc[j][nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        af[mt], __builtin_bit_cast(bf16x8, wf), acc[j][nt][mt], 0, 0, 0);
-                }
-    }
-    __syncthreads();                                      // every wave is done reading the A slice
-
-    // 4. wave partials -> LDS: lane holds rows 16 mt + 4 g + r, column 16 nt + r16
-#pragma unroll
-    for (int j = 0; j < NJ; j++)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    red[((w * NJ + j) * ROWS + 16 * mt + 4 * g + r) * RSTRIDE + 16 * nt + r16] =
-                        acc[j][nt][mt][r];
-    __syncthreads();
-
-    // 5. quads of 4 columns, q = tid + NTHREADS i: row m0 + q / QR, columns
-    //    4 (q % QR) .. +3 (QR = NCOL / 4 quads per row), summed over the
-    //    waves in order; N % 4 == 0, so a quad is wholly in or out
-    constexpr int QR = NCOL / 4;
-    constexpr int NQ = ROWS * QR, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
-    static_assert(NQ % NTHREADS == 0 || NQ < NTHREADS, "quads per thread");
-    f32x4 v[NJ][QPT];
-    uint32_t coff[QPT];                                   // byte offset of the quad in C, or BUF_OOB
-#pragma unroll
-    for (int i = 0; i < QPT; i++) {
-        const bool live = tid + NTHREADS * i < NQ;        // MT = 1: half of the threads
-        const int q = live ? tid + NTHREADS * i : 0;
-        const int m = q / QR, cq = 4 * (q % QR), n = n0 + cq;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            f32x4 t = *reinterpret_cast<const f32x4 *>(&red[(j * ROWS + m) * RSTRIDE + cq]);
-#pragma unroll
-            for (int ww = 1; ww < NW; ww++)
-                t += *reinterpret_cast<const f32x4 *>(&red[((ww * NJ + j) * ROWS + m) * RSTRIDE + cq]);
-            v[j][i] = t;
-        }
-        coff[i] = (live && m0 + m < M && n < N) ? (uint32_t)(((size_t)(m0 + m) * N + n) * 4) : BUF_OOB;
-    }
-    auto finish = [&](const f32x4 &x, const f32x4 &y) -> u32x4 {
-        if constexpr (GATED)
-            return __builtin_bit_cast(u32x4, f32x4{silu_mul(x[0], y[0]), silu_mul(x[1], y[1]),
-                                                   silu_mul(x[2], y[2]), silu_mul(x[3], y[3])});
-        else
-            return __builtin_bit_cast(u32x4, x);
-    };
-    const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, MN * 4);
-    if (ks == 1) {
-#pragma unroll
-        for (int i = 0; i < QPT; i++)
-            __builtin_amdgcn_raw_buffer_store_b128(finish(v[0][i], v[NJ - 1][i]), rc, coff[i], 0, 0);
-        return;
-    }
-    // 6. slice sums out (write-through, agent scope), then a ticket; the last
-    //    block adds the slices
-    const __amdgpu_buffer_rsrc_t rp = xl_rsrc(part, (size_t)ks * NJ * MN * 4);
-    const uint32_t j_bytes = (uint32_t)(MN * 4), sl_bytes = NJ * j_bytes;
-#pragma unroll
-    for (int i = 0; i < QPT; i++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(u32x4, v[j][i]), rp,
-                coff[i] == BUF_OOB ? BUF_OOB : coff[i] + blockIdx.x * sl_bytes + j * j_bytes, 0, AUX_SC1);
-    __builtin_amdgcn_s_waitcnt(0);                        // this thread's sums have landed
-    __syncthreads();                                      // ... and every thread's
-    unsigned *const tick = cnt + blockIdx.z * gridDim.y + blockIdx.y;
-    if (tid == 0)
-        last_s = __hip_atomic_fetch_add(tick, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)ks - 1u;
-    __syncthreads();
-    if (!last_s) return;                                  // uniform over the block
-    f32x4 sum[NJ][QPT];
-#pragma unroll
-    for (int i = 0; i < QPT; i++)
-#pragma unroll
-        for (int j = 0; j < NJ; j++)
-            sum[j][i] = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           rp, coff[i] == BUF_OOB ? BUF_OOB : coff[i] + j * j_bytes, 0, AUX_SC1));
-    for (int sl0 = 1; sl0 < ks; sl0 += 8) {               // 8 slices of every quad in flight, added in order
-        u32x4 t[NJ][QPT][8];
-#pragma unroll
-        for (int i = 0; i < QPT; i++)
-#pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-                    t[j][i][u] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rp, (coff[i] == BUF_OOB || sl0 + u >= ks)
-                                ? BUF_OOB : coff[i] + (uint32_t)(sl0 + u) * sl_bytes + j * j_bytes,
-                        0, AUX_SC1);
-#pragma unroll
-        for (int i = 0; i < QPT; i++)
-#pragma unroll
-            for (int j = 0; j < NJ; j++)
-#pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (sl0 + u < ks) sum[j][i] += __builtin_bit_cast(f32x4, t[j][i][u]);
-    }
-#pragma unroll
-    for (int i = 0; i < QPT; i++)
-        __builtin_amdgcn_raw_buffer_store_b128(finish(sum[0][i], sum[NJ - 1][i]), rc, coff[i], 0, 0);
-    if (tid == 0) __hip_atomic_store(tick, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---------------------------------------------------------------------------
-// Wide GEMM for M <= 64 and very wide N (the tied lm_head of a decode batch)
-// ---------------------------------------------------------------------------
-// One block per CU, four independent waves.  The block's 16 MT rows of A sit
-// in LDS as bf16 for the whole launch (RNE; 16-byte chunks XOR-swizzled by
-// row); each wave walks its own 32-column tiles (DEF = 0: tile t = wave + j
-// waves)
-// over the whole of K, in chunks of 64 k.  A chunk's weights -- 32 rows x
-// 128 bytes -- are read with every load instruction covering 8 rows x 128
-// contiguous bytes (the MFMA fragment order, 16 rows x 64 bytes per
-// instruction, streams about 15% slower from HBM), passed through the wave's
-// own 4 KB of LDS, and read back as 16x16x32 MFMA fragments.  WIDE_D chunks
-// are in flight per wave; no block or wave waits for another.  Loads past N
-// read zeros at out-of-range offsets; rows past M are zeros in LDS.
-// DEF > 0 (every wave has at most DEF tiles, as for the 151,936-column
-// lm_head): wave gw takes the DEF consecutive tiles from DEF gw, holds each
-// finished tile's sums in registers and writes them all after its last one,
-// so that C goes out in rows of DEF x 128 contiguous bytes after the weight
-// stream instead of interleaved with it (measured on MI355X, graph-replayed,
-// 64 / 32 / 8 x 1024 x 151936: 66.0 / 58.9 / 50.7 -> 59.6 / 52.0 / 47.8 us;
-// holding the tiles but keeping the strided tile order: 64.2 / 54.8 / 48.9).
-#define WIDE_KC 64            // k per chunk
-#define WIDE_D 4              // chunks in flight per wave (K / WIDE_KC must be a multiple)
-#define WIDE_A_BYTES (128 * 1024)
-#define WIDE_B_U4 (32 * WIDE_KC / 8)   // 16-byte chunks of one wave's staged weights
-__device__ __forceinline__ int wide_key(int row) { return (row ^ (row >> 3)) & 7; }
-
-template <int MT, int NCH, int DEF>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_wide(float *__restrict__ c, const float *__restrict__ a,
-                                                          const uint16_t *__restrict__ b, int M, int N,
-                                                          int ntiles) {
-    extern __shared__ __align__(16) u32x4 wide_lds[];
-    constexpr int ROWS = 16 * MT, NW = NTHREADS / WAVE, K = NCH * WIDE_KC, CHA = K / 8;
-    static_assert(NCH % WIDE_D == 0 && CHA % 16 == 0 && ROWS * CHA * 16 <= WIDE_A_BYTES, "wide geometry");
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    const int r16 = lane & 15, g = lane >> 4;
-    u32x4 *const sa = wide_lds;                            // [ROWS][CHA] A, swizzled
-    u32x4 *const sb = wide_lds + ROWS * CHA + w * WIDE_B_U4;   // this wave's staged chunk
-    const int gw = blockIdx.x * NW + w, nwaves = gridDim.x * NW;
-    // tiles of this wave: gw, gw + nwaves, ...; with DEF, the DEF consecutive
-    // tiles from gw DEF (their C rows then go out DEF x 128 contiguous bytes)
-    const int my_tiles = DEF > 0 ? min(max(ntiles - gw * DEF, 0), DEF)
-                                 : (gw < ntiles ? (ntiles - gw + nwaves - 1) / nwaves : 0);
-    auto tile_index = [&](int ti) { return DEF > 0 ? gw * DEF + ti : gw + ti * nwaves; };
-    const __amdgpu_buffer_rsrc_t rb = xl_rsrc(b, (size_t)N * K * 2);
-
-    // the loads of chunk kc of tile number ti (of this wave): instruction i
-    // covers rows 32 t + 8 i + lane / 8, bytes 128 kc + 16 (lane % 8)
-    // (32-bit offsets, N * K * 2 < 2^31; computed without branches so that
-    // every load is issued where it stands)
-    auto issue = [&](u32x4 (&dst)[4], int ti, int kc) {
-        const int t = tile_index(ti);
-        const bool live = ti < my_tiles;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int n = 32 * t + 8 * i + (lane >> 3);
-            const uint32_t off = ((uint32_t)n * K + WIDE_KC * kc + 8 * (lane & 7)) * 2u;
-            dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rb, (live && n < N) ? off : BUF_OOB, 0, 2);
-        }
-    };
-    u32x4 ring[WIDE_D][4];
-#pragma unroll
-    for (int d = 0; d < WIDE_D; d++) issue(ring[d], 0, d);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // A -> LDS once: rows past M read zeros
-    {
-        const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
-        constexpr int TOTAL = ROWS * CHA;
-#pragma unroll 1
-        for (int q0 = 0; q0 < TOTAL; q0 += 8 * NTHREADS) {
-            u32x4 lo[8], hi[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int q = q0 + tid + NTHREADS * i;
-                const int m = q / CHA, ch = q % CHA;
-                const bool ok = q < TOTAL && m < M;
-                const uint32_t off = (uint32_t)(((size_t)m * K + 8 * ch) * 4);
-                lo[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off : BUF_OOB, 0, 0);
-                hi[i] = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? off + 16u : BUF_OOB, 0, 0);
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int q = q0 + tid + NTHREADS * i;
-                const int m = q / CHA, ch = q % CHA;
-                u32x4 v;
-                v.x = pack_bf16x2(__uint_as_float(lo[i].x), __uint_as_float(lo[i].y));
-                v.y = pack_bf16x2(__uint_as_float(lo[i].z), __uint_as_float(lo[i].w));
-                v.z = pack_bf16x2(__uint_as_float(hi[i].x), __uint_as_float(hi[i].y));
-                v.w = pack_bf16x2(__uint_as_float(hi[i].z), __uint_as_float(hi[i].w));
-                if (q < TOTAL) sa[m * CHA + (ch ^ (m & 15))] = v;
-            }
-        }
-    }
-    __syncthreads();
-
-    // The tile out through the wave's staging space (see below)
-    auto store_half = [&](const f32x4 (&acc)[2][MT], int ti, const int h) {
-        // The tile out through the wave's staging space, 32 rows at a time, so
-        // that every store instruction writes 8 rows x 128 contiguous bytes
-        // (4-byte stores straight from the MFMA layout, 4 rows x 64 bytes per
-        // instruction, write back at well under half the speed).  Lane holds
-        // rows 16 mt + 4 g + r, column 16 nt + r16; LDS row-major [32][32]
-        // fp32 with the 16-byte chunk XOR-swizzled by row.
-        const int t = tile_index(ti);
-        float *const sc = reinterpret_cast<float *>(sb);
-        const __amdgpu_buffer_rsrc_t rc = xl_rsrc(c, (size_t)M * N * 4);
-        {
-#pragma unroll
-            for (int mh = 0; mh < 2 && 2 * h + mh < MT; mh++)
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const int row = 16 * mh + 4 * g + r, col = 16 * nt + r16;
-                        sc[row * 32 + ((((col >> 2) ^ (row & 7)) << 2) | (col & 3))] = acc[nt][2 * h + mh][r];
-                    }
-#pragma unroll
-            for (int i = 0; i < (MT >= 2 ? 4 : 2); i++) {
-                const int row = 8 * i + (lane >> 3), cq = lane & 7;
-                const f32x4 v = *reinterpret_cast<const f32x4 *>(&sc[row * 32 + ((cq ^ (row & 7)) << 2)]);
-                const int m = 32 * h + row, n = 32 * t + 4 * cq;
-                const uint32_t off = (m < M && n < N) ? (uint32_t)(((size_t)m * N + n) * 4) : BUF_OOB;
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rc, off, 0, 2);   // nt
-            }
-        }
-    };
-    auto store_tile = [&](const f32x4 (&acc)[2][MT], int ti) {
-#pragma unroll
-        for (int h = 0; h < (MT + 1) / 2; h++) store_half(acc, ti, h);
-    };
-    f32x4 held[DEF > 0 ? DEF : 1][2][MT];                 // finished tiles, written after the last one
-    // one iteration per tile, its NCH chunks unrolled: chunk kc always uses
-    // ring slot kc % WIDE_D, and the accumulators live inside the iteration
-    for (int ti = 0; ti < my_tiles; ti++) {
-        f32x4 acc[2][MT];
-#pragma unroll
-        for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < NCH; kc++) {
-            const int d = kc % WIDE_D;
-            // stage this chunk: row 8 i + lane / 8, chunk lane % 8 (swizzled)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int row = 8 * i + (lane >> 3);
-                sb[row * 8 + ((lane & 7) ^ wide_key(row))] = ring[d][i];
-            }
-            // refill the slot WIDE_D chunks ahead (into the next tile near the end)
-            if (kc + WIDE_D < NCH) issue(ring[d], ti, kc + WIDE_D);
-            else issue(ring[d], ti + 1, kc + WIDE_D - NCH);
-            __builtin_amdgcn_sched_barrier(0);            // keep the ring's order of issue
-            // two k-steps of 32: A rows 16 mt + r16, B rows 16 nt + r16, chunk 4 s + g
-#pragma unroll
-            for (int s = 0; s < 2; s++) {
-                const int ka = 4 * (WIDE_KC / 32 * kc + s) + g;         // chunk of A's row
-                bf16x8 af[MT], bfr[2];
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    const int m = 16 * mt + r16;
-                    af[mt] = __builtin_bit_cast(bf16x8, sa[m * CHA + (ka ^ (m & 15))]);
-                }
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++) {
-                    const int row = 16 * nt + r16;
-                    bfr[nt] = __builtin_bit_cast(bf16x8, sb[row * 8 + ((4 * s + g) ^ wide_key(row))]);
-                }
-#pragma unroll
-                for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
-                        acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr[nt], acc[nt][mt], 0, 0, 0);
-            }
-        }
-        if constexpr (DEF == 0) {
-            store_tile(acc, ti);
-        } else {
-#pragma unroll
-            for (int q = 0; q < DEF; q++)
-                if (q == ti) {
-#pragma unroll
-                    for (int nt = 0; nt < 2; nt++)
-#pragma unroll
-                        for (int mt = 0; mt < MT; mt++) held[q][nt][mt] = acc[nt][mt];
-                }
-        }
-    }
-    if constexpr (DEF > 0) {
-#pragma unroll
-        for (int h = 0; h < (MT + 1) / 2; h++)
-#pragma unroll
-            for (int q = 0; q < DEF; q++)
-                if (q < my_tiles) store_half(held[q], q, h);
-    }
-}
-
-// ---------------------------------------------------------------------------
-// 16-row GEMM for M <= 16 (small decode batches)
-// ---------------------------------------------------------------------------
-// blockIdx.x owns 16 CT columns of C (16 CT rows of B); the block's NWV waves
-// split K = KT (wave w: k range [w KW, (w + 1) KW)), each computing 16 x 16
-// tiles with v_mfma_f32_16x16x32_bf16 (A operand = activations, B operand =
-// weights), and the NWV tiles are added through LDS in wave order.  Each lane
-// issues all of its loads at once: its share of the wave's weights, then its
-// share of the wave's 16 x KW slice of A (fp32; rows past M read zeros) --
-// both in row order, every load instruction covering whole 128-byte lines (8
-// rows x 128 bytes of weights, 2 rows x 512 bytes of A at KW = 128).  Loading
-// A in the MFMA fragment order instead (16 rows x two 16-byte pieces 32 bytes
-// apart per instruction) made A the larger part of the kernel (measured on
-// MI355X, graph-replayed per call: 16 x 1024 x 3072 3.87 -> 3.01 us, 16 x
-// 2048 x 2048 5.74 -> 3.68, 8 x 1024 x 3072 3.24 -> 2.82).  Both pass through
-// the wave's own LDS rows (16-byte chunks XOR-swizzled by row; A rounded to
-// bf16 (RNE) on the way in) and come back as fragments; only the wave itself
-// reads its rows, so a wave-scope fence, not a block barrier, orders the
-// writes and reads.  Where the block's LDS does not hold weights and A side
-// by side (m16_asep false), the wave reads its weight fragments into
-// registers first and A then reuses the same rows.  Lane (r, g) =
-// (lane % 16, lane / 16) holds k = 32s + 8g .. 32s + 8g + 7 of step s for
-// row r of both operands.  Rows of B past N read zeros and their columns of C
-// are not stored.  GATED: the block's two tiles are the Wg and the Wu rows of
-// the same 16 columns (CT = 2), and C = silu(x Wg^T) * (x Wu^T).
-constexpr bool m16_asep(int nwv, int kt, int ct) {
-    return ct * 16 * kt * 2 + 16 * kt * 2 + nwv * ct * 16 * 17 * 4 <= 160 * 1024;
-}
-constexpr size_t m16_lds_bytes(int nwv, int kt, int ct) {   // weights, A (if separate), wave tiles
-    return (size_t)ct * 16 * kt * 2 + (m16_asep(nwv, kt, ct) ? (size_t)16 * kt * 2 : 0) +
-           (size_t)nwv * ct * 16 * 17 * 4;
-}
-template <int NWV, int KT, int CT, bool GATED = false>
-__global__ __launch_bounds__(NWV * WAVE) void k_gemm_m16(float *__restrict__ c, const float *__restrict__ a,
-                                                        const uint16_t *__restrict__ b,
-                                                        const uint16_t *__restrict__ b2, int M, int N) {
-    constexpr int KW = KT / NWV, CHW = KW / 8, STEPS = KW / 32, NBL = 16 * CHW / WAVE;
-    constexpr int PPR = KW / 4, APL = 16 * PPR / WAVE;   // 16-byte fp32 pieces of A per row / per lane
-    constexpr int SW = CHW >= 16 ? 15 : CHW - 1;           // swizzle mask: within the row's chunks
-    constexpr bool ASEP = m16_asep(NWV, KT, CT);
-    static_assert(KW * NWV == KT && CHW % 8 == 0 && NBL * WAVE == 16 * CHW && APL * WAVE == 16 * PPR &&
-                  NWV * WAVE >= 256 * CT && (!GATED || CT == 2), "k split");
-    constexpr int COLS = GATED ? 16 : 16 * CT;             // columns of C per block
-    // LDS: [NWV][CT][16][CHW] weights, [NWV][16][CHW] A if separate, [NWV][CT][16][17] fp32 tiles
-    extern __shared__ __align__(16) u32x4 m16_lds[];
-    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    const int r16 = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * COLS;
-    u32x4 *const sb = m16_lds + w * CT * 16 * CHW;
-    u32x4 *const sa = ASEP ? m16_lds + NWV * CT * 16 * CHW + w * 16 * CHW : sb;
-    float *const red = reinterpret_cast<float *>(m16_lds + NWV * CT * 16 * CHW + (ASEP ? NWV * 16 * CHW : 0));
-
-    // weights: load i of tile t covers rows 16 t + 8 (i % 2) + lane / 8 (GATED: rows
-    // 8 (i % 2) + lane / 8 of Wg for t = 0, of Wu for t = 1), chunks 8 (i / 2) + lane % 8
-    const __amdgpu_buffer_rsrc_t rb = buf_rsrc(b, (size_t)N * KT * 2);
-    const __amdgpu_buffer_rsrc_t rb2 = buf_rsrc(GATED ? b2 : b, (size_t)N * KT * 2);
-    u32x4 bw[CT][NBL];
-#pragma unroll
-    for (int t = 0; t < CT; t++)
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
-            const int n = n0 + (GATED ? 0 : 16 * t) + row;
-            const uint32_t off = n < N ? ((uint32_t)n * KT + w * KW + 8 * ch) * 2u : BUF_OOB;
-            bw[t][i] = __builtin_amdgcn_raw_buffer_load_b128(GATED && t ? rb2 : rb, off, 0, 0);
-        }
-    // A: piece q = j WAVE + lane is row q / PPR, floats 4 (q % PPR) .. + 3 of the wave's k range
-    const __amdgpu_buffer_rsrc_t ra = buf_rsrc(a, (size_t)M * KT * 4);
-    u32x4 ap[APL];
-#pragma unroll
-    for (int j = 0; j < APL; j++) {
-        const int q = j * WAVE + lane, row = q / PPR, pc = q % PPR;
-        const uint32_t off = row < M ? ((uint32_t)row * KT + w * KW + 4 * pc) * 4u : BUF_OOB;
-        ap[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    auto wave_sync = [] {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-    auto store_a = [&] {        // rounded to bf16, 8 bytes = half a 16-byte chunk per piece
-#pragma unroll
-        for (int j = 0; j < APL; j++) {
-            const int q = j * WAVE + lane, row = q / PPR, pc = q % PPR;
-            uint2 v;
-            v.x = pack_bf16x2(__uint_as_float(ap[j].x), __uint_as_float(ap[j].y));
-            v.y = pack_bf16x2(__uint_as_float(ap[j].z), __uint_as_float(ap[j].w));
-            *reinterpret_cast<uint2 *>(reinterpret_cast<unsigned char *>(sa + row * CHW + ((pc >> 1) ^ (row & SW))) +
-                                       8 * (pc & 1)) = v;
-        }
-    };
-#pragma unroll
-    for (int t = 0; t < CT; t++)
-#pragma unroll
-        for (int i = 0; i < NBL; i++) {
-            const int row = 8 * (i & 1) + (lane >> 3), ch = 8 * (i >> 1) + (lane & 7);
-            sb[(16 * t + row) * CHW + (ch ^ (row & SW))] = bw[t][i];
-        }
-    if constexpr (ASEP) store_a();
-    wave_sync();
-    bf16x8 bf[ASEP ? 1 : STEPS][CT];
-    if constexpr (!ASEP) {      // weight fragments to registers, then A into the same rows
-#pragma unroll
-        for (int s = 0; s < STEPS; s++)
-#pragma unroll
-            for (int t = 0; t < CT; t++)
-                bf[s][t] = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + ((4 * s + g) ^ (r16 & SW))]);
-        wave_sync();
-        store_a();
-        wave_sync();
-    }
-
-    f32x4 acc[CT];
-#pragma unroll
-    for (int t = 0; t < CT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < STEPS; s++) {
-        const int ch = 4 * s + g;
-        const bf16x8 af = __builtin_bit_cast(bf16x8, sa[r16 * CHW + (ch ^ (r16 & SW))]);
-#pragma unroll
-        for (int t = 0; t < CT; t++) {
-            bf16x8 wf;
-            if constexpr (ASEP) wf = __builtin_bit_cast(bf16x8, sb[(16 * t + r16) * CHW + (ch ^ (r16 & SW))]);
-            else wf = bf[s][t];
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, wf, acc[t], 0, 0, 0);
-        }
-    }
-    // lane (r, g) holds rows 4g .. 4g + 3 of C, column 16 t + r of the block's
-#pragma unroll
-    for (int t = 0; t < CT; t++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) red[((w * CT + t) * 16 + 4 * g + r) * 17 + r16] = acc[t][r];
-    __syncthreads();
-    if constexpr (GATED) {
-        if (threadIdx.x < 256) {
-            const int m = (threadIdx.x >> 4) & 15, col = threadIdx.x & 15;
-            float sg = red[m * 17 + col], su = red[(16 + m) * 17 + col];
-#pragma unroll
-            for (int v = 1; v < NWV; v++) {
-                sg += red[((v * 2) * 16 + m) * 17 + col];
-                su += red[((v * 2 + 1) * 16 + m) * 17 + col];
-            }
-            const int n = n0 + col;
-            if (m < M && n < N) c[(size_t)m * N + n] = silu_mul(sg, su);
-        }
-    } else if (threadIdx.x < 256 * CT) {
-        const int t = threadIdx.x >> 8, m = (threadIdx.x >> 4) & 15, col = threadIdx.x & 15;
-        float sum = red[(t * 16 + m) * 17 + col];
-#pragma unroll
-        for (int v = 1; v < NWV; v++) sum += red[((v * CT + t) * 16 + m) * 17 + col];
-        const int n = n0 + 16 * t + col;
-        if (m < M && n < N) c[(size_t)m * N + n] = sum;
-    }
-}
+// The kernels live in headers by family, all compiled into this unit:
+//   gemm_common.h      types, constants, bf16 / wave-reduction / SiLU helpers
+//   gemv_kernels.h     M = 1 decode GEMV (fused prologues), M <= 4, M <= 16
+//   tile_kernels.h     tiled MFMA GEMMs for M > 4: double-buffered tiles,
+//                      the global_load_lds ring, the large tiles
+//   misc_kernels.h     weight re-layout, A rounding, argmax, copies
+//   small_m_kernels.h  decode-batch GEMMs, 5 <= M <= 64: weight-streaming,
+//                      skinny, narrow, wide (lm_head), 16-row
+#include "gemm_common.h"
+#include "gemv_kernels.h"
+#include "tile_kernels.h"
+#include "misc_kernels.h"
+#include "small_m_kernels.h"
 
 // ---------------------------------------------------------------------------
 // host side of the shim
@@ -4391,3 +1681,4 @@ extern "C" int qh_gemv_pro(float *c, const qh_gemv_pro_t *p, const uint16_t *b, 
     pro.eps = p->eps;
     return launch_gemv1_t<true>(c, nullptr, b, b2, K, N, gated != 0, pro);
 }
+

@@ -104,7 +104,7 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_partner(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
 }
-// sum over the 64 lanes, the same bits in every lane (as wave_sum of hip_gemm.hip)
+// sum over the 64 lanes, the same bits in every lane (as wave_sum of gemm_common.h)
 __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_partner<0xB1>(x);
     x += dpp_partner<0x4E>(x);
