@@ -251,7 +251,7 @@ struct GemvPro {
 // the merge arithmetic after them.
 // KA: the activation row arrives already rounded to packed bf16 pairs in the
 // kernel arguments (ka: the kernel-argument segment, GemvKaRow first) -- the
-// host-pointer path's M = 1 calls with K <= 1024, which then need no copy of
+// host-pointer path's M = 1 calls with K <= 3072, which then need no copy of
 // A to the device before the GEMV.
 template <int ROWS, int CPL, bool GATED, bool PRO, bool MERGE, bool KA>
 __device__ __forceinline__ void gemv1_body(float *__restrict__ c, const float *__restrict__ a,
@@ -455,13 +455,16 @@ __global__ __launch_bounds__(NTHREADS) void k_gemv1(float *__restrict__ c,
     gemv1_body<ROWS, CPL, GATED, PRO, MERGE, false>(c, a, b, b2, K, N, pro, nullptr);
 }
 
-// the activation row of a KA launch: K <= 1024 bf16 values, zero past K
-// (first kernel argument, so it sits at offset 0 of the argument segment)
+// the activation row of a KA launch: K <= 512 CPL bf16 values (at least
+// 1024), zero past K (first kernel argument, so it sits at offset 0 of the
+// argument segment; 6 KB at K = 3072, within what gfx950 launches accept)
+template <int CPL>
 struct GemvKaRow {
-    uint32_t w[512];
+    static constexpr int WORDS = CPL <= 2 ? 512 : 256 * CPL;
+    uint32_t w[WORDS];
 };
 template <int ROWS, int CPL, bool GATED>
-__global__ __launch_bounds__(NTHREADS) void k_gemv1_ka(GemvKaRow row, float *__restrict__ c,
+__global__ __launch_bounds__(NTHREADS) void k_gemv1_ka(GemvKaRow<CPL> row, float *__restrict__ c,
                                                       const uint16_t *__restrict__ b,
                                                       const uint16_t *__restrict__ b2, int K, int N) {
     (void)row;   // read in place, through the argument segment

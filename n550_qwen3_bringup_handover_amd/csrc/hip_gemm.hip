@@ -608,43 +608,59 @@ static int launch_gemv1(float *c, const float *a, const uint16_t *b, const uint1
     return launch_gemv1_t<false>(c, a, b, b2, K, N, gated, GemvPro{});
 }
 
-// M = 1 with K <= 1024 (K % 8 == 0) and the activation row already rounded
-// to bf16 on the host (`row`: 1024 bf16 values, zero past K): the row goes
-// in the launch's kernel arguments, so nothing is copied to the device before
-// the GEMV.  Same kernel body, row choice and results as launch_gemv1_t.
+// M = 1 with K <= 3072 (K % 8 == 0) and the activation row already rounded
+// to bf16 on the host (`row`: max(1024, 512 CPL) bf16 values, zero past K):
+// the row goes in the launch's kernel arguments, so nothing is copied to the
+// device before the GEMV.  Same kernel body, row choice and results as
+// launch_gemv1_t.
 template <int ROWS, int CPL>
-static int launch_gemv1_ka(float *c, const GemvKaRow &row, const uint16_t *b, const uint16_t *b2, int K, int N) {
+static int launch_gemv1_ka(float *c, const uint16_t *row_bf16, const uint16_t *b, const uint16_t *b2, int K, int N) {
+    GemvKaRow<CPL> row;
+    memcpy(row.w, row_bf16, sizeof row.w);
     const int grid = (N + (NTHREADS / WAVE) * ROWS - 1) / ((NTHREADS / WAVE) * ROWS);
     const size_t lds = (size_t)(4 * WAVE * CPL + 8) * sizeof(uint32_t);
-    if (b2)
-        hipLaunchKernelGGL((k_gemv1_ka<ROWS, CPL, true>), dim3(grid), dim3(NTHREADS), lds, g_stream, row, c, b, b2,
-                           K, N);
-    else
+    if (b2) {
+        if constexpr (ROWS * CPL * 2 <= 16)
+            hipLaunchKernelGGL((k_gemv1_ka<ROWS, CPL, true>), dim3(grid), dim3(NTHREADS), lds, g_stream, row, c, b,
+                               b2, K, N);
+        else
+            return QH_EINVAL;
+    } else {
         hipLaunchKernelGGL((k_gemv1_ka<ROWS, CPL, false>), dim3(grid), dim3(NTHREADS), lds, g_stream, row, c, b,
                            nullptr, K, N);
+    }
     HCHECK(hipGetLastError(), QH_ELAUNCH);
     return QH_OK;
 }
+// cpl 5 and 6 run at most 2 rows per wave (launch_gemv1_t's <= 16 loads per lane)
+template <int ROWS>
+static int launch_gemv1_ka_cpl(int cpl, float *c, const uint16_t *row, const uint16_t *b, const uint16_t *b2, int K,
+                               int N) {
+    switch (cpl) {
+        case 1: return launch_gemv1_ka<ROWS, 1>(c, row, b, b2, K, N);
+        case 2: return launch_gemv1_ka<ROWS, 2>(c, row, b, b2, K, N);
+        case 3: return launch_gemv1_ka<ROWS, 3>(c, row, b, b2, K, N);
+        case 4: return launch_gemv1_ka<ROWS, 4>(c, row, b, b2, K, N);
+        case 5: if constexpr (ROWS <= 2) return launch_gemv1_ka<ROWS, 5>(c, row, b, b2, K, N); else return QH_EINVAL;
+        case 6: if constexpr (ROWS <= 2) return launch_gemv1_ka<ROWS, 6>(c, row, b, b2, K, N); else return QH_EINVAL;
+        default: return QH_EINVAL;
+    }
+}
 extern "C" int qh_gemv_ka(float *c, const uint16_t *row_bf16, const uint16_t *b, const uint16_t *b2, int K, int N) {
     if (!g_inited) return QH_ESTATE;
-    if (!c || !row_bf16 || !b || K <= 0 || K > 1024 || (K % 8) || N <= 0 || !aligned16(b) || (b2 && !aligned16(b2)))
+    if (!c || !row_bf16 || !b || K <= 0 || K > 3072 || (K % 8) || N <= 0 || !aligned16(b) || (b2 && !aligned16(b2)))
         return QH_EINVAL;
     if ((size_t)N * K * 2 >= (1ull << 31)) return QH_ETOOBIG;
-    GemvKaRow row;
-    memcpy(row.w, row_bf16, sizeof row.w);
     const int cpl = (K / 8 + WAVE - 1) / WAVE;
     const int per_row = b2 ? 2 * cpl : cpl;
     int rows = 4;
     while (rows > 1 && (long)(N + rows - 1) / rows < 4096) rows /= 2;
     while (rows > 1 && rows * per_row > 16) rows /= 2;
     g_last_plan = PLAN_GEMV;
-    switch (rows * 2 + (cpl - 1)) {
-        case 2: return launch_gemv1_ka<1, 1>(c, row, b, b2, K, N);
-        case 3: return launch_gemv1_ka<1, 2>(c, row, b, b2, K, N);
-        case 4: return launch_gemv1_ka<2, 1>(c, row, b, b2, K, N);
-        case 5: return launch_gemv1_ka<2, 2>(c, row, b, b2, K, N);
-        case 8: return launch_gemv1_ka<4, 1>(c, row, b, b2, K, N);
-        case 9: return launch_gemv1_ka<4, 2>(c, row, b, b2, K, N);
+    switch (rows) {
+        case 1: return launch_gemv1_ka_cpl<1>(cpl, c, row_bf16, b, b2, K, N);
+        case 2: return launch_gemv1_ka_cpl<2>(cpl, c, row_bf16, b, b2, K, N);
+        case 4: return launch_gemv1_ka_cpl<4>(cpl, c, row_bf16, b, b2, K, N);
         default: return QH_EINVAL;
     }
 }

@@ -128,9 +128,10 @@ int qh_gemv_pro(float *c_d, const qh_gemv_pro_t *pro, const uint16_t *b_d, const
 int qh_gemv_merge(float *c_d, const float *part_d, const uint16_t *b_d, int K, int N);
 
 /* M = 1 GEMV (b2: gated, silu(gate) * up) whose activation row is given on
- * the host already rounded to bf16 (row_bf16: 1024 values, zero past K) and
- * travels in the launch's kernel arguments: K <= 1024, K % 8 == 0.  c may be
- * pinned host memory; each element of c is written exactly once. */
+ * the host already rounded to bf16 (row_bf16: max(1024, K rounded up to a
+ * multiple of 512) values, zero past K) and travels in the launch's kernel
+ * arguments: K <= 3072, K % 8 == 0.  c may be pinned host memory; each
+ * element of c is written exactly once. */
 int qh_gemv_ka(float *c, const uint16_t *row_bf16, const uint16_t *b_d, const uint16_t *b2_d, int K, int N);
 
 /* device copy by a plain 16-byte-vector kernel (bytes % 16 == 0, 16-byte

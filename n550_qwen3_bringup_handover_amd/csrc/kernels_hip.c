@@ -420,6 +420,8 @@ static int grow(void **p, size_t *cap, size_t need) {
 }
 
 /* ---- the host-pointer GEMM path ------------------------------------------------------ */
+/* the longest activation row that travels in a GEMV's kernel arguments */
+#define KA_MAX_K 3072
 /* bf16 of an fp32 value, round to nearest even -- the device's conversion
  * (v_cvt_pk_bf16_f32) for every non-NaN input, which is the reference's
  * recipe (fpga_bringup/src/src/qwen3.h:31-37); a NaN stays a (quiet) NaN */
@@ -488,9 +490,9 @@ static int gemm_host(float *c, const float *a, const uint16_t *b, const uint16_t
 
     /* The GEMM writes C straight into pinned staging, which the host copies
      * out once the values are there.  A reaches the GEMM one of two ways:
-     *  - M = 1, K <= 1024 (q, k, v, gate|up, lm_head of a decode step): the
-     *    host rounds the row to bf16 and it travels in the GEMV launch's
-     *    kernel arguments -- one launch per call;
+     *  - M = 1, K <= 3072 (every GEMV of a decode step): the host rounds
+     *    the row to bf16 and it travels in the GEMV launch's kernel
+     *    arguments (up to 6 KB) -- one launch per call;
      *  - otherwise host -> pinned staging (memcpy) -> device by the
      *    library's copy kernel, on the same stream as the GEMM (a runtime
      *    copy from host memory adds a cross-engine wait to every call).
@@ -503,11 +505,12 @@ static int gemm_host(float *c, const float *a, const uint16_t *b, const uint16_t
     if ((rc = grow_host(&g_c_h, &g_c_hcap, cbytes))) return rc;
     const int poll = M == 1 && (size_t)N <= POLL_MAX_ELEMS;
     if (poll) arm_output(g_c_h, (size_t)N);
-    if (M == 1 && K <= 1024 && K % 8 == 0 && ((uintptr_t)bd & 15) == 0 && (!gated || ((uintptr_t)bd2 & 15) == 0) &&
-        (size_t)N * (size_t)K * 2 < ((size_t)1 << 31) && strcmp(qh_gemm_plan(M, K, N, gated), "gemv") == 0) {
-        uint16_t row[1024];
+    if (M == 1 && K <= KA_MAX_K && K % 8 == 0 && ((uintptr_t)bd & 15) == 0 &&
+        (!gated || ((uintptr_t)bd2 & 15) == 0) && (size_t)N * (size_t)K * 2 < ((size_t)1 << 31) &&
+        strcmp(qh_gemm_plan(M, K, N, gated), "gemv") == 0) {
+        uint16_t row[KA_MAX_K];                           /* what qh_gemv_ka reads: zero past K */
         bf16_rne_row(row, a, K);
-        memset(row + K, 0, (size_t)(1024 - K) * sizeof(uint16_t));
+        memset(row + K, 0, (size_t)(KA_MAX_K - K) * sizeof(uint16_t));
         rc = qh_gemv_ka((float *)g_c_h, row, bd, gated ? bd2 : NULL, K, N);
     } else {
         const size_t a16 = (abytes + 15) & ~(size_t)15;     /* the copy kernel moves 16-byte units */

@@ -694,9 +694,14 @@ def test_argmax_dev(n):
 
 @pytest.mark.parametrize("K,N,gated", [(1024, 2048, False), (1024, 1024, False), (1024, 3072, True), (1024, V, False),
                                        (1000, 300, False), (512, 777, True), (8, 64, False), (1032, 100, False),
-                                       (2048, 1024, False), (3072, 1024, False)])
+                                       (2048, 1024, False), (3072, 1024, False),
+                                       # the other kernel-argument row sizes (K up to 3072), 2 and 4
+                                       # rows per wave, gated past K = 1024, and K = 4096 (copied A)
+                                       (1288, 520, False), (1536, 12300, False), (1544, 520, False), (2056, 8200, False), (2560, 96, True),
+                                       (2048, 16384, False), (2048, 1000, True), (3064, 4104, False),
+                                       (3072, 3072, True), (4096, 1024, False)])
 def test_host_path_m1_matches_device_path(K, N, gated):
-    """M = 1 through the host-pointer ABI -- for K <= 1024 the row rounded to
+    """M = 1 through the host-pointer ABI -- for K <= 3072 the row rounded to
     bf16 on the host and passed in the GEMV's kernel arguments, completion
     seen in the pinned output -- bit-identical to the device-pointer entry
     point on the same data, including non-bf16-representable activations
