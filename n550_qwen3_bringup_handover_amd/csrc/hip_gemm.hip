@@ -1091,18 +1091,23 @@ static NarrowGeom narrow_geom(int M, int K, int N, bool gated) {
 static inline size_t narrow_part_bytes(const NarrowGeom &g, int M, int N, bool gated) {
     return g.ks > 1 ? (size_t)g.ks * (gated ? 2 : 1) * M * N * sizeof(float) : 0;
 }
-// the instantiated (mt, kpw, gated, ncol) combinations: loads in flight
-// within 64 (the 16-wide blocks' A in two halves past 48)
-template <int MT, int KPW, bool GATED, int NCOL>
+// the instantiated (mt, kpw, gated, ncol, waves) combinations: loads in
+// flight within 64.  The 16-wide blocks with a 3072-deep slice (geometry kpw
+// 24) run 8 waves of 12 steps each, the same K slice: A and the weights then
+// all go out at entry (24 A loads + 12 weight loads per lane; with 4 waves,
+// 48 + 24, A had to come in two halves).  Measured on MI355X, graph-replayed:
+// 64 x 3072 x 1024 6.51 -> 6.18 us; at kpw 8 and 16 (one phase either way)
+// 8 waves were no faster (64 x 2048 x 1024 4.40 -> 4.49 us), so those stay 4.
+template <int MT, int KPW, bool GATED, int NCOL, int NWV>
 constexpr bool narrow_ok() {
-    return NCOL == 16 ? (MT == 1 && !GATED && KPW % 8 == 0 && KPW <= 24)
-                      : 2 * MT * KPW + 2 * (GATED ? 2 : 1) * KPW <= 64;
+    return NCOL == 16 ? (MT == 1 && !GATED && ((NWV == 4 && (KPW == 8 || KPW == 16)) || (NWV == 8 && KPW == 12)))
+                      : NWV == 4 && 2 * MT * KPW + 2 * (GATED ? 2 : 1) * KPW <= 64;
 }
 
-template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS>
+template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS, int NWV = 4>
 static int launch_narrow_t(const Ws &ws, const NarrowGeom &g, float *c, const float *a, const uint16_t *b,
                            const uint16_t *b2, int M, int K, int N) {
-    if constexpr (!narrow_ok<MT, KPW, GATED, NCOL>()) {
+    if constexpr (!narrow_ok<MT, KPW, GATED, NCOL, NWV>()) {
         return QH_EINVAL;
     } else {
         const int ncb = (N + NCOL - 1) / NCOL;
@@ -1111,8 +1116,9 @@ static int launch_narrow_t(const Ws &ws, const NarrowGeom &g, float *c, const fl
             if (narrow_part_bytes(g, M, N, GATED) > ws.part_bytes || !ws.cnt) return QH_ETOOBIG;
             part = use_part(ws);
         }
-        hipLaunchKernelGGL((k_gemm_narrow<MT, KPW, GATED, NCOL>), dim3((unsigned)g.ks, (unsigned)ncb, (unsigned)g.slabs),
-                           dim3(NTHREADS), 0, g_stream, c, part, ws.cnt, a, b, b2, M, K, N);
+        hipLaunchKernelGGL((k_gemm_narrow<MT, KPW, GATED, NCOL, NWV>),
+                           dim3((unsigned)g.ks, (unsigned)ncb, (unsigned)g.slabs), dim3(64 * NWV), 0, g_stream, c,
+                           part, ws.cnt, a, b, b2, M, K, N);
         HCHECK(hipGetLastError(), QH_ELAUNCH);
         return QH_OK;
     }
@@ -1127,7 +1133,7 @@ static int launch_narrow(const Ws &ws, float *c, const float *a, const uint16_t 
         switch (g.kpw) {
             case 8: return launch_narrow_t<1, 8, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
             case 16: return launch_narrow_t<1, 16, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
-            case 24: return launch_narrow_t<1, 24, GATED, 16>(ws, g, c, a, b, b2, M, K, N);
+            case 24: return launch_narrow_t<1, 12, GATED, 16, 8>(ws, g, c, a, b, b2, M, K, N);   // 8 waves
             default: return QH_EINVAL;
         }
     }

@@ -360,10 +360,11 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // ---------------------------------------------------------------------------
 // Narrow GEMM for M <= 64 and K-heavy shapes (o, down of a decode batch)
 // ---------------------------------------------------------------------------
-// blockIdx.y owns 32 columns of C (two 16-column MFMA tiles; with GATED the
-// same columns of both weights), blockIdx.z a slab of ROWS = 16 MT rows and
-// blockIdx.x a K slice of KSL = 128 * KPW (slice-major, so with a multiple
-// of 8 slices each XCD reads one slice of A).  Every thread issues all of its
+// blockIdx.y owns NCOL = 32 or 16 columns of C (16-column MFMA tiles; with
+// GATED the same columns of both weights), blockIdx.z a slab of ROWS = 16 MT
+// rows and blockIdx.x a K slice of KSL = 32 * NWV * KPW for NWV waves of KPW
+// steps (slice-major, so with a multiple of 8 slices each XCD reads one
+// slice of A).  Every thread issues all of its
 // loads at once: the block's slice of A first (from L2), then its wave's
 // weights (from HBM); the slice is rounded to bf16 (RNE) into LDS (16-byte
 // chunks XOR-swizzled by row) while the weights are in flight.  Where the
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // fragment order (16 rows x 64 bytes per instruction; measured on MI355X,
 // graph-replayed, M = 64: q 4.9 -> 4.25 us, q|k|v 5.74 -> 5.6, k/v 5.88 ->
 // 5.62, o 6.66 -> 6.49, down 7.39 -> 7.25; M = 128 k/v 4.4 -> 4.05, q 5.5 ->
-// 5.05).  The four
+// 5.05).  The NWV
 // waves split the slice (wave w: KPW steps of 32 from k0 + 32 KPW w) and
 // their partial tiles are added through LDS (reusing the A slice's space) in
 // wave order.  With one slice the block writes C (silu(gate) * up when
@@ -386,15 +387,16 @@ __global__ __launch_bounds__(NTHREADS) void k_stream_reduce(float *__restrict__ 
 // is no second launch.  Loads past M and N read zeros at out-of-range
 // offsets.
 #define NARROW_COLS 32                // the widest column block (NCOL); 16 is the other
-template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS>
-__global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
+template <int MT, int KPW, bool GATED, int NCOL = NARROW_COLS, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV, 1) void k_gemm_narrow(float *__restrict__ c, float *__restrict__ part,
                                                             unsigned *__restrict__ cnt,
                                                             const float *__restrict__ a,
                                                             const uint16_t *__restrict__ b,
                                                             const uint16_t *__restrict__ b2, int M, int K, int N) {
     constexpr int NJ = GATED ? 2 : 1;
-    constexpr int KSL = 128 * KPW, CH = KSL / 8;         // slice depth, 16-byte chunks per row
-    constexpr int NT = NCOL / 16, ROWS = 16 * MT, NW = NTHREADS / WAVE;
+    constexpr int NTH = 64 * NWV, NW = NWV;              // threads and waves of a block
+    constexpr int KSL = 32 * NW * KPW, CH = KSL / 8;     // slice depth, 16-byte chunks per row
+    constexpr int NT = NCOL / 16, ROWS = 16 * MT;
     constexpr int RSTRIDE = NCOL + 4;                     // +4: conflict-free column writes, 16-byte aligned rows
     constexpr int SA_U4 = ROWS * CH, RED_U4 = NW * NJ * ROWS * RSTRIDE / 4;
     static_assert(CH % 16 == 0, "the row swizzle stays inside a row");
@@ -418,17 +420,17 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     //    zeros; it comes from L2), then this wave's weights (rows
     //    n0 + 16 nt + r16, k = k0 + 32 (KPW w + s) + 8 g; from HBM), so that the
     //    slice is rounded into LDS while the weights are still in flight
-    constexpr int PER = ROWS * CH / NTHREADS;             // 32-byte pieces of A per thread
+    constexpr int PER = ROWS * CH / NTH;             // 32-byte pieces of A per thread
     // Where A's pieces and the weights together would pass 48 loads in
     // flight (the 16-wide blocks with one 3072-deep slice), A comes in two
     // halves: the second is loaded once the first is in LDS, while the
     // weights are still on their way from HBM.
     constexpr int PA = (2 * PER + NJ * NT * KPW > 48) ? (PER + 1) / 2 : PER;
-    static_assert(PER >= 1 && ROWS * CH % NTHREADS == 0 && 2 * PA + NJ * NT * KPW <= 64, "loads in flight");
+    static_assert(PER >= 1 && ROWS * CH % NTH == 0 && 2 * PA + NJ * NT * KPW <= 64, "loads in flight");
     const __amdgpu_buffer_rsrc_t ra = xl_rsrc(a, (size_t)M * K * 4);
     u32x4 lo[PA], hi[PA];
     auto load_a = [&](int i, int slot) {                  // piece i into register slot
-        const int q = tid + NTHREADS * i;
+        const int q = tid + NTH * i;
         const int m = m0 + q / CH, ch = q % CH;
         const uint32_t off = (uint32_t)(((size_t)m * K + k0 + 8 * ch) * 4);
         lo[slot] = __builtin_amdgcn_raw_buffer_load_b128(ra, m < M ? off : BUF_OOB, 0, 0);
@@ -477,7 +479,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
     // 2. A rounded to bf16 (RNE) into LDS (the second half, if any, loaded
     //    and rounded after the first)
     auto store_a = [&](int i, int slot) {
-        const int q = tid + NTHREADS * i;
+        const int q = tid + NTH * i;
         const int m = q / CH, ch = q % CH;
         u32x4 v;
         v.x = pack_bf16x2(__uint_as_float(lo[slot].x), __uint_as_float(lo[slot].y));
@@ -545,18 +547,18 @@ __global__ __launch_bounds__(NTHREADS, 1) void k_gemm_narrow(float *__restrict__
                         acc[j][nt][mt][r];
     __syncthreads();
 
-    // 5. quads of 4 columns, q = tid + NTHREADS i: row m0 + q / QR, columns
+    // 5. quads of 4 columns, q = tid + NTH i: row m0 + q / QR, columns
     //    4 (q % QR) .. +3 (QR = NCOL / 4 quads per row), summed over the
     //    waves in order; N % 4 == 0, so a quad is wholly in or out
     constexpr int QR = NCOL / 4;
-    constexpr int NQ = ROWS * QR, QPT = NQ >= NTHREADS ? NQ / NTHREADS : 1;
-    static_assert(NQ % NTHREADS == 0 || NQ < NTHREADS, "quads per thread");
+    constexpr int NQ = ROWS * QR, QPT = NQ >= NTH ? NQ / NTH : 1;
+    static_assert(NQ % NTH == 0 || NQ < NTH, "quads per thread");
     f32x4 v[NJ][QPT];
     uint32_t coff[QPT];                                   // byte offset of the quad in C, or BUF_OOB
 #pragma unroll
     for (int i = 0; i < QPT; i++) {
-        const bool live = tid + NTHREADS * i < NQ;        // MT = 1: half of the threads
-        const int q = live ? tid + NTHREADS * i : 0;
+        const bool live = tid + NTH * i < NQ;        // MT = 1: half of the threads
+        const int q = live ? tid + NTH * i : 0;
         const int m = q / QR, cq = 4 * (q % QR), n = n0 + cq;
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
