@@ -814,7 +814,7 @@ def main():
                     "us_per_launch_graph_replay": round(d["us_per_launch"], 3),
                     "frac_graph_replay": round(d["hbm_frac"], 4),
                     "method": "frac = bytes_per_launch / rocprofv3 average duration / peak, from the committed "
-                              "profile when it was made from these kernel sources (sha256 of csrc/*.hip), else "
+                              "profile when it was made from these kernel sources (sha256 of the GPU sources), else "
                               "frac = frac_graph_replay = bytes_per_launch / graph-replay launch period / peak"}
     gemms = None if (args.no_extras or args.no_gemm_tables) else gemm_tables(g)
     if args.calibrate_copy:
