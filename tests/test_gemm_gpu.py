@@ -211,7 +211,7 @@ def test_skinny_kernel(M, K, N):
 NARROW_SHAPES = [(64, 2048, 1024), (64, 3072, 1024), (48, 2048, 1024), (16, 3072, 1024), (1, 3072, 1024),
                  (64, 4096, 2048), (64, 4096, 64), (7, 1152, 36), (33, 1024, 300), (64, 2048, 1000),
                  (5, 128, 100), (64, 1024, 20000), (128, 1024, 1024), (96, 3072, 1024), (256, 1024, 1000),
-                 (200, 2048, 520)]
+                 (200, 2048, 520), (33, 3072, 520), (64, 3072, 1000)]
 
 
 @pytest.mark.parametrize("gated", [False, True], ids=["plain", "gated"])
