@@ -20,30 +20,34 @@
 // path), issues the next stage's weight loads, then waits at the workgroup
 // barrier for the stage's input.
 //
-// Activations move between workgroups as 64-bit words {fp32 value, tag}
+// Activations leave the compute waves as 64-bit words {fp32 value, tag}
 // written with agent-scope (sc1) stores; the tag is the launch's epoch, so a
-// word is valid exactly when its tag matches and no flag, counter or cache
-// flush is needed (a 64-bit access is single-copy atomic).  Only the poller
-// wave polls: it reads every word of the stage's input with agent-scope
-// loads until all tags match (bounded: after PS_SPIN rounds it records an
-// error and goes on, so every wave always finishes), rounds the values to
-// bf16 (RNE) into an LDS buffer, and joins the barrier.  The compute waves'
-// memory counter then holds only weight loads, so waiting for one stage's
-// weights never waits for the input poll, and the poll never waits for the
-// weights.  LDS holds two input buffers: stage s reads buffer s % 2 while the
-// poller fills buffer (s + 1) % 2; one barrier per stage separates them.
+// word is valid exactly when its tag matches and no counter or cache flush
+// is needed (a 64-bit access is single-copy atomic).  Only the poller wave
+// of a workgroup waits for a stage's input (below); every wait is bounded:
+// after PS_SPIN rounds it records an error and goes on, so every wave always
+// finishes.  The input reaches an LDS buffer as bf16 pairs (RNE) and the
+// poller joins the barrier.  The compute waves' memory counter then holds
+// only weight loads, so waiting for one stage's weights never waits for the
+// input, and the poll never waits for the weights.  LDS holds two input
+// buffers: stage s reads buffer s % 2 while the poller fills buffer
+// (s + 1) % 2; one barrier per stage separates them.
 //
 // Relays: reading words that another XCD has just written is slow when all
 // 256 workgroups poll them (measured on MI355X: 2.2-3.1 us from the last
 // store to the median poll).  So the words cross the XCD boundary once per
 // XCD: at launch, the first PS_RELAYS workgroups on each XCD (an
 // agent-scope ticket per XCD, the XCD read from HW_REG_XCC_ID) become its
-// relays; relay r polls part r of every stage's words from the exchange and
-// stores them into its XCD's copy, and every workgroup of the XCD, relays
-// included, polls that copy (same tags, same agent-scope loads, served
-// inside the XCD).  Measured: the 112 layer GEMVs 412 -> 369 us with 8
-// relays per XCD (4: 373, 16: 368, 32: 373; per-call launches: ~350 us).
-// A workgroup that is on no relay's XCD, or a part no relay took, can only
+// relays.  Relay r polls part r of every stage's words from the exchange,
+// stores the part into its XCD's copy as packed bf16 pairs (the LDS format),
+// waits for those stores to be acknowledged by the XCD's L2 and then stores
+// the launch's epoch into its flag for the stage.  Every workgroup of the
+// XCD, relays included, polls the stage's PS_RELAYS flags (32 bytes) and
+// then reads the copy once -- all inside the XCD's L2.  Measured on MI355X,
+// the 112 layer GEMVs: 412 us with every workgroup polling the exchange,
+// 366-369 us with the relays' copies polled word by word (tagged), 332-333
+// us with flags and bf16 copies, against ~350 us as per-call launches.
+// A workgroup on an XCD with no relay, or a part no relay took, can only
 // make the bounded polls give up with the error flag set.
 //
 // Residency: the 256 workgroups must be resident together (each waits for
@@ -93,7 +97,8 @@ struct PersistArgs {
     uint64_t *xch;              // [layers][4][XCH_LD] exchange words
     unsigned *state;            // [0] epoch of the last launch, [1] error flags (1 = poll gave up),
                                 // [2] arrivals, [4 + x] relay tickets of XCD x
-    uint64_t *relay;            // [8 XCDs][PS_MAX_LAYERS][4][XCH_LD]: each XCD's copy of the exchange words
+    uint32_t *relay;            // [8 XCDs][PS_MAX_LAYERS * 4][XCH_LD / 2]: each XCD's copy, bf16 pairs
+    unsigned *flags;            // [8 XCDs][PS_MAX_LAYERS * 4][PS_RELAYS]: epoch of each relay part copied
     int layers;
 };
 
@@ -202,50 +207,18 @@ __device__ __forceinline__ void put_rows(float v, float *out, uint64_t *xch, int
 }
 
 // ---- poller wave -------------------------------------------------------------
-// Wait until all V words of src carry `tag` (agent-scope loads, two words
-// per 16-byte load), then store the values as bf16 pairs into act
-// (act[i] = {v[2i], v[2i+1]}).  Gives up after PS_SPIN rounds (error flag 1).
-template <int V>
-__device__ __forceinline__ void poll_input(const uint64_t *src, unsigned tag, uint32_t *act, unsigned *state,
-                                           int lane, bool &gave_up) {
-    constexpr int NL = V / 128;                 // 16-byte loads per lane
-    const __amdgpu_buffer_rsrc_t rs = rsrc(src, (size_t)V * 8);
-    u32x4 d[NL];
-#pragma unroll
-    for (int i = 0; i < NL; i++) d[i] = u32x4{0u, 0u, 0u, 0u};
-    uint32_t ready = 0;
-    const uint32_t all = (NL >= 32) ? 0xFFFFFFFFu : ((1u << NL) - 1u);
-    for (int spin = 0;; spin++) {
-#pragma unroll
-        for (int i = 0; i < NL; i++)
-            if (!(ready >> i & 1u))
-                d[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)(lane + WAVE * i) * 16u, 0, AUX_SC1);
-#pragma unroll
-        for (int i = 0; i < NL; i++)
-            if (d[i].y == tag && d[i].w == tag) ready |= 1u << i;
-        if (__all(ready == all)) break;
-        if (gave_up || spin >= PS_SPIN) {     // after one give-up, no more waiting in this launch
-            if (lane == 0) atomicOr(state + 1, 1u);
-            gave_up = true;
-            break;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NL; i++)
-        act[lane + WAVE * i] = pack_bf16x2(__uint_as_float(d[i].x), __uint_as_float(d[i].z));
-}
-
 #define PS_RELAYS 8                  // relay workgroups per XCD (of 32)
 #define PS_XCDS 8
 // relay part r: wait until the V / PS_RELAYS words of part r of src carry
-// `tag` (agent-scope loads, bounded as poll_input), then store them into dst
+// `tag` (agent-scope loads, two words per 16-byte load; bounded), store them
+// into dst as packed bf16 pairs (pair q of the part = words 2q, 2q+1, RNE),
+// wait for the stores, then store `tag` in flag[r]
 template <int V>
-__device__ __forceinline__ void relay_copy(const uint64_t *src, uint64_t *dst, unsigned tag, int r, unsigned *state,
-                                           int lane, bool &gave_up) {
+__device__ __forceinline__ void relay_copy(const uint64_t *src, uint32_t *dst, unsigned *flag, unsigned tag, int r,
+                                           unsigned *state, int lane, bool &gave_up) {
     constexpr int VP = V / PS_RELAYS, NL = (VP + 127) / 128;   // words of a part, 16-byte loads per lane
     static_assert(V % PS_RELAYS == 0 && VP % 2 == 0 && NL <= 32, "relay parts");
     const __amdgpu_buffer_rsrc_t rs = rsrc(src + (size_t)r * VP, (size_t)VP * 8);
-    const __amdgpu_buffer_rsrc_t rd = rsrc(dst + (size_t)r * VP, (size_t)VP * 8);
     u32x4 d[NL];
     uint32_t ready = 0;
 #pragma unroll
@@ -269,10 +242,41 @@ __device__ __forceinline__ void relay_copy(const uint64_t *src, uint64_t *dst, u
             break;
         }
     }
+    const __amdgpu_buffer_rsrc_t rd = rsrc(dst + (size_t)r * (VP / 2), (size_t)VP * 2);
 #pragma unroll
     for (int i = 0; i < NL; i++) {
-        const uint32_t off = (uint32_t)(lane + WAVE * i) * 16u;
-        if (off < (uint32_t)VP * 8u) __builtin_amdgcn_raw_buffer_store_b128(d[i], rd, off, 0, 0);
+        const uint32_t q = (uint32_t)(lane + WAVE * i);
+        if (q * 16u < (uint32_t)VP * 8u)
+            __builtin_amdgcn_raw_buffer_store_b32(pack_bf16x2(__uint_as_float(d[i].x), __uint_as_float(d[i].z)), rd,
+                                                  q * 4u, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);                // the wave's pairs are in the XCD's L2 ...
+    if (lane == 0)                                // ... before its flag
+        __builtin_amdgcn_raw_buffer_store_b32(tag, rsrc(flag, PS_RELAYS * 4), (uint32_t)r * 4u, 0, 0);
+}
+
+// V words' copy on this XCD: wait until the PS_RELAYS flags of the stage
+// carry `tag` (bounded), then read the V / 2 bf16 pairs into act
+template <int V>
+__device__ __forceinline__ void poll_copy(const uint32_t *src, const unsigned *flag, unsigned tag, uint32_t *act,
+                                          unsigned *state, int lane, bool &gave_up) {
+    for (int spin = 0;; spin++) {
+        const unsigned f =
+            lane < PS_RELAYS ? __hip_atomic_load(flag + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : tag;
+        if (__all(f == tag)) break;
+        if (gave_up || spin >= PS_SPIN) {
+            if (lane == 0) atomicOr(state + 1, 1u);
+            gave_up = true;
+            break;
+        }
+    }
+    constexpr int NQ = V / 8, NL = (NQ + WAVE - 1) / WAVE;   // 16-byte pieces of 4 pairs, per lane
+    const __amdgpu_buffer_rsrc_t rs = rsrc(src, (size_t)V * 2);
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        const int q = lane + WAVE * i;
+        if (q < NQ)
+            reinterpret_cast<u32x4 *>(act)[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)q * 16u, 0, AUX_SC1);
     }
 }
 
@@ -309,25 +313,29 @@ __global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p)
         // ---- poller: one input per stage, then the barrier -----------------
         bool gave_up = false;
         const int part = s_part;
-        uint64_t *const copy = p.relay + (size_t)s_xcd * PS_MAX_LAYERS * 4 * XCH_LD;
+        // this XCD's copy (bf16 pairs, XCH_LD / 2 per stage slot) and flags
+        uint32_t *const copy = p.relay + (size_t)s_xcd * PS_MAX_LAYERS * 4 * (XCH_LD / 2);
+        unsigned *const flags = p.flags + (size_t)s_xcd * PS_MAX_LAYERS * 4 * PS_RELAYS;
+        auto slot = [&](int si) { return copy + (size_t)si * (XCH_LD / 2); };
+        auto flag = [&](int si) { return flags + (size_t)si * PS_RELAYS; };
         for (int l = 0; l < p.layers; l++) {
-            const uint64_t *x = p.xch + (size_t)l * 4 * XCH_LD;      // the exchange words
-            uint64_t *xc = copy + (size_t)l * 4 * XCH_LD;            // this XCD's copy of them
+            const uint64_t *x = p.xch + (size_t)l * 4 * XCH_LD;      // the exchange words of layer l
+            const int si = 4 * l;                                     // slots si .. si+3: q, o, h, x
             if (l == 0) {
                 load_input(p.x0, act[0], lane);
             } else {                                                  // x of layer l-1
-                if (part >= 0) relay_copy<H_DIM>(x - XCH_LD, xc - XCH_LD, tag, part, p.state, lane, gave_up);
-                poll_input<H_DIM>(xc - XCH_LD, tag, act[0], p.state, lane, gave_up);
+                if (part >= 0) relay_copy<H_DIM>(x - XCH_LD, slot(si - 1), flag(si - 1), tag, part, p.state, lane, gave_up);
+                poll_copy<H_DIM>(slot(si - 1), flag(si - 1), tag, act[0], p.state, lane, gave_up);
             }
             __syncthreads();
-            if (part >= 0) relay_copy<Q_N>(x, xc, tag, part, p.state, lane, gave_up);                     // q
-            poll_input<Q_N>(xc, tag, act[1], p.state, lane, gave_up);
+            if (part >= 0) relay_copy<Q_N>(x, slot(si), flag(si), tag, part, p.state, lane, gave_up);     // q
+            poll_copy<Q_N>(slot(si), flag(si), tag, act[1], p.state, lane, gave_up);
             __syncthreads();
-            if (part >= 0) relay_copy<H_DIM>(x + XCH_LD, xc + XCH_LD, tag, part, p.state, lane, gave_up);  // o
-            poll_input<H_DIM>(xc + XCH_LD, tag, act[0], p.state, lane, gave_up);
+            if (part >= 0) relay_copy<H_DIM>(x + XCH_LD, slot(si + 1), flag(si + 1), tag, part, p.state, lane, gave_up);   // o
+            poll_copy<H_DIM>(slot(si + 1), flag(si + 1), tag, act[0], p.state, lane, gave_up);
             __syncthreads();
-            if (part >= 0) relay_copy<I_N>(x + 2 * XCH_LD, xc + 2 * XCH_LD, tag, part, p.state, lane, gave_up);   // h
-            poll_input<I_N>(xc + 2 * XCH_LD, tag, act[1], p.state, lane, gave_up);
+            if (part >= 0) relay_copy<I_N>(x + 2 * XCH_LD, slot(si + 2), flag(si + 2), tag, part, p.state, lane, gave_up);   // h
+            poll_copy<I_N>(slot(si + 2), flag(si + 2), tag, act[1], p.state, lane, gave_up);
             __syncthreads();
         }
     } else {
@@ -387,7 +395,8 @@ __global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p)
 // ---- host side ------------------------------------------------------------------
 static uint64_t *g_xch = nullptr;     // [PS_MAX_LAYERS][4][XCH_LD] exchange words
 static unsigned *g_state = nullptr;   // epoch, error flags, arrivals, relay tickets
-static uint64_t *g_relay = nullptr;   // [PS_XCDS] copies of the exchange words
+static uint32_t *g_relay = nullptr;   // [PS_XCDS] bf16 copies of the exchange words
+static unsigned *g_flags = nullptr;   // their relay flags
 static int g_ps_ok = 0;               // 1 = the device keeps the grid resident
 
 // at library init (device current): the exchange words start at tag 0,
@@ -400,8 +409,11 @@ extern "C" int qh_persist_init(void) {
               cus == PS_BLOCKS && nb >= 1;
     (void)hipGetLastError();
     const size_t xb = (size_t)PS_MAX_LAYERS * 4 * XCH_LD * sizeof(uint64_t);
+    const size_t fb = (size_t)PS_XCDS * PS_MAX_LAYERS * 4 * PS_RELAYS * sizeof(unsigned);
     if (hipMalloc((void **)&g_xch, xb) != hipSuccess || hipMalloc((void **)&g_state, 64) != hipSuccess ||
-        hipMalloc((void **)&g_relay, PS_XCDS * xb) != hipSuccess || hipMemset(g_relay, 0, PS_XCDS * xb) != hipSuccess ||
+        hipMalloc((void **)&g_relay, PS_XCDS * xb / 4) != hipSuccess ||
+        hipMemset(g_relay, 0, PS_XCDS * xb / 4) != hipSuccess ||
+        hipMalloc((void **)&g_flags, fb) != hipSuccess || hipMemset(g_flags, 0, fb) != hipSuccess ||
         hipMemset(g_xch, 0, xb) != hipSuccess || hipMemset(g_state, 0, 64) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         (void)hipGetLastError();
@@ -414,9 +426,11 @@ extern "C" void qh_persist_shutdown(void) {
     (void)hipFree(g_xch);
     (void)hipFree(g_state);
     (void)hipFree(g_relay);
+    (void)hipFree(g_flags);
     g_xch = nullptr;
     g_state = nullptr;
     g_relay = nullptr;
+    g_flags = nullptr;
     g_ps_ok = 0;
 }
 
@@ -438,6 +452,7 @@ extern "C" int qh_decode_persist(const uint16_t *const *w, const float *x0_d, fl
     a.xch = g_xch;
     a.state = g_state;
     a.relay = g_relay;
+    a.flags = g_flags;
     a.layers = layers;
     hipLaunchKernelGGL(k_decode_persist, dim3(PS_BLOCKS), dim3(PS_THREADS), 0, (hipStream_t)qh_stream(), a);
     return hipGetLastError() == hipSuccess ? QH_OK : QH_ELAUNCH;
