@@ -46,7 +46,9 @@
 // then reads the copy once -- all inside the XCD's L2.  Measured on MI355X,
 // the 112 layer GEMVs: 412 us with every workgroup polling the exchange,
 // 366-369 us with the relays' copies polled word by word (tagged), 332-333
-// us with flags and bf16 copies, against ~350 us as per-call launches.
+// us with flags and bf16 copies, 292-294 us when the relays' first poll of a
+// stage waits ~0.85 us (PS_PRE), 284 us with the weight prefetch paced
+// (PACE_*), against ~350 us as per-call launches.
 // A workgroup on an XCD with no relay, or a part no relay took, can only
 // make the bounded polls give up with the error flag set.
 //
@@ -84,6 +86,15 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #define OUT_LD 9216
 // per-layer exchange slots of XCH_LD words: q (2048), o (1024), h (3072), x (1024)
 #define XCH_LD 3072
+
+// s_sleep units between consecutive weight loads of a stage's prefetch (load_wts).
+// Measured on MI355X, the 112 layer GEMVs with the relays' first poll after
+// 24 units: 293 us unpaced, 289 / 286 / 286 us at 3 / 4 / 5 units everywhere,
+// 284 us at these (8 units everywhere: 319 us, the waves reach the barrier late)
+#define PACE_QKV 4
+#define PACE_O 3
+#define PACE_GU 5
+#define PACE_D 3
 
 #define PS_MAX_LAYERS 32
 struct PersistArgs {
@@ -140,13 +151,18 @@ __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f 
 // ---- compute waves -----------------------------------------------------------
 // Weights of ROWS consecutive rows (and the matching rows of b2 when GATED)
 // starting at row0, K = 512 * CPL: every row and chunk is in range (the
-// stage shapes divide evenly), so the loads are unconditional.
+// stage shapes divide evenly), so the loads are unconditional.  PACE s_sleep
+// units (64 clocks) separate consecutive loads: a stage's output exchange
+// queues behind the weight loads issued just after its stores (a relay's
+// one poll took 1.65 / 0.62 / 1.18 / 0.42 us after q, o, h and x, the time
+// to stream the 12.6 / 6.3 / 8.4 / 4.2 MB issued then), so the loads are
+// spread over the exchange instead of issued as one burst.
 template <int ROWS, int CPL, bool GATED>
 struct Wts {
     u32x4 v[GATED ? 2 * ROWS : ROWS][CPL];
 };
 
-template <int ROWS, int CPL, bool GATED>
+template <int ROWS, int CPL, bool GATED, int PACE>
 __device__ __forceinline__ void load_wts(Wts<ROWS, CPL, GATED> &w, const uint16_t *b, const uint16_t *b2, int row0,
                                          int nrows, int lane) {
     constexpr int K = 512 * CPL;
@@ -158,7 +174,11 @@ __device__ __forceinline__ void load_wts(Wts<ROWS, CPL, GATED> &w, const uint16_
         for (int j = 0; j < CPL; j++) {
             const uint32_t off = (uint32_t)(row0 + r) * (uint32_t)(K * 2) + (uint32_t)(lane + WAVE * j) * 16u;
             w.v[r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, AUX_NT);
-            if constexpr (GATED) w.v[ROWS + r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, AUX_NT);
+            if (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+            if constexpr (GATED) {
+                w.v[ROWS + r][j] = __builtin_amdgcn_raw_buffer_load_b128(rb2, off, 0, AUX_NT);
+                if (PACE > 0) __builtin_amdgcn_s_sleep(PACE);
+            }
         }
 }
 
@@ -209,6 +229,13 @@ __device__ __forceinline__ void put_rows(float v, float *out, uint64_t *xch, int
 // ---- poller wave -------------------------------------------------------------
 #define PS_RELAYS 8                  // relay workgroups per XCD (of 32)
 #define PS_XCDS 8
+// s_sleep units (64 clocks) a relay waits after the stage's barrier before
+// its first poll: polls that reach the words before their producers' stores
+// slow the exchange down.  Measured on MI355X, the 112 layer GEMVs with
+// unpaced weight loads: 333 us polling at once, 296 / 293 / 292 / 308 / 340
+// us after 8 / 16 / 32 / 48 / 64 units (sleeping between polls instead: 341
+// us); with the paced loads (PACE_*) 287 / 286 / 286 us after 20 / 24 / 28
+#define PS_PRE 24
 // relay part r: wait until the V / PS_RELAYS words of part r of src carry
 // `tag` (agent-scope loads, two words per 16-byte load; bounded), store them
 // into dst as packed bf16 pairs (pair q of the part = words 2q, 2q+1, RNE),
@@ -227,6 +254,7 @@ __device__ __forceinline__ void relay_copy(const uint64_t *src, uint32_t *dst, u
         if ((uint32_t)(lane + WAVE * i) * 16u >= (uint32_t)VP * 8u) ready |= 1u << i;
     }
     const uint32_t all = (NL >= 32) ? 0xFFFFFFFFu : ((1u << NL) - 1u);
+    __builtin_amdgcn_s_sleep(PS_PRE);
     for (int spin = 0;; spin++) {
 #pragma unroll
         for (int i = 0; i < NL; i++)
@@ -345,22 +373,22 @@ __global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p)
         Wts<1, 4, false> wb;    // o: row gw of 1024, K 2048
         Wts<3, 2, true> wc;     // gate|up: rows 3gw .. 3gw+2 of 3072, K 1024
         Wts<1, 6, false> wd;    // down: row gw of 1024, K 3072
-        load_wts(wa, p.w[0][0], nullptr, 4 * gw, QKV_N, lane);
+        load_wts<4, 2, false, 0>(wa, p.w[0][0], nullptr, 4 * gw, QKV_N, lane);
         for (int l = 0; l < p.layers; l++) {
             const uint16_t *const *wl = p.w[l];
             float *out = p.out + (size_t)l * OUT_LD;
             uint64_t *x = p.xch + (size_t)l * 4 * XCH_LD;
-            load_wts(wb, wl[1], nullptr, gw, H_DIM, lane);
+            load_wts<1, 4, false, PACE_O>(wb, wl[1], nullptr, gw, H_DIM, lane);
             __syncthreads();
             float v = gemv_rows(wa, act[0], lane);
             put_rows<4>(v, out + OUT_QKV, 4 * gw < Q_N ? x : nullptr, 4 * gw, tag, lane);
 
-            load_wts(wc, wl[2], wl[3], 3 * gw, I_N, lane);
+            load_wts<3, 2, true, PACE_GU>(wc, wl[2], wl[3], 3 * gw, I_N, lane);
             __syncthreads();
             v = gemv_rows(wb, act[1], lane);
             put_rows<1>(v, out + OUT_O, x + XCH_LD, gw, tag, lane);
 
-            load_wts(wd, wl[4], nullptr, gw, H_DIM, lane);
+            load_wts<1, 6, false, PACE_D>(wd, wl[4], nullptr, gw, H_DIM, lane);
             __syncthreads();
             v = gemv_rows(wc, act[0], lane);
             put_rows<3>(v, out + OUT_H, x + 2 * XCH_LD, 3 * gw, tag, lane);
@@ -370,7 +398,7 @@ __global__ __launch_bounds__(PS_THREADS, 1) void k_decode_persist(PersistArgs p)
             // the compiler counts the loads exactly and stage D waits for its
             // own weights only
             const bool more = l + 1 < p.layers;
-            load_wts(wa, p.w[more ? l + 1 : l][0], nullptr, 4 * gw, more ? QKV_N : 0, lane);
+            load_wts<4, 2, false, PACE_QKV>(wa, p.w[more ? l + 1 : l][0], nullptr, 4 * gw, more ? QKV_N : 0, lane);
             __syncthreads();
             v = gemv_rows(wd, act[1], lane);
             put_rows<1>(v, out + OUT_X, x + 3 * XCH_LD, gw, tag, lane);
