@@ -651,18 +651,20 @@ DECODE_PROFILE = "decode_gemv_set_kernel_trace.txt"
 
 # the headers hip_gemm.hip includes (its kernel families)
 GEMM_KERNEL_HEADERS = ("gemm_common.h", "gemv_kernels.h", "tile_kernels.h", "misc_kernels.h", "small_m_kernels.h")
+# the device headers of the model and persistent kernels
+MODEL_KERNEL_HEADERS = ("persist_common.h", "fp_pinned.h", "model_shim.h")
 
 
 def kernel_sources_digest():
     """sha256 over the library's GPU sources (csrc/*.hip, hip_shim.h and the
-    kernel headers hip_gemm.hip compiles, by name): a committed profile
+    kernel headers the .hip files compile, by name): a committed profile
     records the digest of the sources it was made from, so a profile of
     other kernels is not taken for these"""
     import glob
     import hashlib
     h = hashlib.sha256()
     csrc = os.path.join(ROOT, "n550_qwen3_bringup_handover_amd", "csrc")
-    headers = ["hip_shim.h"] + list(GEMM_KERNEL_HEADERS)
+    headers = ["hip_shim.h"] + list(GEMM_KERNEL_HEADERS) + list(MODEL_KERNEL_HEADERS)
     for path in sorted(glob.glob(os.path.join(csrc, "*.hip")) + [os.path.join(csrc, n) for n in headers]):
         h.update(os.path.basename(path).encode())
         with open(path, "rb") as f:

@@ -103,6 +103,21 @@ int qwen3_hip_model_timing(const qwen3_hip_model *model, double *prefill_ms, dou
  * launches (0); both compute the same thing. */
 int qwen3_hip_model_set_graph(qwen3_hip_model *model, int on);
 
+/* Decode steps with the 28 decoder layers as one persistent launch (1) or
+ * as five launches per layer (0, the default; QWEN3_HIP_MODEL_PERSIST=1 in
+ * the environment makes 1 the default); both give the same bits (no
+ * counterpart in the reference, which has no launches).  On MI355X the
+ * persistent launch measured 3% slower (1,720-1,750 against 1,780-1,805
+ * tok/s for 128 greedy steps after a 128-token prompt).  Turning it on where
+ * the device cannot keep the launch's 256 workgroups resident returns
+ * QWEN3_HIP_ENODEV.  qwen3_hip_model_persistent returns the mode. */
+int qwen3_hip_model_set_persistent(qwen3_hip_model *model, int on);
+int qwen3_hip_model_persistent(const qwen3_hip_model *model);
+/* Error flags raised by persistent decode launches since the last call
+ * (nonzero: a launch gave up waiting for another workgroup's outputs, and
+ * the tokens it produced are invalid); synchronises the device. */
+int qwen3_hip_model_persist_errors(qwen3_hip_model *model, unsigned *flags);
+
 /* Intermediate-activation dumps, as qwen3_set_dump (SRC/qwen3.h:166-178):
  * during qwen3_hip_model_forward the callback receives, in host memory and
  * under the reference's names, every tensor this forward materialises:

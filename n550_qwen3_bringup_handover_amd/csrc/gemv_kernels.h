@@ -6,6 +6,7 @@
 #define QH_GEMV_KERNELS_H
 
 #include "gemm_common.h"
+#include "fp_pinned.h"
 
 // ---------------------------------------------------------------------------
 // GEMV: M <= 4
@@ -366,7 +367,7 @@ __device__ __forceinline__ void gemv1_body(float *__restrict__ c, const float *_
         float ss = 0.0f;
 #pragma unroll
         for (int q = 0; q < QMAX; q++)
-            ss += xa[q].x * xa[q].x + xa[q].y * xa[q].y + xa[q].z * xa[q].z + xa[q].w * xa[q].w;
+            ss += sumsq4(xa[q].x, xa[q].y, xa[q].z, xa[q].w);
         ss = wave_sum(ss);
         if (lane == 0) sred[wave] = ss;
         if (pro.x_out && blockIdx.x == 0) {

@@ -153,6 +153,7 @@ extern "C" void qh_shutdown(void) {
     g_am_v = nullptr;
     g_am_i = nullptr;
     qh_persist_shutdown();
+    qm_persist_shutdown();
     (void)hipStreamDestroy(g_stream);
     g_stream = nullptr;
     g_inited = 0;

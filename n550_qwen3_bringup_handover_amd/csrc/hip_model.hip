@@ -23,6 +23,7 @@
 
 #include "hip_shim.h"
 #include "model_shim.h"
+#include "fp_pinned.h"
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(NTH) void k_rows_norm(float *__restrict__ x, const 
                 }
             }
             if (emb || r || ks > 0) reinterpret_cast<f32x4 *>(x + (size_t)row * K)[c] = v[j];
-            ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+            ss += sumsq4(v[j].x, v[j].y, v[j].z, v[j].w);
         }
     }
     __shared__ float red[NTH / WAVE];
@@ -196,11 +197,11 @@ __global__ __launch_bounds__(NTH) void k_qk_rope_cache(float *__restrict__ qkv, 
     const float x0 = src[lane], x1 = src[lane + 64];
     const float w0 = bf16f(w[lane]), w1 = bf16f(w[lane + 64]);
     const float c = rcos[(size_t)pos * (HD / 2) + lane], sn = rsin[(size_t)pos * (HD / 2) + lane];
-    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float ss = wave_sum(sumsq2(x0, x1));
     const float sc = 1.0f / sqrtf(ss / (float)HD + eps);
     const float y0 = (x0 * sc) * w0, y1 = (x1 * sc) * w1;
-    const float o0 = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
-    const float o1 = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
+    float o0, o1;
+    rope_pair(y0, y1, c, sn, o0, o1);
     if (isq) {
         src[lane] = o0;
         src[lane + 64] = o1;
@@ -344,8 +345,8 @@ __global__ __launch_bounds__(NTH) void k_attention(const float *__restrict__ qkv
 #pragma unroll
                 for (int r = 0; r < R; r++) {
                     const float pw = p[r * ldp + t + 4 * u];
-                    o[r].x = __fadd_rn(o[r].x, __fmul_rn(pw, v[u].x));
-                    o[r].y = __fadd_rn(o[r].y, __fmul_rn(pw, v[u].y));
+                    o[r].x = mul_add(pw, v[u].x, o[r].x);
+                    o[r].y = mul_add(pw, v[u].y, o[r].y);
                 }
         }
     };
@@ -470,11 +471,10 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
     // 3. QK-norm + RoPE: waves 0/1 the two query heads, wave 2 the new k
     if (wave < GRP + 1) {
         float *dst = wave < GRP ? sq + wave * HD : sk;
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float ss = wave_sum(sumsq2(x0, x1));
         const float sc_ = 1.0f / sqrtf(ss / (float)HD + eps);
         const float y0 = (x0 * sc_) * w0, y1 = (x1 * sc_) * w1;
-        dst[lane] = __fsub_rn(__fmul_rn(y0, c), __fmul_rn(y1, sn));
-        dst[lane + 64] = __fadd_rn(__fmul_rn(y1, c), __fmul_rn(y0, sn));
+        rope_pair(y0, y1, c, sn, dst[lane], dst[lane + 64]);
     }
     __syncthreads();
     if (sp == 0) {                               // one block per kv head writes the new entry
@@ -529,8 +529,8 @@ __global__ __launch_bounds__(NTH) void k_attn_part(const float *__restrict__ qkv
         const float e0 = valid ? expf(s0 - nm0) : 0.0f, e1 = valid ? expf(s1 - nm1) : 0.0f;
         const float r0 = m0 == -INFINITY ? 0.0f : expf(m0 - nm0);
         const float r1 = m1 == -INFINITY ? 0.0f : expf(m1 - nm1);
-        l0 = l0 * r0 + wave_sum(e0);
-        l1 = l1 * r1 + wave_sum(e1);
+        l0 = mul_add(l0, r0, wave_sum(e0));
+        l1 = mul_add(l1, r1, wave_sum(e1));
         m0 = nm0;
         m1 = nm1;
         if (wave == 0) { pe[0][lane] = e0; pe[1][lane] = e1; }

@@ -77,6 +77,9 @@ int qh_persist_out_ld(void);
 int qh_persist_errors(unsigned *flags);
 int qh_persist_init(void);
 void qh_persist_shutdown(void);
+/* the persistent decoder-stack launch's buffers (hip_model_persist.hip),
+ * allocated by the first model that uses it, freed at shutdown */
+void qm_persist_shutdown(void);
 /* name of the plan the last GEMM call launched */
 const char *qh_last_plan(void);
 /* h[M,N] = silu(X.Wg^T) * (X.Wu^T) */

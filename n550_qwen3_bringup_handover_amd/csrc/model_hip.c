@@ -55,6 +55,7 @@ struct qwen3_hip_model {
     int *state;                        /* [0] token, [1] position, [2] step */
     int *out_tok;                      /* [max_seq + 1] */
     int use_graph;
+    int use_persist;                   /* decode layers as one persistent launch */
     int graph_id;                      /* -1 until captured */
     qwen3_hip_dump_fn dump;            /* chunk-path intermediate dumps (NULL = off) */
     void *dump_ctx;
@@ -155,6 +156,14 @@ int qwen3_hip_model_open(qwen3_hip_model **out, const void *blob, size_t size, i
     m->max_seq = max_seq;
     m->use_graph = 1;
     m->graph_id = -1;
+    {
+        /* the persistent decode launch, opt-in: measured slower than the
+         * per-layer launches (1,720-1,750 against 1,780-1,805 tok/s).  Its buffers are
+         * shared by every model; failing to get them only leaves it off. */
+        const char *env = getenv("QWEN3_HIP_MODEL_PERSIST");
+        const int ok = qm_persist_init() == 0 && qm_persist_supported();
+        m->use_persist = ok && env && strcmp(env, "1") == 0;
+    }
 
 #define DEV(ptr, bytes)                                                   \
     do {                                                                  \
@@ -285,6 +294,27 @@ int qwen3_hip_model_set_graph(qwen3_hip_model *m, int on) {
     return QWEN3_HIP_OK;
 }
 
+int qwen3_hip_model_set_persistent(qwen3_hip_model *m, int on) {
+    if (!m) return QWEN3_HIP_EINVAL;
+    if (on && !qm_persist_supported()) return QWEN3_HIP_ENODEV;
+    if ((on ? 1 : 0) != m->use_persist && m->graph_id >= 0) {   /* the captured step is the other kind */
+        int rc = qh_sync();
+        if (!rc) rc = qh_graph_destroy(m->graph_id);
+        if (rc) return rc;
+        m->graph_id = -1;
+    }
+    m->use_persist = on ? 1 : 0;
+    return QWEN3_HIP_OK;
+}
+
+int qwen3_hip_model_persistent(const qwen3_hip_model *m) { return m ? m->use_persist : 0; }
+
+int qwen3_hip_model_persist_errors(qwen3_hip_model *m, unsigned *flags) {
+    if (!m || !flags) return QWEN3_HIP_EINVAL;
+    *flags = 0;
+    return qm_persist_supported() ? qm_persist_errors(flags) : QWEN3_HIP_OK;
+}
+
 /* ---- forward ----------------------------------------------------------------- */
 
 static size_t kv_layer_floats(const qwen3_hip_model *m) {
@@ -376,7 +406,18 @@ static int run_chunk(qwen3_hip_model *m, const kv_t *kv, int nt, int pos0, int w
 static int decode_step(qwen3_hip_model *m) {
     int rc = QWEN3_HIP_OK;
     const float eps = QW3M_RMS_EPS;
-    for (int l = 0; l < NL && !rc; l++) {
+    if (m->use_persist) {
+        /* the 28 layers in one launch: x0 and dn as the per-layer launches leave them */
+        const uint16_t *w[NL * 9];
+        for (int l = 0; l < NL; l++) {
+            const layer_t *L = &m->L[l];
+            const uint16_t *lw[9] = {L->in_norm, L->wqkv, L->qn, L->kn, L->wo, L->post_norm, L->wg, L->wu, L->wd};
+            memcpy(w + 9 * l, lw, sizeof lw);
+        }
+        rc = qm_decode_layers_persist(w, NL, m->embed, V, m->state, m->kc, m->vc, kv_layer_floats(m), m->rcos,
+                                      m->rsin, m->max_seq, eps, m->x0, m->dn);
+    }
+    for (int l = 0; l < NL && !rc && !m->use_persist; l++) {
         const layer_t *L = &m->L[l];
         qh_gemv_pro_t pro = {m->x0, NULL, NULL, 0, m->dn, L->in_norm, m->x1, eps};
         if (l == 0) { pro.x = NULL; pro.r = NULL; pro.emb = m->embed; pro.tok = m->state; pro.emb_rows = V; }

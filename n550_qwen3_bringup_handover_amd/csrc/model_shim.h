@@ -69,6 +69,23 @@ int qm_attention_decode_batch(const float *qkv_d, float *att_d, float *part_d, f
 int qm_argmax_rows(const float *logits_d, int n, int n_rows, int *tok_d, int *pos_d, const int *plen_d,
                    int *out_d, int out_ld);
 
+/* One decode token's 28 decoder layers as one persistent launch
+ * (hip_model_persist.hip), the same bits as the per-layer launches of
+ * model_hip.c decode_step: w holds 9 weight pointers per layer (input norm,
+ * q|k|v, q norm, k norm, o, post-attention norm, gate, up, down); the token
+ * and position come from state[0], state[1]; writes each layer's new K/V
+ * cache entry, the residual after the last layer's o add to x_out and the
+ * last down output to dn_out.  qm_persist_init allocates its buffers once
+ * (device current); qm_persist_supported says whether the device keeps the
+ * launch's 256 workgroups resident; qm_persist_errors returns (and clears)
+ * the error flags of launches that gave up waiting on an exchange. */
+int qm_persist_init(void);
+int qm_persist_supported(void);
+int qm_decode_layers_persist(const uint16_t *const *w, int layers, const uint16_t *embed, int vocab,
+                             const int *state, float *kc, float *vc, size_t kv_layer, const float *rcos,
+                             const float *rsin, int max_seq, float eps, float *x_out, float *dn_out);
+int qm_persist_errors(unsigned *flags);
+
 /* *p = v, as a kernel (safe inside stream capture) */
 int qm_set_i32(int *p_d, int v);
 /* p[0..n) = 0, as a kernel */

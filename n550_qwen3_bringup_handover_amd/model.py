@@ -118,6 +118,23 @@ class Model:
     def set_graph(self, on):
         _rc(runtime.lib().qwen3_hip_model_set_graph(self._h, 1 if on else 0), "qwen3_hip_model_set_graph")
 
+    def set_persistent(self, on):
+        """decode steps with the 28 layers as one persistent launch (True) or
+        five launches per layer (False); both give the same bits"""
+        _rc(runtime.lib().qwen3_hip_model_set_persistent(self._h, 1 if on else 0),
+            "qwen3_hip_model_set_persistent")
+
+    @property
+    def persistent(self):
+        return bool(runtime.lib().qwen3_hip_model_persistent(self._h))
+
+    def persist_errors(self):
+        """error flags of persistent decode launches since the last call
+        (nonzero: a launch gave up waiting on another workgroup)"""
+        f = ctypes.c_uint(0)
+        _rc(runtime.lib().qwen3_hip_model_persist_errors(self._h, ctypes.byref(f)), "qwen3_hip_model_persist_errors")
+        return f.value
+
     def generate(self, prompt, n_decode, stop_at_eos=False):
         p = _i32(prompt)
         out = np.zeros(n_decode + 1, dtype=np.int32)
@@ -214,6 +231,8 @@ def main(argv=None):
     ap.add_argument("--decode", type=int, default=128, help="greedy decode steps")
     ap.add_argument("--repeat", type=int, default=1)
     ap.add_argument("--eager", action="store_true", help="launch decode kernels one by one instead of a graph replay")
+    ap.add_argument("--persistent", action="store_true",
+                    help="decode with one persistent launch for the 28 layers instead of five launches per layer")
     ap.add_argument("--tile", action="store_true", help="tile-major blob")
     ap.add_argument("--batch", type=int, default=0,
                     help="decode this many sequences together (each with its own random prompt)")
@@ -225,12 +244,15 @@ def main(argv=None):
     with Model(blob, max_seq=args.prompt + args.decode) as m:
         del blob
         m.set_graph(not args.eager)
+        if args.persistent:
+            m.set_persistent(True)
         for r in range(args.repeat):
             toks = m.generate(prompt, args.decode)
             pre, dec = m.timing()
             rate = args.decode / dec * 1e3 if dec > 0 else float("nan")
             print(f"run {r}: prefill {args.prompt} tokens {pre:.3f} ms; {args.decode} decode steps "
-                  f"{dec:.3f} ms ({rate:.1f} tok/s); first tokens {toks[:8].tolist()}", flush=True)
+                  f"{dec:.3f} ms ({rate:.1f} tok/s, {'persistent' if m.persistent else 'per-layer'} launches); "
+                  f"first tokens {toks[:8].tolist()}", flush=True)
     return 0
 
 

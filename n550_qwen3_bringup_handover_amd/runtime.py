@@ -96,6 +96,9 @@ _PROTOS = {
     "qwen3_hip_model_generate": (ctypes.c_int, [VP, I32P, ctypes.c_int, ctypes.c_int, ctypes.c_int, I32P, I32P]),
     "qwen3_hip_model_timing": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
     "qwen3_hip_model_set_graph": (ctypes.c_int, [VP, ctypes.c_int]),
+    "qwen3_hip_model_set_persistent": (ctypes.c_int, [VP, ctypes.c_int]),
+    "qwen3_hip_model_persistent": (ctypes.c_int, [VP]),
+    "qwen3_hip_model_persist_errors": (ctypes.c_int, [VP, ctypes.POINTER(ctypes.c_uint)]),
     "qwen3_hip_model_set_dump": (ctypes.c_int, [VP, VP, VP]),
     "qwen3_hip_batch_open": (ctypes.c_int, [ctypes.POINTER(VP), VP, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_batch_close": (None, [VP]),
