@@ -158,11 +158,11 @@ int qwen3_hip_model_open(qwen3_hip_model **out, const void *blob, size_t size, i
     m->graph_id = -1;
     {
         /* the persistent decode launch, opt-in: measured slower than the
-         * per-layer launches (1,720-1,750 against 1,780-1,805 tok/s).  Its buffers are
-         * shared by every model; failing to get them only leaves it off. */
+         * per-layer launches (1,720-1,750 against 1,780-1,805 tok/s).  Its
+         * buffers, shared by every model, are allocated when first wanted;
+         * failing to get them only leaves it off. */
         const char *env = getenv("QWEN3_HIP_MODEL_PERSIST");
-        const int ok = qm_persist_init() == 0 && qm_persist_supported();
-        m->use_persist = ok && env && strcmp(env, "1") == 0;
+        m->use_persist = env && strcmp(env, "1") == 0 && qm_persist_init() == 0 && qm_persist_supported();
     }
 
 #define DEV(ptr, bytes)                                                   \
@@ -296,7 +296,11 @@ int qwen3_hip_model_set_graph(qwen3_hip_model *m, int on) {
 
 int qwen3_hip_model_set_persistent(qwen3_hip_model *m, int on) {
     if (!m) return QWEN3_HIP_EINVAL;
-    if (on && !qm_persist_supported()) return QWEN3_HIP_ENODEV;
+    if (on) {
+        const int rc = qm_persist_init();   /* once: the launch's buffers and the residency check */
+        if (rc) return rc;
+        if (!qm_persist_supported()) return QWEN3_HIP_ENODEV;
+    }
     if ((on ? 1 : 0) != m->use_persist && m->graph_id >= 0) {   /* the captured step is the other kind */
         int rc = qh_sync();
         if (!rc) rc = qh_graph_destroy(m->graph_id);
