@@ -479,6 +479,14 @@ def persistent_step(g, layers, emb, act):
     return launch
 
 
+def use_persistent(pers, per_call_flag):
+    """whether the headline is the persistent step: it was measured (the
+    device keeps its grid resident), no launch gave up waiting on its
+    exchange (whose outputs would then be invalid), and --per-call was not
+    given"""
+    return bool(pers) and not per_call_flag and pers.get("exchange_errors", 1) == 0
+
+
 def persistent_class(g, launch_step):
     """the persistent launch alone: its duration (HIP events around each
     launch on the library stream; a launch takes ~0.2 ms, so the events'
@@ -784,7 +792,7 @@ def main():
         flags = ctypes.c_uint(0)
         g.rt.check(g.L.qwen3_hip_decode_set_errors(ctypes.byref(flags)), "decode_set_errors")
         pers["exchange_errors"] = flags.value
-    persistent = bool(pers and not args.per_call and pers["exchange_errors"] == 0)
+    persistent = use_persistent(pers, args.per_call)
     ms_step, wall = (pers if persistent else per_call)["ms_per_step"], (pers if persistent else per_call)["wall_s"]
     value = 1000.0 / ms_step
     kclasses = None if args.no_extras else kernel_classes(g, layers, emb, act)

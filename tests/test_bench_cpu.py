@@ -1,6 +1,7 @@
 """bench.py's contract on the CPU: the one-GPU refusal, the algorithmic byte
-and flop counts behind `roofline.achieved`, and the CPU-baseline leg (the
-reference's compiled scalar GEMM, timed on a tiny budget)."""
+and flop counts behind `roofline.achieved`, the choice of the headline step
+and the CPU-baseline leg (the reference's compiled scalar GEMM, timed on a
+tiny budget)."""
 import json
 import os
 import subprocess
@@ -52,3 +53,14 @@ def test_cpu_baseline_leg():
     assert out["cores"] == 1
     assert out["kind"] in ("reference", "port")
     assert out["unit"] == "tok/s"
+
+
+@pytest.mark.parametrize("pers,per_call,want", [
+    ({"ms_per_step": 0.33, "exchange_errors": 0}, False, True),
+    ({"ms_per_step": 0.33, "exchange_errors": 0}, True, False),     # --per-call
+    ({"ms_per_step": 0.33, "exchange_errors": 1}, False, False),    # a launch gave up: outputs invalid
+    ({"ms_per_step": 0.33}, False, False),                          # no error count: not trusted
+    (None, False, False),                                           # grid not resident: not measured
+])
+def test_headline_step_choice(pers, per_call, want):
+    assert bench.use_persistent(pers, per_call) is want
