@@ -33,6 +33,7 @@
 // the next stage's weights in registers while they wait (paced loads).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "hip_shim.h"
 #include "persist_common.h"
@@ -722,6 +723,7 @@ extern "C" int qm_decode_layers_persist(const uint16_t *const *w, int layers, co
     if (layers > MP_MAX_LAYERS) return QH_ETOOBIG;
     if (!g_mx || !g_mp_ok) return QH_ENODEV;
     ModelPersistArgs a;
+    memset(&a, 0, sizeof a);          // no stray stack bytes in the kernel arguments' padding
     for (int l = 0; l < MP_MAX_LAYERS; l++)
         for (int k = 0; k < LW_N; k++) {
             a.w[l][k] = l < layers ? w[LW_N * l + k] : nullptr;

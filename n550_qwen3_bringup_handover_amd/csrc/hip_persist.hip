@@ -59,6 +59,7 @@
 // the error flag set.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <string.h>
 
 #include "hip_shim.h"
 #include "persist_common.h"
@@ -307,6 +308,7 @@ extern "C" int qh_decode_persist(const uint16_t *const *w, const float *x0_d, fl
     if (layers > PS_MAX_LAYERS) return QH_ETOOBIG;
     if (!g_xch || !g_ps_ok) return QH_ENODEV;
     PersistArgs a;
+    memset(&a, 0, sizeof a);          // no stray stack bytes in the kernel arguments' padding
     for (int l = 0; l < PS_MAX_LAYERS; l++)
         for (int k = 0; k < 5; k++) {
             a.w[l][k] = l < layers ? w[5 * l + k] : nullptr;

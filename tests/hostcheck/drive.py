@@ -72,6 +72,16 @@ def run_model():
         prompt = rng.integers(0, M.VOCAB, 150).astype(np.int32)
         toks = m.generate(prompt, 8)
         say(f"generate: {len(toks)} tokens")
+        # the opt-in persistent decode launch: its graph replaces the
+        # per-layer one, and back (each switch destroys the captured step)
+        m.set_persistent(True)
+        m.generate(prompt, 8)
+        m.set_graph(False)
+        m.generate(prompt[:40], 3)
+        m.set_graph(True)
+        m.set_persistent(False)
+        m.generate(prompt, 4)
+        say("generate: persistent and back")
         m.forward(prompt[:64], 0)
         m.logits()
         for n_seq in (3, 20, 64):
