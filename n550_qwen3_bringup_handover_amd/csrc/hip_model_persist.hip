@@ -202,7 +202,7 @@ __device__ __forceinline__ AttnRange attn_range(int b, int pos) {
     a.sp = b / MP_NKV;
     a.pos = pos;
     const int ctx = pos + 1;
-    const int chunk = (ctx + MP_S - 1) / MP_S;
+    const int chunk = ((ctx + MP_S - 1) / MP_S + 7) & ~7;   // k_attn_part's ranges
     a.t0 = min(ctx, a.sp * chunk);
     const int t1 = min(ctx, a.t0 + chunk);
     a.n = t1 - a.t0;
