@@ -12,7 +12,7 @@ Three checks, all against oracle outputs on the same inputs:
    1/K of the magnitude sum, far above the bound.
 2. the same against the reference's portable scalar GEMM (kernels_scalar.c),
    which itself rounds K times: bound (K + K/16 + 16) * 2^-24.
-3. the north-star strict per-element relative error of 1e-3 against the
+3. the required strict per-element relative error of 1e-3 against the
    scalar reference, on every element whose |ref| >= 1e-3 * sum|ab|; the
    others (near-total cancellation) are counted and reported, and covered by
    checks 1 and 2.
@@ -22,7 +22,7 @@ import numpy as np
 import oracle
 
 U = 2.0 ** -24
-REL_TOL = 1e-3          # per-element relative error bound from the north star
+REL_TOL = 1e-3          # the required per-element relative error bound
 NEAR_ZERO = 1e-3        # |ref| < NEAR_ZERO * sum|ab| is excluded from the strict check
 
 
