@@ -739,7 +739,7 @@ def main():
                     help="headline on the per-call GEMV kernels instead of the persistent decode-set "
                          "launch (both are measured either way)")
     ap.add_argument("--calibrate-copy", action="store_true",
-                    help="also run a 512 MiB copy kernel (traffic-counter calibration)")
+                    help="also run a 512 MiB copy and a 512 MiB read-only stream (traffic-counter calibration)")
     ap.add_argument("--no-model", action="store_true", help="skip the full-forward and batched-decode measurements")
     ap.add_argument("--gemm-shape", default=None, metavar="M,K,N,GATED",
                     help="only time one GEMM shape on its automatic plan (--steps launches, "
@@ -830,14 +830,17 @@ def main():
                               "frac = frac_graph_replay = bytes_per_launch / graph-replay launch period / peak"}
     gemms = None if (args.no_extras or args.no_gemm_tables) else gemm_tables(g)
     if args.calibrate_copy:
-        # a kernel of known traffic (512 MiB read + 512 MiB written per
-        # launch, twice the 256 MB last-level cache, so every byte goes to
-        # and from HBM) for scaling FETCH_SIZE / WRITE_SIZE counters in
-        # profiled runs
+        # kernels of known traffic for scaling FETCH_SIZE / WRITE_SIZE counters
+        # in profiled runs, each over 512 MiB (twice the 256 MB last-level
+        # cache, so every byte goes to or from HBM): a copy (512 MiB read +
+        # 512 MiB written per launch) and a read-only stream in the decode
+        # GEMVs' load form (512 MiB read)
         nb = 512 << 20
         src, dst = g.alloc(nb), g.alloc(nb)
         for _ in range(5):
             g.rt.check(g.L.qwen3_hip_copy_dev(ctypes.c_void_p(dst), ctypes.c_void_p(src), nb), "copy")
+        for _ in range(5):
+            g.rt.check(g.L.qwen3_hip_read_dev(ctypes.c_void_p(src), nb), "read")
         g.sync()
 
     model = batch = None

@@ -187,6 +187,10 @@ int qwen3_hip_tile_to_row_dev(uint16_t *dst_d, const uint16_t *src_d,
  * 16-byte aligned pointers); its traffic is exactly bytes read + bytes
  * written, which makes it the reference for HBM traffic counters */
 int qwen3_hip_copy_dev(void *dst_d, const void *src_d, size_t bytes);
+/* reads bytes (a multiple of 16, below 2 GiB, 16-byte aligned pointer) once
+ * with the decode GEMVs' load form and writes nothing: the reference for
+ * read-traffic counters (no counterpart in the reference; for measurement) */
+int qwen3_hip_read_dev(const void *src_d, size_t bytes);
 
 /* HIP graphs: device-pointer calls made between capture_begin and
  * capture_end are recorded, not run; graph_launch replays them on the

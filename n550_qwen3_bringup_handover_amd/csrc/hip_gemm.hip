@@ -1623,6 +1623,18 @@ extern "C" int qh_copy(void *dst, const void *src, size_t bytes) {
     return QH_OK;
 }
 
+extern "C" int qh_read(const void *src, size_t bytes) {
+    if (!g_inited) return QH_ESTATE;
+    if (!src || (bytes & 15u) || !aligned16(src) || bytes >= ((size_t)1 << 31)) return QH_EINVAL;
+    if (bytes == 0) return QH_OK;
+    const size_t n16 = bytes / 16;
+    const size_t want = (n16 + NTHREADS - 1) / NTHREADS;
+    const int grid = (int)(want < 4096 ? want : 4096);
+    hipLaunchKernelGGL(k_read16, dim3(grid), dim3(NTHREADS), 0, g_stream, (const u32x4 *)src, n16);
+    HCHECK(hipGetLastError(), QH_ELAUNCH);
+    return QH_OK;
+}
+
 extern "C" int qh_argmax(int *out, const float *v, int n) {
     if (!g_inited) return QH_ESTATE;
     if (n <= 0 || !out || !v) return QH_EINVAL;

@@ -140,6 +140,10 @@ int qh_gemv_ka(float *c, const uint16_t *row_bf16, const uint16_t *b_d, const ui
 /* device copy by a plain 16-byte-vector kernel (bytes % 16 == 0, 16-byte
  * aligned pointers): the known-traffic reference for HBM counter calibration */
 int qh_copy(void *dst_d, const void *src_d, size_t bytes);
+/* reads bytes (% 16 == 0, < 2 GiB, 16-byte aligned) once with the decode
+ * GEMVs' buffer-load form and writes nothing: the known-traffic reference for
+ * read counters */
+int qh_read(const void *src_d, size_t bytes);
 
 /* stream capture: launches between begin and end are recorded (not run)
  * into a graph that qh_graph_launch replays on the shim stream */

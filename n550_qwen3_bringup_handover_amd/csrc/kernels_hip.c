@@ -610,6 +610,11 @@ int qwen3_hip_copy_dev(void *dst, const void *src, size_t bytes) {
     return note(qh_copy(dst, src, bytes));
 }
 
+int qwen3_hip_read_dev(const void *src, size_t bytes) {
+    READY_OR_RETURN();
+    return note(qh_read(src, bytes));
+}
+
 int qwen3_hip_capture_begin(void) { READY_OR_RETURN(); return note(qh_capture_begin()); }
 int qwen3_hip_capture_end(int *graph_id) { READY_OR_RETURN(); return note(qh_capture_end(graph_id)); }
 int qwen3_hip_graph_launch(int graph_id) { READY_OR_RETURN(); return note(qh_graph_launch(graph_id)); }

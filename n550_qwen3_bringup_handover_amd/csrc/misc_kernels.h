@@ -80,6 +80,27 @@ __global__ __launch_bounds__(NTHREADS) void k_copy16(u32x4 *__restrict__ dst,
         dst[i] = __builtin_nontemporal_load(src + i);
 }
 
+// Reads n16 16-byte chunks once and writes nothing: the decode GEMVs' load
+// form (buffer loads, non-temporal, a wave covering 1 KB per instruction),
+// four loads in flight per lane per step.  The reference for read-traffic
+// counters: its traffic is exactly the bytes read.  n16 * 16 < 2^31.
+__global__ __launch_bounds__(NTHREADS) void k_read16(const u32x4 *__restrict__ src, size_t n16) {
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(src, n16 * 16);
+    const uint32_t stride = gridDim.x * NTHREADS;
+    u32x4 acc = {0u, 0u, 0u, 0u};
+    for (uint32_t i = blockIdx.x * NTHREADS + threadIdx.x; i < n16; i += 4 * stride) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t q = i + u * stride;
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, q < n16 ? q * 16u : BUF_OOB, 0, 2);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u];
+    }
+    asm volatile("" ::"v"(acc.x), "v"(acc.y), "v"(acc.z), "v"(acc.w));
+}
+
 // dst[i] = bf16 RNE of src[i]; 8 elements per lane per step (n % 8 == 0,
 // 16-byte aligned src and dst)
 __global__ __launch_bounds__(NTHREADS) void k_cvt_bf16(uint16_t *__restrict__ dst,

@@ -68,6 +68,7 @@ _PROTOS = {
     "qwen3_hip_argmax_dev": (ctypes.c_int, [VP, VP, ctypes.c_int]),
     "qwen3_hip_tile_to_row_dev": (ctypes.c_int, [VP, VP, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "qwen3_hip_copy_dev": (ctypes.c_int, [VP, VP, ctypes.c_size_t]),
+    "qwen3_hip_read_dev": (ctypes.c_int, [VP, ctypes.c_size_t]),
     "qwen3_hip_capture_begin": (ctypes.c_int, []),
     "qwen3_hip_capture_end": (ctypes.c_int, [I32P]),
     "qwen3_hip_graph_launch": (ctypes.c_int, [ctypes.c_int]),

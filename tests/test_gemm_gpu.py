@@ -692,6 +692,29 @@ def test_argmax_dev(n):
         assert got == oracle.argmax(t)
 
 
+def test_copy_and_read_streams():
+    """the known-traffic kernels behind the counter calibration: the copy
+    moves every byte, the read-only stream reads and leaves memory as it was;
+    both refuse sizes that are not whole 16-byte chunks or pointers that are
+    not 16-byte aligned"""
+    L = runtime.lib()
+    n = (3 << 20) + 48                     # not a multiple of the grid's stride
+    src = np.random.default_rng(3).integers(0, 2 ** 32, n // 4, dtype=np.uint32)
+    sd, dd = abi.DeviceBuffer.from_array(src), abi.DeviceBuffer(n)
+    dd.upload(np.zeros(n // 4, np.uint32))
+    assert L.qwen3_hip_copy_dev(ctypes.c_void_p(dd.ptr), ctypes.c_void_p(sd.ptr), n) == 0
+    assert np.array_equal(dd.download(np.uint32, n // 4), src)
+    assert L.qwen3_hip_read_dev(ctypes.c_void_p(sd.ptr), n) == 0
+    assert L.qwen3_hip_read_dev(ctypes.c_void_p(sd.ptr), 0) == 0
+    assert np.array_equal(sd.download(np.uint32, n // 4), src)
+    EINVAL = 1                             # QWEN3_HIP_EINVAL (include/qwen3_hip.h)
+    assert L.qwen3_hip_read_dev(ctypes.c_void_p(sd.ptr), n - 8) == EINVAL
+    assert L.qwen3_hip_read_dev(ctypes.c_void_p(sd.ptr + 8), 16) == EINVAL
+    assert L.qwen3_hip_read_dev(ctypes.c_void_p(sd.ptr), 1 << 31) == EINVAL
+    assert L.qwen3_hip_copy_dev(ctypes.c_void_p(dd.ptr), ctypes.c_void_p(sd.ptr), n - 8) == EINVAL
+    assert L.qwen3_hip_last_error() == EINVAL  # the refusals were recorded; reading clears it
+
+
 @pytest.mark.parametrize("K,N,gated", [(1024, 2048, False), (1024, 1024, False), (1024, 3072, True), (1024, V, False),
                                        (1000, 300, False), (512, 777, True), (8, 64, False), (1032, 100, False),
                                        (2048, 1024, False), (3072, 1024, False),
