@@ -64,3 +64,20 @@ def test_cpu_baseline_leg():
 ])
 def test_headline_step_choice(pers, per_call, want):
     assert bench.use_persistent(pers, per_call) is want
+
+
+def test_committed_profiles_match_kernel_sources():
+    """every rocprofv3 summary under profiles/ was made from the kernel
+    sources in the tree: its '# sources:' digest is the one bench.py
+    computes, so the roofline figures it quotes describe these kernels"""
+    pdir = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "profiles")
+    want = bench.kernel_sources_digest()
+    stale = {}
+    for name in sorted(os.listdir(pdir)):
+        if not name.endswith(".txt"):
+            continue
+        digests = [ln.split(":", 1)[1].split()[0] for ln in open(os.path.join(pdir, name))
+                   if ln.startswith("# sources:")]
+        if digests != [want]:
+            stale[name] = digests
+    assert not stale, stale
